@@ -1,0 +1,104 @@
+// capi.cpp - extern "C" entry points of libfns_hip.so (include/fns_hip.h): thin forwards to fns::impl.
+#include "fns_hip.h"
+
+#include "fns_host.hpp"
+#include "fns_internal.hpp"
+
+using namespace fns;
+
+static inline hipStream_t S(void *s) { return (hipStream_t) s; }
+
+extern "C" {
+
+int fns_hip_abi_version(void) { return 1; }
+const char *fns_hip_last_error(void) { return host::last_error(); }
+
+size_t fns_hip_q8_1_row_bytes(int64_t ncols) { return (size_t) host::q8_1_row_bytes(ncols); }
+
+int fns_hip_quantize_q8_1(const float *x, void *xq, int64_t ncols, int64_t nrows, void *stream) {
+    return impl::quantize_q8_1(x, xq, ncols, nrows, S(stream));
+}
+
+int fns_hip_mmvq(int type, const void *w, int64_t ncols, int64_t nrows, const void *xq, float *dst, int64_t n_cols,
+                 void *stream) {
+    return impl::mmvq(type, w, ncols, nrows, xq, dst, n_cols, S(stream));
+}
+
+int fns_hip_mmvq_ids(int type, const void *w, int64_t ncols, int64_t nrows, int64_t n_mats, const void *xq,
+                     int64_t n_xq, const int32_t *ids, int64_t n_ids, float *dst, void *stream) {
+    return impl::mmvq_ids(type, w, ncols, nrows, n_mats, xq, n_xq, ids, n_ids, dst, S(stream));
+}
+
+int fns_hip_mmvq_swiglu(int type, const void *w_gate, const void *w_up, int64_t ncols, int64_t nrows, const void *xq,
+                        float *dst, void *stream) {
+    return impl::mmvq_swiglu(type, w_gate, w_up, ncols, nrows, xq, dst, S(stream));
+}
+
+int fns_hip_mmvq_ids_swiglu_shared(int type, const void *w_gate, const void *w_up, int64_t ncols, int64_t nrows,
+                                   int64_t n_mats, const void *xq, const int32_t *ids, int64_t n_ids, float *dst,
+                                   const void *sh_gate, const void *sh_up, float *sh_dst, void *stream) {
+    return impl::mmvq_ids_swiglu_shared(type, w_gate, w_up, ncols, nrows, n_mats, xq, ids, n_ids, dst, sh_gate, sh_up,
+                                        sh_dst, S(stream));
+}
+
+int fns_hip_mmvq_experts_swiglu(int type, const void *const *table, size_t gate_off, size_t up_off, int64_t ncols,
+                                int64_t nrows, const void *xq, int64_t n_xq, const int32_t *ids, int64_t n_ids,
+                                float *dst, void *stream) {
+    return impl::mmvq_experts_swiglu(type, (const char *const *) table, gate_off, up_off, ncols, nrows, xq, n_xq, ids,
+                                     n_ids, dst, S(stream));
+}
+
+int fns_hip_mmvq_experts(int type, const void *const *table, size_t off, int64_t ncols, int64_t nrows, const void *xq,
+                         int64_t n_xq, const int32_t *ids, int64_t n_ids, float *dst, void *stream) {
+    return impl::mmvq_experts(type, (const char *const *) table, off, ncols, nrows, xq, n_xq, ids, n_ids, dst,
+                              S(stream));
+}
+
+int fns_hip_mmvq_supports(int type) { return host::is_kquant(type) ? 1 : 0; }
+
+int fns_hip_rms_norm_q8_1(const float *x, const float *w, float *out, void *xq, int n, float eps, int rows,
+                          void *stream) {
+    return impl::rms_norm_q8_1(x, w, out, xq, n, eps, rows, S(stream));
+}
+
+int fns_hip_gemv_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int cols,
+                        void *stream) {
+    return impl::gemv_router(dtype, w, x, y, ncols, nrows, cols, S(stream));
+}
+
+int fns_hip_gemm_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int n_tok,
+                        void *stream) {
+    return impl::gemm_router(dtype, w, x, y, ncols, nrows, n_tok, S(stream));
+}
+
+int fns_hip_route_topk(const float *logits, int32_t *ids, float *w, int n_expert, int k, int n_tok, int gating,
+                       int norm, void *stream) {
+    return impl::route_topk(logits, ids, w, n_expert, k, n_tok, gating, norm, S(stream));
+}
+
+int fns_hip_count_routes(const int32_t *ids, uint32_t *counts, int k, void *stream) {
+    return impl::count_routes(ids, counts, k, S(stream));
+}
+
+int fns_hip_swiglu(const float *g, const float *u, float *act, int n, int rows, void *stream) {
+    return impl::swiglu(g, u, act, n, rows, S(stream));
+}
+
+int fns_hip_glu_mmvq(const float *g, const float *u, float *act, int n, void *stream) {
+    return impl::glu_mmvq(g, u, act, n, S(stream));
+}
+
+int fns_hip_amax_guard(float *act, float *escale, int n, int rows, void *stream) {
+    return impl::amax_guard(act, escale, n, rows, S(stream));
+}
+
+int fns_hip_amax_guard_q8_1(const float *act, float *escale, void *xq, int n, int rows, void *stream) {
+    return impl::amax_guard_q8_1(act, escale, xq, n, rows, S(stream));
+}
+
+int fns_hip_moe_combine(const float *dexp, const float *escale, const float *w, const float *sh, const float *x_in,
+                        float *out, int n, int k, int n_tok, void *stream) {
+    return impl::moe_combine(dexp, escale, w, sh, x_in, out, n, k, n_tok, S(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,46 @@
+// fns_host.hpp - host-side helpers shared by the HIP translation units: error reporting for the C ABI, the abort
+// behaviour of the C++ API (the reference aborts on launch failures and unsupported types: src/kernels.cu:9-16,
+// src/ggml/ggml_cuda_host.cu:14-17), and small shape utilities.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+namespace fns::host {
+
+// Error codes of the C ABI (include/fns_hip.h).
+enum Status : int {
+    OK = 0,
+    ERR_TYPE = -1,    // unsupported ggml type
+    ERR_SHAPE = -2,   // shape / argument precondition violated
+    ERR_LAUNCH = -3,  // HIP launch or runtime error
+    ERR_NOMEM = -4,   // a caller-provided buffer is too small
+};
+
+// Records a message for fns_hip_last_error() (thread-local) and returns `code`.
+int set_error(int code, const char *fmt, ...);
+const char *last_error();
+
+// After a launch: converts a pending HIP error into ERR_LAUNCH.
+int check_launch(const char *what);
+
+// C++ API behaviour: print the last error and abort when `rc` is not OK.
+void abort_on_error(int rc, const char *what);
+
+inline int64_t pad512(int64_t n) { return (n + 511) / 512 * 512; }
+inline bool is_kquant(int t) { return t == 11 || t == 12 || t == 13 || t == 14; }
+inline int64_t kquant_block_bytes(int t) {
+    return t == 11 ? 110 : t == 12 ? 144 : t == 13 ? 176 : t == 14 ? 210 : 0;
+}
+inline int64_t q8_1_row_bytes(int64_t ncols) { return pad512(ncols) / 32 * 36; }
+
+}  // namespace fns::host
+
+#define FNS_TRY(...)                       \
+    do {                                   \
+        const int rc_ = (__VA_ARGS__);     \
+        if (rc_ != ::fns::host::OK) return rc_; \
+    } while (0)

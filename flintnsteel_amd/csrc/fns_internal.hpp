@@ -1,0 +1,45 @@
+// fns_internal.hpp - status-returning implementations behind the C ABI (include/fns_hip.h) and the C++ API
+// (include/fns/ggml_kernels.h, include/fns/kernels.h). Every function validates its arguments, launches on `st`
+// and returns fns::host::Status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "fns_hip.h"
+
+namespace fns::impl {
+
+int quantize_q8_1(const float *x, void *xq, int64_t ncols, int64_t nrows, hipStream_t st);
+int rms_norm_q8_1(const float *x, const float *w, float *out, void *xq, int n, float eps, int rows, hipStream_t st);
+int amax_guard(float *act, float *escale, int n, int rows, hipStream_t st);
+int amax_guard_q8_1(const float *act, float *escale, void *xq, int n, int rows, hipStream_t st);
+int swiglu(const float *g, const float *u, float *act, int n, int rows, hipStream_t st);
+int glu_mmvq(const float *g, const float *u, float *act, int n, hipStream_t st);
+
+int mmvq(int type, const void *w, int64_t ncols, int64_t nrows, const void *xq, float *dst, int64_t n_cols,
+         hipStream_t st);
+int mmvq_ids(int type, const void *w, int64_t ncols, int64_t nrows, int64_t n_mats, const void *xq, int64_t n_xq,
+             const int32_t *ids, int64_t n_ids, float *dst, hipStream_t st);
+int mmvq_swiglu(int type, const void *w_gate, const void *w_up, int64_t ncols, int64_t nrows, const void *xq,
+                float *dst, hipStream_t st);
+int mmvq_ids_swiglu_shared(int type, const void *w_gate, const void *w_up, int64_t ncols, int64_t nrows,
+                           int64_t n_mats, const void *xq, const int32_t *ids, int64_t n_ids, float *dst,
+                           const void *sh_gate, const void *sh_up, float *sh_dst, hipStream_t st);
+int mmvq_experts_swiglu(int type, const char *const *table, size_t gate_off, size_t up_off, int64_t ncols,
+                        int64_t nrows, const void *xq, int64_t n_xq, const int32_t *ids, int64_t n_ids, float *dst,
+                        hipStream_t st);
+int mmvq_experts(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, const void *xq,
+                 int64_t n_xq, const int32_t *ids, int64_t n_ids, float *dst, hipStream_t st);
+
+int gemv_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int cols, hipStream_t st);
+int gemm_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int n_tok, hipStream_t st);
+int route_topk(const float *logits, int32_t *ids, float *w, int n_expert, int k, int n_tok, int gating, int norm,
+               hipStream_t st);
+int moe_combine(const float *dexp, const float *escale, const float *w, const float *sh, const float *x_in, float *out,
+                int n, int k, int n_tok, hipStream_t st);
+int count_routes(const int32_t *ids, uint32_t *counts, int k, hipStream_t st);
+
+}  // namespace fns::impl

@@ -1,0 +1,254 @@
+// router.hip - router logits (fp32 / bf16 GEMV and batch GEMM), gating + top-k + renormalisation, weighted combine
+// and the routing histogram, for MI355X gfx950.
+//
+// Reference: src/kernels.cu:452-514 (gemv_bf16, route_topk), :579-586 (moe_combine), :955-962 (count_routes);
+// src/prefill_kernels.cu:133-183,217-242 (batch router, route_topk_batch, moe_combine_batch). Gating is
+// generalised to softmax (the configs, llama.cpp build_moe_ffn) or sigmoid (the Flint model), any expert count up to
+// 256 and k up to 16; the reference hard-codes sigmoid, 256 experts and k <= 8.
+#include "fns/kernels.h"
+#include "fns_common.hpp"
+#include "fns_host.hpp"
+#include "fns_internal.hpp"
+#include "fns_route.hpp"
+
+namespace fns {
+
+using namespace fns::dev;
+
+namespace {
+
+__device__ __forceinline__ float bf16_to_float(uint16_t b) { return __builtin_bit_cast(float, (uint32_t) b << 16); }
+
+// One workgroup (256 lanes) per output row r; COLS input columns share the row read.
+template <int COLS, bool BF16>
+__global__ __launch_bounds__(256) void k_gemv_router(const void *__restrict__ w, const float *__restrict__ x,
+                                                     float *__restrict__ y, int ncols, int nrows) {
+    __shared__ float red[4][COLS];
+    const int r = blockIdx.x;
+    float s[COLS];
+#pragma unroll
+    for (int c = 0; c < COLS; ++c) s[c] = 0.0f;
+    if (ncols % 4 == 0) {
+        for (int i = threadIdx.x; i < ncols / 4; i += 256) {
+            float4 wv;
+            if constexpr (BF16) {
+                const uint2 pk = ((const uint2 *) ((const uint16_t *) w + (size_t) r * ncols))[i];
+                wv = make_float4(bf16_to_float(pk.x & 0xffff), bf16_to_float(pk.x >> 16), bf16_to_float(pk.y & 0xffff),
+                                 bf16_to_float(pk.y >> 16));
+            } else {
+                wv = ((const float4 *) ((const float *) w + (size_t) r * ncols))[i];
+            }
+#pragma unroll
+            for (int c = 0; c < COLS; ++c) {
+                const float4 xv = ((const float4 *) (x + (size_t) c * ncols))[i];
+                s[c] += wv.x * xv.x + wv.y * xv.y + wv.z * xv.z + wv.w * xv.w;
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < ncols; i += 256) {
+            const float wv = BF16 ? bf16_to_float(((const uint16_t *) w)[(size_t) r * ncols + i])
+                                  : ((const float *) w)[(size_t) r * ncols + i];
+#pragma unroll
+            for (int c = 0; c < COLS; ++c) s[c] += wv * x[(size_t) c * ncols + i];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < COLS; ++c) {
+        float v = s[c];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+        if (threadIdx.x % 64 == 0) red[threadIdx.x / 64][c] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < COLS)
+        y[(size_t) threadIdx.x * nrows + r] =
+            (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
+}
+
+// Batch router GEMM y[t][e] = sum_i W[e][i] x[t][i]: 64 x 64 output tile per workgroup, k-chunks of 16 staged in LDS,
+// 4 x 4 outputs per lane. BF16: W is bf16 and x is rounded to bf16 first (the reference's cuBLAS BF16 path).
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_gemm_router(const void *__restrict__ w, const float *__restrict__ x,
+                                                     float *__restrict__ y, int ncols, int nrows, int n_tok) {
+    __shared__ float xs[16][68], ws[16][68];
+    const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < ncols; k0 += 16) {
+        for (int i = threadIdx.x; i < 64 * 16; i += 256) {
+            const int rr = i / 16, kk = i % 16;
+            const int t = t0 + rr, e = e0 + rr, k = k0 + kk;
+            float xv = (t < n_tok && k < ncols) ? x[(size_t) t * ncols + k] : 0.0f;
+            float wv = 0.0f;
+            if (e < nrows && k < ncols) {
+                if constexpr (BF16) wv = bf16_to_float(((const uint16_t *) w)[(size_t) e * ncols + k]);
+                else wv = ((const float *) w)[(size_t) e * ncols + k];
+            }
+            if constexpr (BF16) {  // round x to bf16, nearest even
+                uint32_t b = __builtin_bit_cast(uint32_t, xv);
+                b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+                xv = __builtin_bit_cast(float, b);
+            }
+            xs[kk][rr] = xv;
+            ws[kk][rr] = wv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = xs[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = ws[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = t0 + ty * 4 + i, e = e0 + tx * 4 + j;
+            if (t < n_tok && e < nrows) y[(size_t) t * nrows + e] = acc[i][j];
+        }
+}
+
+}  // namespace
+
+namespace {
+
+__global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ logits, int32_t *__restrict__ ids,
+                                                   float *__restrict__ w, int n_expert, int k, int gating, int norm) {
+    const int t = blockIdx.x;
+    route_topk_wave(logits + (size_t) t * n_expert, n_expert, k, gating, norm, ids + (size_t) t * k,
+                    w + (size_t) t * k, nullptr);
+}
+
+__global__ void k_moe_combine(const float *__restrict__ dexp, const float *__restrict__ escale,
+                              const float *__restrict__ w, const float *__restrict__ sh, const float *x_in, float *out,
+                              int n, int k) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float *d = dexp + (size_t) t * k * n;
+    const float *e = escale ? escale + (size_t) t * k : nullptr;
+    const float *ww = w + (size_t) t * k;
+    float moe = (d[i] * (e ? e[0] : 1.0f)) * ww[0];
+    for (int j = 1; j < k; ++j) moe = moe + (d[(size_t) j * n + i] * (e ? e[j] : 1.0f)) * ww[j];
+    const float s = sh ? sh[(size_t) t * n + i] : 0.0f;
+    out[(size_t) t * n + i] = (moe + s) + (x_in ? x_in[(size_t) t * n + i] : 0.0f);
+}
+
+__global__ void k_count_routes(const int32_t *ids, uint32_t *counts, int k) {
+    if ((int) threadIdx.x < k) atomicAdd(&counts[ids[threadIdx.x]], 1u);
+}
+
+template <bool BF16> int launch_gemv(const void *w, const float *x, float *y, int ncols, int nrows, int cols,
+                                     hipStream_t st) {
+    const dim3 g((unsigned) nrows);
+    switch (cols) {
+        case 1: hipLaunchKernelGGL((k_gemv_router<1, BF16>), g, dim3(256), 0, st, w, x, y, ncols, nrows); break;
+        case 2: hipLaunchKernelGGL((k_gemv_router<2, BF16>), g, dim3(256), 0, st, w, x, y, ncols, nrows); break;
+        case 3: hipLaunchKernelGGL((k_gemv_router<3, BF16>), g, dim3(256), 0, st, w, x, y, ncols, nrows); break;
+        case 4: hipLaunchKernelGGL((k_gemv_router<4, BF16>), g, dim3(256), 0, st, w, x, y, ncols, nrows); break;
+        case 5: hipLaunchKernelGGL((k_gemv_router<5, BF16>), g, dim3(256), 0, st, w, x, y, ncols, nrows); break;
+        case 6: hipLaunchKernelGGL((k_gemv_router<6, BF16>), g, dim3(256), 0, st, w, x, y, ncols, nrows); break;
+        case 7: hipLaunchKernelGGL((k_gemv_router<7, BF16>), g, dim3(256), 0, st, w, x, y, ncols, nrows); break;
+        default: hipLaunchKernelGGL((k_gemv_router<8, BF16>), g, dim3(256), 0, st, w, x, y, ncols, nrows); break;
+    }
+    return host::check_launch("gemv_router");
+}
+
+}  // namespace
+
+namespace impl {
+
+int gemv_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int cols, hipStream_t st) {
+    if (cols < 1 || cols > 8) return host::set_error(host::ERR_SHAPE, "gemv: expected 1 to 8 columns");
+    if (!w || !x || !y || ncols <= 0 || nrows <= 0) return host::set_error(host::ERR_SHAPE, "gemv: bad arguments");
+    if (dtype == T_BF16) return launch_gemv<true>(w, x, y, ncols, nrows, cols, st);
+    if (dtype == 0) return launch_gemv<false>(w, x, y, ncols, nrows, cols, st);
+    return host::set_error(host::ERR_TYPE, "gemv: router dtype %d not supported (f32 = 0, bf16 = 30)", dtype);
+}
+
+int gemm_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int n_tok, hipStream_t st) {
+    if (!w || !x || !y || ncols <= 0 || nrows <= 0 || n_tok < 0)
+        return host::set_error(host::ERR_SHAPE, "gemm_router: bad arguments");
+    if (n_tok == 0) return host::OK;
+    const dim3 g((unsigned) ((n_tok + 63) / 64), (unsigned) ((nrows + 63) / 64));
+    if (dtype == T_BF16) hipLaunchKernelGGL(k_gemm_router<true>, g, dim3(256), 0, st, w, x, y, ncols, nrows, n_tok);
+    else if (dtype == 0) hipLaunchKernelGGL(k_gemm_router<false>, g, dim3(256), 0, st, w, x, y, ncols, nrows, n_tok);
+    else return host::set_error(host::ERR_TYPE, "gemm_router: dtype %d not supported", dtype);
+    return host::check_launch("gemm_router");
+}
+
+int route_topk(const float *logits, int32_t *ids, float *w, int n_expert, int k, int n_tok, int gating, int norm,
+               hipStream_t st) {
+    if (!logits || !ids || !w || n_expert < 1 || n_expert > 256 || k < 1 || k > 16 || k > n_expert || n_tok < 0 ||
+        (gating != 0 && gating != 1))
+        return host::set_error(host::ERR_SHAPE, "route_topk: expected 1 <= k <= min(16, n_expert), n_expert <= 256");
+    if (n_tok == 0) return host::OK;
+    hipLaunchKernelGGL(k_route_topk, dim3((unsigned) n_tok), dim3(64), 0, st, logits, ids, w, n_expert, k, gating,
+                       norm);
+    return host::check_launch("route_topk");
+}
+
+int moe_combine(const float *dexp, const float *escale, const float *w, const float *sh, const float *x_in, float *out,
+                int n, int k, int n_tok, hipStream_t st) {
+    if (!dexp || !w || !out || n < 0 || k < 1 || n_tok < 0)
+        return host::set_error(host::ERR_SHAPE, "moe_combine: bad arguments");
+    if (n == 0 || n_tok == 0) return host::OK;
+    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned) ((n + 255) / 256), (unsigned) n_tok), dim3(256), 0, st, dexp,
+                       escale, w, sh, x_in, out, n, k);
+    return host::check_launch("moe_combine");
+}
+
+int count_routes(const int32_t *ids, uint32_t *counts, int k, hipStream_t st) {
+    if (!ids || !counts || k < 1 || k > 64) return host::set_error(host::ERR_SHAPE, "count_routes: bad arguments");
+    hipLaunchKernelGGL(k_count_routes, dim3(1), dim3(64), 0, st, ids, counts, k);
+    return host::check_launch("count_routes");
+}
+
+}  // namespace impl
+
+namespace k {
+
+void gemv_bf16(const void *w, const float *x, float *y, int ncols, int nrows, int cols, hipStream_t st) {
+    host::abort_on_error(impl::gemv_router(T_BF16, w, x, y, ncols, nrows, cols, st), "gemv_bf16");
+}
+void gemv_f32(const float *w, const float *x, float *y, int ncols, int nrows, int cols, hipStream_t st) {
+    host::abort_on_error(impl::gemv_router(0, w, x, y, ncols, nrows, cols, st), "gemv_f32");
+}
+void route_topk(const float *logits, int32_t *ids, float *w, int n_expert, int k, hipStream_t st, Gating gating,
+                bool norm) {
+    host::abort_on_error(impl::route_topk(logits, ids, w, n_expert, k, 1, gating, norm, st), "route_topk");
+}
+void route_topk_batch(const float *logits, int32_t *ids, float *w, int n_expert, int k, int n_tok, hipStream_t st,
+                      Gating gating, bool norm) {
+    host::abort_on_error(impl::route_topk(logits, ids, w, n_expert, k, n_tok, gating, norm, st), "route_topk_batch");
+}
+void count_routes(const int32_t *ids, uint32_t *counts, int k, hipStream_t st) {
+    host::abort_on_error(impl::count_routes(ids, counts, k, st), "count_routes");
+}
+void moe_combine(const float *dexp, const float *escale, const float *w, const float *sh, float *x, int n, int k,
+                 hipStream_t st) {
+    host::abort_on_error(impl::moe_combine(dexp, escale, w, sh, x, x, n, k, 1, st), "moe_combine");
+}
+void moe_combine_batch(const float *dexp, const float *escale, const float *w, const float *sh, float *x, int n,
+                       int k, int n_tok, hipStream_t st) {
+    host::abort_on_error(impl::moe_combine(dexp, escale, w, sh, x, x, n, k, n_tok, st), "moe_combine_batch");
+}
+void gemm_bf16_batch(void *, const void *w, const float *x, void *, float *y, int ncols, int nrows, int n_tok,
+                     hipStream_t st) {
+    host::abort_on_error(impl::gemm_router(T_BF16, w, x, y, ncols, nrows, n_tok, st), "gemm_bf16_batch");
+}
+void gemm_f32_batch(const float *w, const float *x, float *y, int ncols, int nrows, int n_tok, hipStream_t st) {
+    host::abort_on_error(impl::gemm_router(0, w, x, y, ncols, nrows, n_tok, st), "gemm_f32_batch");
+}
+
+}  // namespace k
+
+}  // namespace fns

@@ -1,0 +1,63 @@
+"""The C ABI library loads and exports every symbol include/fns_hip.h declares; argument validation happens on the
+host before any launch (these calls never touch a GPU). Reference error behaviour: unsupported types and shape
+preconditions are rejected (reference src/ggml/ggml_mmvq.cu:385, src/kernels.cu:911-918); the C ABI reports them
+as status codes, the C++ API aborts."""
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from flintnsteel_amd import _lib
+
+
+def test_exports_every_declared_symbol():
+    L = _lib.lib()
+    declared = _lib.header_symbols()
+    assert len(declared) >= 20
+    missing = [s for s in declared if not hasattr(L, s)]
+    assert not missing, f"declared in include/fns_hip.h but not exported: {missing}"
+    untyped = [s for s in declared if s not in _lib.SIGNATURES]
+    assert not untyped, f"no ctypes signature for {untyped}"
+
+
+def test_q8_1_row_bytes_padding():
+    L = _lib.lib()
+    assert L.fns_hip_q8_1_row_bytes(2048) == 64 * 36
+    assert L.fns_hip_q8_1_row_bytes(768) == 32 * 36   # padded to 1024 columns
+    assert L.fns_hip_q8_1_row_bytes(1) == 16 * 36
+
+
+def test_supported_types():
+    L = _lib.lib()
+    assert [t for t in range(40) if L.fns_hip_mmvq_supports(t)] == [11, 12, 13, 14]
+
+
+def _buf():
+    return ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+
+
+def test_unsupported_type_is_rejected():
+    L = _lib.lib()
+    rc = L.fns_hip_mmvq(8, _buf(), 2048, 16, _buf(), _buf(), 1, None)
+    assert rc == -1
+    assert b"not supported" in L.fns_hip_last_error()
+    with pytest.raises(_lib.FnsError, match="not supported"):
+        _lib.call("fns_hip_mmvq_experts", 99, _buf(), 0, 2048, 16, _buf(), 1, _buf(), 8, _buf(), None)
+
+
+def test_shape_preconditions():
+    L = _lib.lib()
+    assert L.fns_hip_mmvq(12, _buf(), 1000, 16, _buf(), _buf(), 1, None) == -2      # ncols % 256
+    assert L.fns_hip_mmvq_experts_swiglu(12, _buf(), 0, 0, 2048, 768, _buf(), 3, _buf(), 8, _buf(), None) == -2
+    assert L.fns_hip_route_topk(_buf(), _buf(), _buf(), 300, 8, 1, 0, 1, None) == -2  # > 256 experts
+    assert L.fns_hip_route_topk(_buf(), _buf(), _buf(), 128, 17, 1, 0, 1, None) == -2  # k > 16
+    assert L.fns_hip_gemv_router(0, _buf(), _buf(), _buf(), 2048, 128, 9, None) == -2  # > 8 columns
+    assert L.fns_hip_gemv_router(5, _buf(), _buf(), _buf(), 2048, 128, 1, None) == -1  # router dtype
+
+
+def test_empty_inputs_are_noops():
+    L = _lib.lib()
+    assert L.fns_hip_mmvq_experts(12, _buf(), 0, 2048, 16, _buf(), 1, _buf(), 0, _buf(), None) == 0
+    assert L.fns_hip_quantize_q8_1(_buf(), _buf(), 2048, 0, None) == 0
+    assert L.fns_hip_route_topk(_buf(), _buf(), _buf(), 128, 8, 0, 0, 1, None) == 0
