@@ -1,0 +1,280 @@
+#!/usr/bin/env python3
+"""bench.py - MI355X MoE FFN decode benchmark (BASELINE.json metric: us/token per MoE layer + achieved HBM GB/s,
+batch 1, Q4_K experts).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-extra]
+
+Workload (config 0): one MoE FFN layer at batch 1 - hidden 2048, 128 experts, top-8 softmax gating with
+renormalisation, SwiGLU experts of width 768, gate/up/down Q4_K (ggml reference quantiser on N(0, 0.02)), fp32
+router N(0, 0.02), x ~ N(0, 1) fresh per layer and step. A "step" is one token through L resident copies of that
+layer (distinct weights, L * 340 MB > the 256 MB Infinity Cache, so every layer streams its experts from HBM);
+value = step time / L. All inputs are resident in HBM before the timed region; each layer is the library's
+three-kernel fns_hip_moe_layer call, replayed from a HIP graph.
+
+The JSON line also carries:
+  roofline     - for the dominant kernel (gate/up + SwiGLU, k_gate_up): algorithmic bytes per launch (8 experts x
+                 (gate + up) Q4_K = 14,155,776 B) / its average duration, timed with HIP events on the launch stream
+                 over back-to-back launches on rotating layers; peak 8 TB/s (MI355X HBM3E); traffic from the committed
+                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/) when present.
+  cpu_baseline - the oracle's OpenMP CPU restatement of the same layer (int8 x K-quant dot products, not ggml), timed
+                 on this host's cores on a bounded sample.
+  extra        - configs 1 (Q3_K/Q5_K mix), 2 (4-token speculative verify) and 3 (48-layer Q4_K/Q6_K stack).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+H, F, NE, K_TOP = 2048, 768, 128, 8
+SEED = 20261022
+Q3_K, Q4_K, Q5_K, Q6_K = 11, 12, 13, 14
+BLOCK = {Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+PEAK_GBS = 8000.0
+
+
+def expert_bytes(gu: int, dn: int) -> int:
+    return 2 * F * (H // 256) * BLOCK[gu] + H * (F // 256) * BLOCK[dn]
+
+
+def layer_bytes(gu: int, dn: int, n_distinct: int = K_TOP) -> int:
+    """Algorithmic HBM bytes of one layer-token: the selected experts' gate/up/down blocks + the fp32 router."""
+    return n_distinct * expert_bytes(gu, dn) + NE * H * 4
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_layers(synth, n: int, gu: int, dn: int, seed_base: int):
+    return [synth.build_layer(H, F, NE, K_TOP, gu, dn, SEED, layer=seed_base + l) for l in range(n)]
+
+
+def make_xs(synth, torch, n_tok: int, n_steps: int, n_layers: int, seed_layer0: int):
+    """x[s][l] ~ N(0, 1) [n_tok][H]: fresh per (step, layer)."""
+    xs = torch.empty(n_steps, n_layers, n_tok, H, device="cuda")
+    for l in range(n_layers):
+        for s in range(n_steps):
+            xs[s, l].copy_(synth.activations(n_tok, H, SEED, layer=seed_layer0 + l, step=s))
+    return xs
+
+
+def capture(torch, layers, xs, outs, wss, steps_per_graph: int):
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for st in range(steps_per_graph):  # eager warm-up of every launch in the graph
+            for l, layer in enumerate(layers):
+                layer(xs[st, l], out=outs[l], ws=wss[l])
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for st in range(steps_per_graph):
+            for l, layer in enumerate(layers):
+                layer(xs[st, l], out=outs[l], ws=wss[l])
+    return g
+
+
+def time_graph(torch, g, replays: int, warmup: int) -> float:
+    """ms per replay."""
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / replays
+
+
+def stage_times(torch, layers, xs, outs, wss, reps: int) -> list[float]:
+    """Average duration (us) of each of the three kernels, timed with HIP events on the launch stream over
+    back-to-back launches of the same kernel on the L rotating layers (inputs left by the previous stage)."""
+    L = len(layers)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+    tot = [0.0, 0.0, 0.0]
+    n_steps = xs.shape[0]
+    for r in range(reps):
+        st = r % n_steps
+        for k in range(3):
+            ev[2 * k].record()
+            for l, layer in enumerate(layers):
+                layer.stage(k, xs[st, l], outs[l], wss[l])
+            ev[2 * k + 1].record()
+        torch.cuda.synchronize()
+        for k in range(3):
+            tot[k] += ev[2 * k].elapsed_time(ev[2 * k + 1]) * 1e3 / L
+    return [t / reps for t in tot]
+
+
+def read_traffic() -> dict | None:
+    """HBM bytes per k_gate_up launch from the committed rocprofv3 --pmc summary (calibrated), if present."""
+    p = ROOT / "profiles" / "k_gate_up_cfg0_traffic.md"
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return {"bytes": float(m.group(1))} if m else None
+
+
+def cpu_baseline(torch, layer, budget_s: float = 15.0) -> dict:
+    """Oracle CPU restatement of one config-0 layer on this host (bounded sample)."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    nthreads = min(os.cpu_count() or 1, 16)
+    router = layer.router_w.cpu().numpy()
+    slots = [layer.slots.expert_bytes(e).cpu().numpy() for e in range(NE)]
+    xs = [torch.randn(H, generator=torch.Generator().manual_seed(SEED + i)).numpy().astype(np.float32) for i in range(4)]
+    args = (Q4_K, Q4_K, router, slots, layer.slots.gate_off, layer.slots.up_off, layer.slots.down_off)
+    orc.cpu_moe_layer(*args, xs[0], H, F, K_TOP, nthreads)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        orc.cpu_moe_layer(*args, xs[n % 4], H, F, K_TOP, nthreads)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt > budget_s or n >= 2000:
+            break
+    return {"value": dt / n * 1e6, "unit": "us/layer", "cores": nthreads, "kind": "port",
+            "sample": f"{n} batch-1 config-0 layers (Q4_K, 128 experts, top-8) with fresh x; OpenMP restatement in "
+                      f"oracle/fns_oracle.c (int8 x K-quant integer dots), not ggml (llama.cpp is not on the box)"}
+
+
+def run_stack(torch, synth, gu: int, dn: int, n_layers: int, n_tok: int, steps: int, warmup: int, seed_base: int,
+              steps_per_graph: int = 4):
+    layers = build_layers(synth, n_layers, gu, dn, seed_base)
+    xs = make_xs(synth, torch, n_tok, steps_per_graph, n_layers, seed_base + 500)
+    outs = [torch.empty(n_tok, H, device="cuda") for _ in layers]
+    wss = [layer.workspace(n_tok) for layer in layers]
+    g = capture(torch, layers, xs, outs, wss, steps_per_graph)
+    replays = max(1, steps // steps_per_graph)
+    ms = time_graph(torch, g, replays, warmup)
+    distinct = float(sum(len(torch.unique(layer.trace(ws, n_tok)["ids"])) for layer, ws in zip(layers, wss)) / n_layers)
+    del g
+    return layers, ms / steps_per_graph, distinct
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--layers", type=int, default=16, help="resident copies of the config-0 layer (MALL defeat)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 1-3")
+    ap.add_argument("--profile-stages", type=int, default=0,
+                    help="profiling mode for rocprofv3: only N back-to-back rounds of the three kernels + a 256 MiB copy")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the MoE layer would shard "
+              f"experts across GPUs (see DESIGN.md), which is not built or measured here.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from flintnsteel_amd import synth
+    torch.cuda.init()
+    dev = torch.cuda.get_device_properties(0)
+    log(f"device {dev.name} {dev.gcnArchName if hasattr(dev, 'gcnArchName') else ''} CUs {dev.multi_processor_count}")
+
+    L = args.layers
+    t0 = time.time()
+    layers = build_layers(synth, L, Q4_K, Q4_K, 0)
+    torch.cuda.synchronize()
+    log(f"built {L} config-0 layers in {time.time() - t0:.1f} s")
+    steps_per_graph = max(d for d in range(1, 9) if args.steps % d == 0)
+    xs = make_xs(synth, torch, 1, steps_per_graph, L, 1000)
+    outs = [torch.empty(1, H, device="cuda") for _ in layers]
+    wss = [layer.workspace(1) for layer in layers]
+
+    if args.profile_stages:
+        for r in range(args.profile_stages):
+            for k in range(3):
+                for l, layer in enumerate(layers):
+                    layer.stage(k, xs[r % steps_per_graph, l], outs[l], wss[l])
+        a = torch.empty(64 << 20, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)  # 256 MiB read + 256 MiB write: FETCH_SIZE / WRITE_SIZE calibration
+        torch.cuda.synchronize()
+        log("profile rounds done")
+        return 0
+
+    g = capture(torch, layers, xs, outs, wss, steps_per_graph)
+    replays = args.steps // steps_per_graph
+    ms_replay = time_graph(torch, g, replays, max(1, args.warmup // steps_per_graph))
+    ms_per_step = ms_replay / steps_per_graph
+    us_layer = ms_per_step * 1e3 / L
+    log(f"config 0: {us_layer:.2f} us/layer ({ms_per_step:.3f} ms per step of {L} layers)")
+    st = stage_times(torch, layers, xs, outs, wss, reps=16)
+    log(f"per-kernel (us): router {st[0]:.2f}  gate/up {st[1]:.2f}  down+combine {st[2]:.2f}")
+    gu_bytes = K_TOP * 2 * F * (H // 256) * BLOCK[Q4_K]
+    achieved = gu_bytes / (st[1] * 1e-6) / 1e9
+    traffic = read_traffic()
+    roofline = {"bound": "hbm", "kernel": "k_gate_up (routing + gate/up + SwiGLU)", "achieved": round(achieved, 1),
+                "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
+                "traffic": traffic["bytes"] if traffic else None, "algorithmic_bytes": gu_bytes,
+                "avg_us": round(st[1], 3)}
+    layer_gbs = layer_bytes(Q4_K, Q4_K) / (us_layer * 1e-6) / 1e9
+    del g
+
+    extra = {"config0_layer_hbm_gbs": round(layer_gbs, 1), "config0_stage_us": [round(v, 3) for v in st]}
+    if not args.no_extra:
+        for name, gu, dn in (("config1_q3k_q5k", Q3_K, Q5_K),):
+            _, ms, _ = run_stack(torch, synth, gu, dn, L, 1, 16, 4, 100)
+            us = ms * 1e3 / L
+            extra[name] = {"us_per_layer": round(us, 3),
+                           "hbm_gbs": round(layer_bytes(gu, dn) / (us * 1e-6) / 1e9, 1)}
+            log(f"{name}: {us:.2f} us/layer")
+        _, ms, distinct = run_stack(torch, synth, Q4_K, Q4_K, L, 4, 16, 4, 200)
+        us = ms * 1e3 / L
+        extra["config2_verify4"] = {"us_per_layer_step": round(us, 3), "distinct_experts": distinct,
+                                    "hbm_gbs": round(layer_bytes(Q4_K, Q4_K, distinct) / (us * 1e-6) / 1e9, 1)}
+        log(f"config2 (4-token verify): {us:.2f} us/layer, {distinct:.1f} distinct experts")
+        del layers
+        torch.cuda.empty_cache()
+        t1 = time.time()
+        stack, ms, _ = run_stack(torch, synth, Q4_K, Q6_K, 48, 1, 256, 8, 300, steps_per_graph=4)
+        tok_s = 1e3 / ms
+        per_tok = 48 * layer_bytes(Q4_K, Q6_K)
+        extra["config3_stack48"] = {"tokens_per_s": round(tok_s, 1), "us_per_layer": round(ms * 1e3 / 48, 3),
+                                    "hbm_gbs": round(per_tok * tok_s / 1e9, 1), "build_s": round(time.time() - t1, 1)}
+        log(f"config3 (48 layers): {tok_s:.1f} tok/s")
+        layers = stack[:1]
+        del stack
+    cpu = None
+    if not args.no_cpu:
+        if args.no_extra:
+            cpu_layer = layers[0]
+        else:
+            cpu_layer = build_layers(synth, 1, Q4_K, Q4_K, 0)[0]
+        cpu = cpu_baseline(torch, cpu_layer)
+        log(f"cpu baseline: {cpu['value']:.1f} us/layer on {cpu['cores']} threads")
+
+    line = {
+        "metric": "us/token per MoE layer + achieved HBM GB/s (batch 1, Q4_K experts)",
+        "value": round(us_layer, 3), "unit": "us/layer", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8xK-quant dot, fp32 accumulate", "data": "synthetic (seeded Philox N(0,1) / N(0,0.02) on device)",
+        "config": {"workload": "config 0: 1 MoE FFN layer, decode batch 1, hidden 2048, 128 experts top-8 softmax, "
+                               f"inter 768, Q4_K gate/up/down, fp32 router; {L} resident layer copies per step",
+                   "layers_per_step": L, "hbm_bytes_per_layer": layer_bytes(Q4_K, Q4_K),
+                   "achieved_layer_hbm_gbs": round(layer_gbs, 1)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

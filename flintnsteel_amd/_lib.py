@@ -44,6 +44,12 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_amax_guard": [_P, _P, _I, _I, _P],
     "fns_hip_amax_guard_q8_1": [_P, _P, _P, _I, _I, _P],
     "fns_hip_moe_combine": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "fns_hip_moe_workspace_layout": [_P, _I, _P, _P],
+    "fns_hip_moe_layer": [_P, _P, _P, _P, _I, _P, _SZ, _P],
+    "fns_hip_moe_layer_profiled": [_P, _P, _P, _P, _I, _P, _SZ, _P, _P],
+    "fns_hip_moe_layer_stage": [_P, _I, _P, _P, _P, _I, _P, _SZ, _P],
+    "fns_hip_fill_normal": [_P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F, _F, _P],
+    "fns_hip_quantize_weights": [_I, _P, _P, _I64, _I64, _P],
 }
 _RESTYPE = {
     "fns_hip_last_error": ctypes.c_char_p,

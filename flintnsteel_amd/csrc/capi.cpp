@@ -101,4 +101,31 @@ int fns_hip_moe_combine(const float *dexp, const float *escale, const float *w, 
     return impl::moe_combine(dexp, escale, w, sh, x_in, out, n, k, n_tok, S(stream));
 }
 
+int fns_hip_moe_workspace_layout(const FnsMoeLayer *layer, int n_tok, size_t *offsets, size_t *total_bytes) {
+    return impl::moe_workspace_layout(layer, n_tok, offsets, total_bytes);
+}
+
+int fns_hip_moe_layer(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int n_tok,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+    return impl::moe_layer(layer, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream));
+}
+
+int fns_hip_moe_layer_profiled(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int n_tok,
+                               void *workspace, size_t workspace_bytes, void *const *events, void *stream) {
+    return impl::moe_layer(layer, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream), events);
+}
+
+int fns_hip_moe_layer_stage(const FnsMoeLayer *layer, int stage, const float *x, const float *x_resid, float *out,
+                            int n_tok, void *workspace, size_t workspace_bytes, void *stream) {
+    return impl::moe_layer_stage(layer, stage, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream));
+}
+
+int fns_hip_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, void *stream) {
+    return impl::fill_normal(out, n, seed, offset, mean, std, S(stream));
+}
+
+int fns_hip_quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, void *stream) {
+    return impl::quantize_weights(type, x, out, nrows, ncols, S(stream));
+}
+
 }  // extern "C"

@@ -37,6 +37,21 @@ inline int64_t kquant_block_bytes(int t) {
 }
 inline int64_t q8_1_row_bytes(int64_t ncols) { return pad512(ncols) / 32 * 36; }
 
+// Lane-group shape for a row of `nslots` 16-byte slots: lanes per row (a power of two dividing the slot count, at
+// most the 64-lane wave) and slots per lane (0: runtime loop for uncommon shapes).
+struct Shape {
+    int lpr, spl;
+};
+inline Shape pick_shape(int nslots) {
+    if (nslots % 64 == 0 && nslots / 64 <= 3) return {64, nslots / 64};
+    if (nslots == 32) return {32, 1};
+    if (nslots == 16) return {16, 1};
+    if (nslots == 24) return {8, 3};
+    if (nslots == 12) return {4, 3};
+    return {64, 0};
+}
+inline int slots_per_block(int t) { return t == 11 ? 4 : 8; }
+
 }  // namespace fns::host
 
 #define FNS_TRY(...)                       \

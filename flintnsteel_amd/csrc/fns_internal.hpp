@@ -42,4 +42,13 @@ int moe_combine(const float *dexp, const float *escale, const float *w, const fl
                 int n, int k, int n_tok, hipStream_t st);
 int count_routes(const int32_t *ids, uint32_t *counts, int k, hipStream_t st);
 
+int moe_workspace_layout(const FnsMoeLayer *L, int n_tok, size_t *offsets, size_t *total);
+int moe_layer(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int n_tok, void *ws,
+              size_t ws_bytes, hipStream_t st, void *const *events = nullptr);
+int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float *x_resid, float *out, int n_tok,
+                    void *ws, size_t ws_bytes, hipStream_t st);
+
+int fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t st);
+int quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, hipStream_t st);
+
 }  // namespace fns::impl

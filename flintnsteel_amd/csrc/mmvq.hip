@@ -181,19 +181,6 @@ __global__ __launch_bounds__(256) void k_mmvq(const MmvqParams p) {
     }
 }
 
-// Lane-group shape for a row of `nslots` slots: lanes per row (LPR) and slots per lane (SPL, 0 = loop).
-struct Shape {
-    int lpr, spl;
-};
-Shape pick_shape(int nslots) {
-    if (nslots % 64 == 0 && nslots / 64 <= 3) return {64, nslots / 64};
-    if (nslots == 32) return {32, 1};
-    if (nslots == 16) return {16, 1};
-    if (nslots % 8 == 0 && nslots / 8 == 3) return {8, 3};
-    if (nslots % 4 == 0 && nslots / 4 == 3) return {4, 3};
-    return {64, 0};
-}
-
 template <int T, int LPR, int SPL, int NC, bool GLU>
 int launch_shape(const MmvqParams &p, int n_chan, hipStream_t st) {
     constexpr int RPB = (256 / LPR) * rows_per_group<LPR>();
@@ -206,7 +193,7 @@ int launch_shape(const MmvqParams &p, int n_chan, hipStream_t st) {
 }
 
 template <int T, int NC, bool GLU> int launch_nc(const MmvqParams &p, int n_chan, hipStream_t st) {
-    const Shape s = pick_shape(p.ncols / 256 * Traits<T>::slots);
+    const host::Shape s = host::pick_shape(p.ncols / 256 * Traits<T>::slots);
     if (s.lpr == 64 && s.spl == 1) return launch_shape<T, 64, 1, NC, GLU>(p, n_chan, st);
     if (s.lpr == 64 && s.spl == 2) return launch_shape<T, 64, 2, NC, GLU>(p, n_chan, st);
     if (s.lpr == 64 && s.spl == 3) return launch_shape<T, 64, 3, NC, GLU>(p, n_chan, st);

@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import torch
 
 from ._lib import call, lib
@@ -198,22 +199,123 @@ class ExpertSlots:
     """Fully resident expert storage: expert e is one slot [gate | up | down] of raw GGUF blocks at
     base + e * slot_bytes (256-byte aligned), plus a device table of slot pointers - the reference engine's
     `exp_table` / `gate_bytes` / `up_bytes` contract (reference include/fns/engine.h:28-32, src/engine.cu:375-471),
-    in the trivial case where every expert lives in HBM.
+    in the trivial case where every expert lives in HBM. `pad` bytes of zeros follow the last slot
+    (reference src/engine.cu:42-45).
     """
 
-    def __init__(self, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor, pad: int = 4096):
-        # gate/up/down: uint8 [n_expert][bytes per expert matrix] (host or device)
-        n = gate.shape[0]
-        self.n_expert = n
-        self.gate_bytes, self.up_bytes, self.down_bytes = gate.shape[1], up.shape[1], down.shape[1]
-        raw = self.gate_bytes + self.up_bytes + self.down_bytes
+    def __init__(self, n_expert: int, gate_bytes: int, up_bytes: int, down_bytes: int, pad: int = 4096):
+        self.n_expert = n_expert
+        self.gate_bytes, self.up_bytes, self.down_bytes = gate_bytes, up_bytes, down_bytes
+        raw = gate_bytes + up_bytes + down_bytes
         self.slot_bytes = (raw + 255) // 256 * 256
-        self.gate_off, self.up_off, self.down_off = 0, self.gate_bytes, self.gate_bytes + self.up_bytes
-        dev = torch.device("cuda")
-        self.storage = torch.zeros(n * self.slot_bytes + pad, dtype=torch.uint8, device=dev)
-        view = self.storage[: n * self.slot_bytes].view(n, self.slot_bytes)
-        view[:, : self.gate_bytes].copy_(gate.to(dev))
-        view[:, self.up_off: self.up_off + self.up_bytes].copy_(up.to(dev))
-        view[:, self.down_off: self.down_off + self.down_bytes].copy_(down.to(dev))
+        self.gate_off, self.up_off, self.down_off = 0, gate_bytes, gate_bytes + up_bytes
+        self.storage = torch.zeros(n_expert * self.slot_bytes + pad, dtype=torch.uint8, device="cuda")
         base = self.storage.data_ptr()
-        self.table = torch.tensor([base + e * self.slot_bytes for e in range(n)], dtype=torch.int64, device=dev)
+        self.table = torch.tensor([base + e * self.slot_bytes for e in range(n_expert)], dtype=torch.int64,
+                                  device="cuda")
+
+    @classmethod
+    def from_tensors(cls, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor, pad: int = 4096):
+        """gate/up/down: uint8 [n_expert][bytes of one expert matrix] (host or device)."""
+        s = cls(gate.shape[0], gate.shape[1], up.shape[1], down.shape[1], pad)
+        for name, t in (("gate", gate), ("up", up), ("down", down)):
+            s.view(name).copy_(t.to("cuda"))
+        return s
+
+    def view(self, name: str) -> torch.Tensor:
+        """[n_expert][bytes] strided view of one matrix kind inside the slots."""
+        off = {"gate": self.gate_off, "up": self.up_off, "down": self.down_off}[name]
+        size = {"gate": self.gate_bytes, "up": self.up_bytes, "down": self.down_bytes}[name]
+        slots = self.storage[: self.n_expert * self.slot_bytes].view(self.n_expert, self.slot_bytes)
+        return slots[:, off: off + size]
+
+    def expert_bytes(self, e: int) -> torch.Tensor:
+        return self.storage[e * self.slot_bytes: (e + 1) * self.slot_bytes]
+
+
+class MoeLayerDesc(ctypes.Structure):
+    """Mirror of FnsMoeLayer (include/fns_hip.h)."""
+    _fields_ = [
+        ("hidden", ctypes.c_int), ("inter", ctypes.c_int), ("n_expert", ctypes.c_int), ("k", ctypes.c_int),
+        ("gating", ctypes.c_int), ("norm_w", ctypes.c_int), ("guard", ctypes.c_int),
+        ("router_dtype", ctypes.c_int), ("router_w", ctypes.c_void_p),
+        ("gu_type", ctypes.c_int), ("down_type", ctypes.c_int),
+        ("table", ctypes.c_void_p), ("gate_off", ctypes.c_size_t), ("up_off", ctypes.c_size_t),
+        ("down_off", ctypes.c_size_t),
+    ]
+
+
+WS_SECTIONS = ("logits", "xq", "ids", "w", "act", "escale")
+
+
+class MoeLayer:
+    """One MoE FFN layer resident in HBM: fp32/bf16 router + expert slots, run by fns_hip_moe_layer."""
+
+    def __init__(self, router_w: torch.Tensor, slots: ExpertSlots, gu_type: int, down_type: int, hidden: int,
+                 inter: int, k: int, gating: int = GATING_SOFTMAX, norm: bool = True, guard: bool = False):
+        self.router_w, self.slots = router_w, slots
+        self.desc = MoeLayerDesc(hidden, inter, slots.n_expert, k, gating, int(norm), int(guard),
+                                 _dtype_code(router_w), router_w.data_ptr(), gu_type, down_type,
+                                 slots.table.data_ptr(), slots.gate_off, slots.up_off, slots.down_off)
+
+    def workspace_layout(self, n_tok: int):
+        offs = (ctypes.c_size_t * 6)()
+        total = ctypes.c_size_t()
+        call("fns_hip_moe_workspace_layout", ctypes.byref(self.desc), n_tok, offs, ctypes.byref(total))
+        return list(offs), total.value
+
+    def workspace(self, n_tok: int) -> torch.Tensor:
+        _, total = self.workspace_layout(n_tok)
+        return torch.zeros(total, dtype=torch.uint8, device="cuda")
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
+                 x_resid: torch.Tensor | None = None) -> torch.Tensor:
+        x = x.contiguous()
+        n_tok = x.numel() // self.desc.hidden
+        out = torch.empty_like(x) if out is None else out
+        ws = self.workspace(n_tok) if ws is None else ws
+        call("fns_hip_moe_layer", ctypes.byref(self.desc), _p(x), _p(x_resid), _p(out), n_tok, _p(ws), ws.numel(), _s())
+        return out
+
+    def stage(self, stage: int, x: torch.Tensor, out: torch.Tensor, ws: torch.Tensor,
+              x_resid: torch.Tensor | None = None) -> None:
+        """Launch one of the layer's three kernels (0 router, 1 gate/up, 2 down + combine)."""
+        n_tok = x.numel() // self.desc.hidden
+        call("fns_hip_moe_layer_stage", ctypes.byref(self.desc), stage, _p(x), _p(x_resid), _p(out), n_tok, _p(ws),
+             ws.numel(), _s())
+
+    def profiled(self, x: torch.Tensor, out: torch.Tensor, ws: torch.Tensor, events) -> None:
+        """Full layer with torch.cuda.Event markers before each kernel and after the last (4 events, recorded)."""
+        n_tok = x.numel() // self.desc.hidden
+        arr = (ctypes.c_void_p * 4)(*[e.cuda_event for e in events])
+        call("fns_hip_moe_layer_profiled", ctypes.byref(self.desc), _p(x), None, _p(out), n_tok, _p(ws), ws.numel(),
+             arr, _s())
+
+    def trace(self, ws: torch.Tensor, n_tok: int) -> dict:
+        """Views of the intermediates a call left in its workspace."""
+        offs, _ = self.workspace_layout(n_tok)
+        d = self.desc
+        sizes = {"logits": (torch.float32, (n_tok, d.n_expert)), "xq": (torch.uint8, (n_tok, q8_1_row_bytes(d.hidden))),
+                 "ids": (torch.int32, (n_tok, d.k)), "w": (torch.float32, (n_tok, d.k)),
+                 "act": (torch.float32, (n_tok * d.k, d.inter)), "escale": (torch.float32, (n_tok * d.k,))}
+        out = {}
+        for name, off in zip(WS_SECTIONS, offs):
+            dt, shape = sizes[name]
+            n = int(np.prod(shape)) * torch.tensor([], dtype=dt).element_size()
+            out[name] = ws[off:off + n].view(dt).view(*shape)
+        return out
+
+
+def fill_normal(out: torch.Tensor, seed: int, offset: int = 0, mean: float = 0.0, std: float = 1.0) -> torch.Tensor:
+    call("fns_hip_fill_normal", _p(out), out.numel(), seed, offset, ctypes.c_float(mean), ctypes.c_float(std), _s())
+    return out
+
+
+def quantize_weights(qtype: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x f32 [..., ncols] on the device -> uint8 [..., row_bytes] GGUF blocks (ggml reference quantisers)."""
+    ncols = x.shape[-1]
+    nrows = x.numel() // ncols
+    if out is None:
+        out = torch.empty(*x.shape[:-1], row_bytes(qtype, ncols), dtype=torch.uint8, device=x.device)
+    call("fns_hip_quantize_weights", qtype, _p(x.contiguous()), _p(out), nrows, ncols, _s())
+    return out

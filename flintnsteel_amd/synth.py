@@ -1,0 +1,52 @@
+"""Seeded synthetic MoE layers built on the device (the configs' data: router fp32 ~N(0, 0.02), expert gate/up
+[inter x hidden] and down [hidden x inter] ~N(0, 0.02) quantised with ggml's reference quantisers, activations
+~N(0, 1)). Everything is generated and quantised by libfns_hip.so on the GPU, so a 48-layer stack of 128 experts
+(~18.8 GB of blocks) builds in seconds; nothing here is measured.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+KIND_ROUTER, KIND_GATE, KIND_UP, KIND_DOWN, KIND_X, KIND_BIAS = range(6)
+
+
+def tensor_seed(seed: int, layer: int, kind: int) -> int:
+    """Independent Philox key per (config seed, layer, tensor kind)."""
+    return (seed * 1_000_003 + layer * 1_009 + kind * 7) & 0xFFFFFFFFFFFFFFFF
+
+
+def quantized_matrices(qtype: int, n_mat: int, nrows: int, ncols: int, seed: int, std: float, out: torch.Tensor,
+                       chunk_values: int = 1 << 25) -> None:
+    """out[m] <- quantize(N(0, std) [nrows][ncols]) for m < n_mat; fp32 is generated in chunks of whole matrices."""
+    per = nrows * ncols
+    mats_per_chunk = max(1, chunk_values // per)
+    scratch = torch.empty(mats_per_chunk * per, dtype=torch.float32, device="cuda")
+    for m0 in range(0, n_mat, mats_per_chunk):
+        m = min(mats_per_chunk, n_mat - m0)
+        buf = scratch[: m * per]
+        ops.fill_normal(buf, seed, offset=m0 * per, std=std)
+        q = ops.quantize_weights(qtype, buf.view(m * nrows, ncols))
+        out[m0: m0 + m].copy_(q.view(m, -1))
+
+
+def build_layer(hidden: int, inter: int, n_expert: int, k: int, gu_type: int, down_type: int, seed: int,
+                layer: int = 0, gating: int = ops.GATING_SOFTMAX, guard: bool = False,
+                router_dtype: torch.dtype = torch.float32, std: float = 0.02) -> ops.MoeLayer:
+    router = ops.fill_normal(torch.empty(n_expert, hidden, device="cuda"), tensor_seed(seed, layer, KIND_ROUTER),
+                             std=std)
+    if router_dtype != torch.float32:
+        router = router.to(router_dtype)
+    slots = ops.ExpertSlots(n_expert, ops.row_bytes(gu_type, hidden) * inter, ops.row_bytes(gu_type, hidden) * inter,
+                            ops.row_bytes(down_type, inter) * hidden)
+    quantized_matrices(gu_type, n_expert, inter, hidden, tensor_seed(seed, layer, KIND_GATE), std, slots.view("gate"))
+    quantized_matrices(gu_type, n_expert, inter, hidden, tensor_seed(seed, layer, KIND_UP), std, slots.view("up"))
+    quantized_matrices(down_type, n_expert, hidden, inter, tensor_seed(seed, layer, KIND_DOWN), std, slots.view("down"))
+    return ops.MoeLayer(router, slots, gu_type, down_type, hidden, inter, k, gating=gating, guard=guard)
+
+
+def activations(n_tok: int, hidden: int, seed: int, layer: int = 0, step: int = 0) -> torch.Tensor:
+    """x ~ N(0, 1) [n_tok][hidden], fresh per (layer, step)."""
+    x = torch.empty(n_tok, hidden, device="cuda")
+    return ops.fill_normal(x, tensor_seed(seed, layer, KIND_X), offset=step * n_tok * hidden)

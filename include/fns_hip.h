@@ -98,6 +98,47 @@ int fns_hip_amax_guard_q8_1(const float *act, float *escale, void *xq, int n, in
 int fns_hip_moe_combine(const float *dexp, const float *escale, const float *w, const float *sh, const float *x_in,
                         float *out, int n, int k, int n_tok, void *stream);
 
+/* --- fused MoE FFN layer: decode (n_tok = 1) and speculative verify (n_tok <= 4) ---
+ * The MoE section of the reference's Engine::ffn_block (src/engine.cu:655-696: router gemv_bf16, route_topk,
+ * mmvq_experts_swiglu, amax_guard_q8_1, mmvq_experts, moe_combine) as one call of three kernels:
+ *   out[t] = sum_j w[t][j] * e[t][j] * down_{e_j}(q8_1(act[t][j] / e[t][j])) (+ x_resid[t]),
+ *   act[t][j] = up_{e_j} . q8_1(x[t]) * silu(gate_{e_j} . q8_1(x[t])), (ids, w) = top-k of gating(router . x[t]).
+ * Expert e's slot is table[e] (device array) with gate/up/down matrices at the byte offsets below (GGUF blocks).
+ * For n_tok > 1 the selected experts are compacted: each distinct expert's weights are read once per call.
+ * workspace: fns_hip_moe_workspace_layout() bytes, device memory, sections (byte offsets in offsets[6]):
+ *   0 logits f32 [n_tok][n_expert], 1 xq Q8_1 [n_tok][q8_1_row_bytes(hidden)], 2 ids i32 [n_tok][k],
+ *   3 w f32 [n_tok][k], 4 act f32 [n_tok*k][inter], 5 escale f32 [n_tok*k]. */
+typedef struct FnsMoeLayer {
+    int hidden, inter, n_expert, k;
+    int gating;       /* FNS_GATING_SOFTMAX or FNS_GATING_SIGMOID */
+    int norm_w;       /* 1: w = p / max(sum p, 6.103515625e-5) */
+    int guard;        /* 1: F16 guard of act before down (reference src/kernels.cu:534-577) */
+    int router_dtype; /* FNS_TYPE_F32 or FNS_TYPE_BF16 */
+    const void *router_w; /* [n_expert][hidden] */
+    int gu_type, down_type;
+    const void *const *table;
+    size_t gate_off, up_off, down_off;
+} FnsMoeLayer;
+
+int fns_hip_moe_workspace_layout(const FnsMoeLayer *layer, int n_tok, size_t *offsets, size_t *total_bytes);
+int fns_hip_moe_layer(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int n_tok,
+                      void *workspace, size_t workspace_bytes, void *stream);
+/* Same, recording events[0..3] (hipEvent_t, any may be NULL) on `stream` before the router kernel, before the
+ * gate/up kernel, before the down kernel and after it: per-kernel durations for measurement. */
+int fns_hip_moe_layer_profiled(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int n_tok,
+                               void *workspace, size_t workspace_bytes, void *const *events, void *stream);
+/* One of the three kernels of fns_hip_moe_layer (stage 0 router + Q8_1 of x, 1 routing + gate/up + SwiGLU,
+ * 2 F16 guard + Q8_1 of act + down + combine), each reading what the previous stage left in the workspace:
+ * per-stage tracing (the reference's FNS_TRACE nodes, src/engine.cu:590-599) and per-kernel timing. */
+int fns_hip_moe_layer_stage(const FnsMoeLayer *layer, int stage, const float *x, const float *x_resid, float *out,
+                            int n_tok, void *workspace, size_t workspace_bytes, void *stream);
+
+/* --- seeded synthetic data on the device (benchmarks and large tests) ---
+ * out[i] = mean + std * N(0,1), Philox-4x32-10 counter (offset + i) / 4 and Box-Muller; offset % 4 == 0. */
+int fns_hip_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, void *stream);
+/* ggml's reference K-quant quantisers (quantize_row_q{3,4,5,6}_K_ref) on the device: x f32 [nrows][ncols] -> out. */
+int fns_hip_quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
