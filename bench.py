@@ -98,18 +98,27 @@ def time_graph(torch, g, replays: int, warmup: int) -> float:
 
 
 def stage_times(torch, layers, xs, outs, wss, reps: int) -> list[float]:
-    """Average duration (us) of each of the three kernels, timed with HIP events on the launch stream over
-    back-to-back launches of the same kernel on the L rotating layers (inputs left by the previous stage)."""
+    """Average duration (us) of each of the three kernels, timed with HIP events on the launch stream around graph
+    replays of back-to-back launches of that kernel over the L rotating layers (each reads what the previous stage
+    left in its workspace)."""
     L = len(layers)
+    graphs = []
+    for k in range(3):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for l, layer in enumerate(layers):
+                layer.stage(k, xs[0, l], outs[l], wss[l])
+        graphs.append(g)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
     tot = [0.0, 0.0, 0.0]
-    n_steps = xs.shape[0]
-    for r in range(reps):
-        st = r % n_steps
-        for k in range(3):
+    for _ in range(2):
+        for g in graphs:
+            g.replay()
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        for k, g in enumerate(graphs):
             ev[2 * k].record()
-            for l, layer in enumerate(layers):
-                layer.stage(k, xs[st, l], outs[l], wss[l])
+            g.replay()
             ev[2 * k + 1].record()
         torch.cuda.synchronize()
         for k in range(3):

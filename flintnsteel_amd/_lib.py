@@ -50,6 +50,7 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_moe_layer_stage": [_P, _I, _P, _P, _P, _I, _P, _SZ, _P],
     "fns_hip_fill_normal": [_P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F, _F, _P],
     "fns_hip_quantize_weights": [_I, _P, _P, _I64, _I64, _P],
+    "fns_hip_selftest_lanes": [_P, _P],
 }
 _RESTYPE = {
     "fns_hip_last_error": ctypes.c_char_p,

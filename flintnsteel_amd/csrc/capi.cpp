@@ -128,4 +128,6 @@ int fns_hip_quantize_weights(int type, const float *x, void *out, int64_t nrows,
     return impl::quantize_weights(type, x, out, nrows, ncols, S(stream));
 }
 
+int fns_hip_selftest_lanes(int *bad_mask, void *stream) { return impl::selftest_lanes(bad_mask, S(stream)); }
+
 }  // extern "C"

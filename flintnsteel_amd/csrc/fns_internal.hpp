@@ -51,4 +51,6 @@ int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float
 int fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t st);
 int quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, hipStream_t st);
 
+int selftest_lanes(int *bad_mask_device, hipStream_t st);
+
 }  // namespace fns::impl

@@ -1,24 +1,30 @@
 // moe_layer.hip - the fused MoE FFN decode / speculative-verify layer for MI355X gfx950: three kernels per layer.
 //
-//   K1 k_route_quant : router logits (one workgroup per expert row, fp32 or bf16 weights) and Q8_1 of the token rows.
-//   K2 k_gate_up     : every workgroup runs gating + top-k for the n_tok tokens on one wave (the routing is ~1 us of
-//                      ALU and is cheaper to repeat than to publish through a grid barrier), compacts the selected
-//                      experts (distinct ids, ascending, for n_tok > 1; slot order for n_tok = 1), then computes
-//                      act = up . x * silu(gate . x) for its rows of one expert and every token routed to it (ncols <= 4
-//                      per expert: each expert's weights are read once per step).
-//   K3 k_down_combine: stages act of all (token, slot) rows, applies the optional F16 guard and quantises to Q8_1 in
-//                      LDS (bit-exact with amax_guard_q8_1), computes its output rows of down_e . act for every
-//                      (token, slot) and combines them in slot order (reference src/kernels.cu:579-586).
-// On this GPU a kernel boundary inside a HIP graph costs less than a software grid barrier across 256 CUs (measured),
-// so the two global dependencies of the layer (all logits -> routing, all act rows -> down) are kernel boundaries.
+//   K1 k_route_quant : router logits (one workgroup per expert row, fp32 or bf16 weights) and Q8_1 of the token rows
+//                      (the reference's 36-byte blocks, plus an unpacked copy laid out exactly as the LDS image the
+//                      GEMV kernels read, so they stage it with plain 16-byte copies).
+//   K2 k_gate_up     : every workgroup runs gating + top-k for the n_tok tokens on one wave (~1 us of ALU; cheaper
+//                      than publishing the result through a grid barrier), compacts the selected experts (distinct ids
+//                      ascending for n_tok > 1, slot order for n_tok = 1), computes act = up . x * silu(gate . x) for
+//                      32 consecutive rows of one expert for every token routed to it (each expert's weights are read
+//                      once per call), and quantises those 32 rows - one Q8_1 block per (token, slot) - for the down
+//                      projection.
+//   K3 k_down_combine: reads the selected experts' down pointers, issues its weight loads, stages the Q8_1 act rows,
+//                      applies the F16 guard when enabled (re-quantising a row only when its scale is not 1), computes
+//                      its 8 output rows of down_e . act for every (token, slot) and combines them in slot order
+//                      (reference src/kernels.cu:579-586).
+// A kernel boundary inside a HIP graph costs less on this GPU than a software grid barrier across 256 CUs (measured),
+// so the layer's two global dependencies (all logits -> routing, all act rows -> down) are kernel boundaries.
 //
-// Caller contract: reference Engine::ffn_block (src/engine.cu:655-696) - rms_norm_q8_1 output (here: any fp32 x),
-// router, route_topk, mmvq_experts_swiglu, amax_guard_q8_1, mmvq_experts, moe_combine - in one call.
-// Per-(token, row) arithmetic does not depend on the other tokens of the step: a verify column equals the batch-1
-// result bit for bit (reference src/engine.cu:601-603).
+// Caller contract: the MoE section of the reference's Engine::ffn_block (src/engine.cu:655-696) - router, route_topk,
+// mmvq_experts_swiglu, amax_guard_q8_1, mmvq_experts, moe_combine - in one call. Per-(token, row) arithmetic does not
+// depend on the other tokens of the call: a verify column equals the batch-1 result bit for bit (reference
+// src/engine.cu:601-603).
+#include "fns_block.hpp"
 #include "fns_common.hpp"
 #include "fns_host.hpp"
 #include "fns_internal.hpp"
+#include "fns_lanes.hpp"
 #include "fns_route.hpp"
 
 namespace fns {
@@ -28,233 +34,382 @@ using namespace fns::dev;
 namespace {
 
 constexpr int kMaxTok = 4;
+constexpr int kMaxCh = kMaxTok * 16;
+constexpr int kDownRows = 8;  // output rows per down workgroup
 
 struct LayerArgs {
-    // shapes
     int H, F, NE, K, T;
     int gating, norm, guard;
-    // weights
     int router_dtype;
     const void *router_w;
     const char *const *table;
     int64_t gate_off, up_off, down_off;
-    // activations / workspace
-    const float *x;       // [T][H]
-    const float *x_resid; // [T][H] or null
-    float *out;           // [T][H]
+    const float *x;        // [T][H]
+    const float *x_resid;  // [T][H] or null
+    float *out;            // [T][H]
+    // workspace
     float *logits;        // [T][NE]
-    uint8_t *xq;          // [T][q8_1_row_bytes(H)]
-    int64_t xq_row_bytes;
+    uint8_t *xq;          // [T][q8_1_row_bytes(H)]  reference Q8_1 blocks
     int32_t *ids;         // [T][K]
     float *w;             // [T][K]
     float *act;           // [T*K][F]
     float *escale;        // [T*K]
+    uint8_t *xpack;       // [T][act_lds_bytes(Hpad)]   Q8_1 of x, LDS image
+    uint8_t *apack;       // [T*K][act_lds_bytes(Fpad)] Q8_1 of act, LDS image
+    float *blk_amax;      // [T*K][Fpad / 32]
+    const uint8_t **dptr; // [T*K] down matrix of each (token, slot)
+    int64_t xq_row_bytes;
 };
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t) b << 16); }
 
+// Plain copy of `bytes` (multiple of 16) from global memory into LDS by the whole workgroup.
+__device__ __forceinline__ void copy_to_lds(uint8_t *dst, const uint8_t *__restrict__ src, int bytes, int tid, int nt) {
+    for (int i = tid; i < bytes / 16; i += nt) ((uint4 *) dst)[i] = ((const uint4 *) src)[i];
+}
+
+__device__ __forceinline__ ActView view_of(const uint8_t *base, int npad) {
+    return ActView{(const int8_t *) base, (const float *) (base + npad), (const float *) (base + npad) + npad / 32};
+}
+
+// Writes one lane's Q8_1 value into the LDS-image row `pack` (npad columns) at column i; lanes of one block agree
+// on d and the sums.
+__device__ __forceinline__ void pack_store(uint8_t *pack, int npad, int i, const Q8Lane &r) {
+    const float dh = half_to_float(float_to_half(r.d));
+    float *d = (float *) (pack + npad);
+    pack[i] = (uint8_t) (int8_t) r.q;
+    if (i % 32 == 0) d[i / 32] = dh;
+    if (i % 16 == 0) d[npad / 32 + i / 16] = dh * (float) r.qsum16;
+    if (i % 32 == 0) d[npad / 32 + npad / 16 + i / 32] = dh * (float) r.qsum32;
+}
+
 // ---- K1: router rows + Q8_1 of x ----------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_route_quant(const LayerArgs a) {
-    __shared__ float red[4][kMaxTok];
+// 1024-thread workgroups: the first ceil(n_expert / 4) each compute four router rows (256 lanes per row), the rest
+// quantise 1024 columns of one token row. Few, wide workgroups start faster than one small workgroup per row.
+constexpr int kK1Threads = 1024, kK1Rows = 4;
+
+__global__ __launch_bounds__(1024) void k_route_quant(const LayerArgs a) {
+    __shared__ float red[kK1Rows][4][kMaxTok];
     const int H = a.H, T = a.T;
-    if ((int) blockIdx.x < a.NE) {
-        const int r = blockIdx.x;
+    const int n_router_wg = (a.NE + kK1Rows - 1) / kK1Rows;
+    if ((int) blockIdx.x < n_router_wg) {
+        const int sub = threadIdx.x / 256, t256 = threadIdx.x % 256;
+        const int r = blockIdx.x * kK1Rows + sub;
         float s[kMaxTok] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int i = threadIdx.x; i < H / 4; i += 256) {
-            float4 wv;
-            if (a.router_dtype == T_BF16) {
-                const uint2 pk = ((const uint2 *) ((const uint16_t *) a.router_w + (size_t) r * H))[i];
-                wv = make_float4(bf16f(pk.x & 0xffff), bf16f(pk.x >> 16), bf16f(pk.y & 0xffff), bf16f(pk.y >> 16));
-            } else {
-                wv = ((const float4 *) ((const float *) a.router_w + (size_t) r * H))[i];
-            }
+        if (r < a.NE) {
+            for (int i = t256; i < H / 4; i += 256) {
+                float4 wv;
+                if (a.router_dtype == T_BF16) {
+                    const uint2 pk = ((const uint2 *) ((const uint16_t *) a.router_w + (size_t) r * H))[i];
+                    wv = make_float4(bf16f(pk.x & 0xffff), bf16f(pk.x >> 16), bf16f(pk.y & 0xffff), bf16f(pk.y >> 16));
+                } else {
+                    wv = ((const float4 *) ((const float *) a.router_w + (size_t) r * H))[i];
+                }
 #pragma unroll
-            for (int t = 0; t < kMaxTok; ++t) {
-                if (t < T) {
-                    const float4 xv = ((const float4 *) (a.x + (size_t) t * H))[i];
-                    s[t] += wv.x * xv.x + wv.y * xv.y + wv.z * xv.z + wv.w * xv.w;
+                for (int t = 0; t < kMaxTok; ++t) {
+                    if (t < T) {
+                        const float4 xv = ((const float4 *) (a.x + (size_t) t * H))[i];
+                        s[t] += wv.x * xv.x + wv.y * xv.y + wv.z * xv.z + wv.w * xv.w;
+                    }
                 }
             }
         }
 #pragma unroll
         for (int t = 0; t < kMaxTok; ++t) {
-            float v = s[t];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-            if (threadIdx.x % 64 == 0) red[threadIdx.x / 64][t] = v;
+            const float v = lanes_sum<64>(s[t]);
+            if (t256 % 64 == 0) red[sub][t256 / 64][t] = v;
         }
         __syncthreads();
-        if ((int) threadIdx.x < T)
-            a.logits[(size_t) threadIdx.x * a.NE + r] =
-                (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
+        if (t256 < T && r < a.NE)
+            a.logits[(size_t) t256 * a.NE + r] =
+                (red[sub][0][t256] + red[sub][1][t256]) + (red[sub][2][t256] + red[sub][3][t256]);
         return;
     }
-    // Q8_1 of x: chunk -> (token, 256 columns)
     const int npad = (H + 511) / 512 * 512;
-    const int chunks = npad / 256;
-    const int chunk = blockIdx.x - a.NE;
-    const int t = chunk / chunks, i = (chunk % chunks) * 256 + threadIdx.x;
+    const int chunks = (npad + kK1Threads - 1) / kK1Threads;
+    const int chunk = blockIdx.x - n_router_wg;
+    const int t = chunk / chunks, i = (chunk % chunks) * kK1Threads + threadIdx.x;
     const float v = i < H ? a.x[(size_t) t * H + i] : 0.0f;
-    float amax = fabsf(v), sum = v;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
-        sum += __shfl_xor(sum, o, kWave);
+    const Q8Lane r = q8_1_lane(v);  // whole 32-lane blocks: the lanes past npad form whole blocks and store nothing
+    if (i < npad) {
+        uint8_t *b = a.xq + (size_t) t * a.xq_row_bytes + (size_t) (i / 32) * 36;
+        b[4 + i % 32] = (uint8_t) (int8_t) r.q;
+        if (i % 32 == 0) *(uint32_t *) b = float_to_half(r.d) | (float_to_half(r.sum) << 16);
+        pack_store(a.xpack + (size_t) t * act_lds_bytes(npad), npad, i, r);
     }
-    const float d = amax / 127.0f;
-    uint8_t *b = a.xq + (size_t) t * a.xq_row_bytes + (size_t) (i / 32) * 36;
-    b[4 + i % 32] = (uint8_t) (amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(v / d));
-    if (i % 32 == 0) *(uint32_t *) b = float_to_half(d) | (float_to_half(sum) << 16);
 }
 
-// ---- K2: routing + gate/up + SwiGLU -----------------------------------------------------------------------------
-template <int T_, int LPR, int SPL, int NC>
-__global__ __launch_bounds__(256) void k_gate_up(const LayerArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int s_ids[kMaxTok * 16];
-    __shared__ int s_wave_cnt[4];
-    __shared__ int s_e, s_ncol, s_xrow[kMaxTok], s_orow[kMaxTok];
-    constexpr int SPB = Traits<T_>::slots, BB = Traits<T_>::bytes;
-    constexpr int G = 256 / LPR;
-    constexpr int RPG = LPR >= 32 ? 2 : 1;
-    constexpr int SPLX = SPL > 0 ? SPL : 1;
-    const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
-    const int T = a.T, K = a.K, H = a.H;
-    const int npad = (H + 511) / 512 * 512;
+// ---- K2: routing + gate/up + SwiGLU + Q8_1 of act ------------------------------------------------------------------
+// NT threads per workgroup; LPR lanes per row; rows per workgroup RPB = max(32, NT / LPR) (whole Q8_1 blocks of act).
+template <int NT, int LPR> constexpr int gu_rows_per_group() { return (NT / LPR) >= 32 ? 1 : 32 / (NT / LPR); }
 
-    // 1. stage the Q8_1 rows of all tokens (independent of the routing)
+// LDS of the routing preamble.
+struct RouteLds {
+    int ids[kMaxCh];
+    float p[256], pv[16], wsel[16];
+    int sel[16];
+    int wave_cnt[16];
+    int e, ncol, xrow[kMaxTok], orow[kMaxTok];
+};
+
+// Gating + top-k for every token (workgroup (0, 0) publishes ids, weights and down pointers), then channel
+// blockIdx.y -> expert and its (token, slot) columns: slot order for n_tok = 1, distinct experts ascending for
+// n_tok > 1 (compaction: channel c takes the c-th smallest selected id). Sets rs.e = -1 for an idle channel.
+template <int NT>
+__device__ __forceinline__ void route_channel(const LayerArgs &a, RouteLds &rs) {
+    const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
+    const int T = a.T, K = a.K;
+    const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
     for (int t = 0; t < T; ++t) {
-        uint8_t *base = smem + t * act_lds_bytes(npad);
-        stage_q8_1_row(a.xq + (size_t) t * a.xq_row_bytes, npad / 32, (int8_t *) base, (float *) (base + npad),
-                       (float *) (base + npad) + npad / 32, tid, 256);
+        route_topk_block<NT>(a.logits + (size_t) t * a.NE, a.NE, K, a.gating, a.norm, rs.p, rs.sel, rs.pv, rs.wsel);
+        __syncthreads();
+        if (tid < K) {
+            rs.ids[t * K + tid] = rs.sel[tid];
+            if (pub) {
+                a.ids[t * K + tid] = rs.sel[tid];
+                a.w[t * K + tid] = rs.wsel[tid];
+                a.dptr[t * K + tid] = (const uint8_t *) a.table[rs.sel[tid]] + a.down_off;
+            }
+        }
+        __syncthreads();
     }
-    // 2. routing on wave 0
-    if (wave == 0) {
-        const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
-        for (int t = 0; t < T; ++t)
-            route_topk_wave(a.logits + (size_t) t * a.NE, a.NE, K, a.gating, a.norm, pub ? a.ids + t * K : nullptr,
-                            pub ? a.w + t * K : nullptr, s_ids + t * K);
-    }
-    if (tid == 0) s_e = -1;
+    if (tid == 0) rs.e = -1;
     __syncthreads();
-    // 3. channel -> expert and its (token, slot) columns
     if (T == 1) {
         if (tid == 0) {
-            s_e = s_ids[blockIdx.y];
-            s_ncol = 1;
-            s_xrow[0] = 0;
-            s_orow[0] = blockIdx.y;
+            rs.e = rs.ids[blockIdx.y];
+            rs.ncol = 1;
+            rs.xrow[0] = 0;
+            rs.orow[0] = blockIdx.y;
         }
     } else {
-        bool present = false;
-        if (tid < a.NE)
-            for (int i = 0; i < T * K; ++i) present |= s_ids[i] == tid;
-        const uint64_t m = __ballot(present);
-        if (lane64 == 0) s_wave_cnt[wave] = __popcll(m);
-        __syncthreads();
-        int rank = __popcll(m & ((1ull << lane64) - 1ull));
-        for (int wv = 0; wv < wave; ++wv) rank += s_wave_cnt[wv];
-        if (present && rank == (int) blockIdx.y) {
-            s_e = tid;
-            int n = 0;
-            for (int t = 0; t < T; ++t)
-                for (int j = 0; j < K; ++j)
-                    if (s_ids[t * K + j] == tid) {
-                        s_xrow[n] = t;
-                        s_orow[n] = t * K + j;
-                        ++n;
-                    }
-            s_ncol = n;
+        int base = 0;  // selected experts below e0
+        for (int e0 = 0; e0 < a.NE; e0 += NT) {
+            const int ex = e0 + tid;
+            bool present = false;
+            if (ex < a.NE)
+                for (int i = 0; i < T * K; ++i) present |= rs.ids[i] == ex;
+            const uint64_t m = __ballot(present);
+            if (lane64 == 0) rs.wave_cnt[wave] = __popcll(m);
+            __syncthreads();
+            int rank = base + __popcll(m & ((1ull << lane64) - 1ull));
+            for (int wv = 0; wv < wave; ++wv) rank += rs.wave_cnt[wv];
+            for (int wv = 0; wv < NT / kWave; ++wv) base += rs.wave_cnt[wv];
+            if (present && rank == (int) blockIdx.y) {
+                rs.e = ex;
+                int n = 0;
+                for (int t = 0; t < T; ++t)
+                    for (int j = 0; j < K; ++j)
+                        if (rs.ids[t * K + j] == ex) {
+                            rs.xrow[n] = t;
+                            rs.orow[n] = t * K + j;
+                            ++n;
+                        }
+                rs.ncol = n;
+            }
+            __syncthreads();
         }
     }
     __syncthreads();
-    const int e = s_e;
+}
+
+// SwiGLU epilogue of one row (LPR-lane partial sums) and the Q8_1 of the workgroup's RPB act rows per column.
+template <int LPR, int NC>
+__device__ __forceinline__ void gate_up_epilogue(const LayerArgs &a, const RouteLds &rs, float *s_act, int RPB,
+                                                 int lrow, int row, int lane, const float *acc, const float *accg) {
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+        float v = lanes_sum<LPR>(acc[n]);
+        const float gs = lanes_sum<LPR>(accg[n]);
+        v += 0.0f;  // fused-GLU epilogue with zero biases (reference src/ggml/ggml_mmvq.cu:240-247)
+        v *= silu(gs + 0.0f);
+        if (lane == 0 && (NC == 1 || n < rs.ncol)) {
+            s_act[n * RPB + lrow] = v;
+            a.act[(size_t) rs.orow[n] * a.F + row] = v;
+        }
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void quant_act(const LayerArgs &a, const RouteLds &rs, const float *s_act, int RPB, int rowb) {
+    const int wave = threadIdx.x / kWave, lane64 = threadIdx.x % kWave;
+    const int fpad = (a.F + 511) / 512 * 512;
+    const int fbytes = act_lds_bytes(fpad);
+    const int nqb = RPB / 32, ncol = rs.ncol;
+    for (int p0 = wave * 2; p0 < ncol * nqb; p0 += 2 * (NT / kWave)) {  // uniform per wave: both halves run
+        const int p = p0 + lane64 / 32;
+        const bool live = p < ncol * nqb;
+        const int n = live ? p / nqb : 0, qb = live ? p % nqb : 0;
+        const int i = rowb + qb * 32 + lane64 % 32;  // act column (= gate/up row)
+        const float v = live && i < a.F ? s_act[n * RPB + qb * 32 + lane64 % 32] : 0.0f;
+        const Q8Lane r = q8_1_lane(v);
+        const int c = rs.orow[n];
+        if (live && i < fpad) pack_store(a.apack + (size_t) c * fbytes, fpad, i, r);
+        if (live && i % 32 == 0 && i < fpad) a.blk_amax[(size_t) c * (fpad / 32) + i / 32] = r.d * 127.0f;
+    }
+}
+
+// Register-staged form (any row length): each lane loads whole blocks of its rows straight into VGPRs.
+template <int TQ, int LPR, int BPL, int NC, int NT>
+__global__ __launch_bounds__(NT) void k_gate_up(const LayerArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ RouteLds rs;
+    constexpr int BB = Traits<TQ>::bytes;
+    constexpr int G = NT / LPR;
+    constexpr int RPG = gu_rows_per_group<NT, LPR>();
+    constexpr int RPB = G * RPG;  // rows per workgroup, a multiple of 32
+    constexpr int BPLX = BPL > 0 ? BPL : 1;
+    float *s_act = (float *) smem;  // [NC][RPB]
+    uint8_t *s_x = smem + NC * RPB * 4;
+    const int tid = threadIdx.x;
+    const int T = a.T, H = a.H;
+    const int npad = (H + 511) / 512 * 512;
+    const int xbytes = act_lds_bytes(npad);
+
+    for (int t = 0; t < T; ++t) copy_to_lds(s_x + t * xbytes, a.xpack + (size_t) t * xbytes, xbytes, tid, NT);
+    route_channel<NT>(a, rs);
+    const int e = rs.e;
     if (e < 0) return;  // fewer distinct experts than channels: uniform exit of the whole workgroup
-    const int ncol = s_ncol;
+    const int ncol = rs.ncol;
 
     const uint8_t *slot = (const uint8_t *) a.table[e];
     const uint8_t *wa = slot + a.up_off, *wb = slot + a.gate_off;
-    const int nblk = H / 256, nslots = nblk * SPB;
+    const int nblk = H / 256;
     const int64_t row_bytes = (int64_t) nblk * BB;
     const int lane = tid % LPR, grp = tid / LPR;
-    const int row0 = blockIdx.x * (G * RPG) + grp;
-
-    Frag fa[RPG][SPLX], fb[RPG][SPLX];
-    if constexpr (SPL > 0) {
+    const int rowb = blockIdx.x * RPB;  // inter is a multiple of 256: every row of the workgroup exists
+    BlockRegs<TQ> ru[RPG][BPLX], rg[RPG][BPLX];
+    if constexpr (BPL > 0) {
 #pragma unroll
         for (int r = 0; r < RPG; ++r) {
-            const int row = row0 + r * G;
+            const int row = rowb + r * G + grp;
 #pragma unroll
-            for (int s = 0; s < SPL; ++s) {
-                const int sl = lane + s * LPR;
-                if (row < a.F && sl < nslots) {
-                    slot_load<T_>(wa + row * row_bytes + (int64_t) (sl / SPB) * BB, sl % SPB, fa[r][s]);
-                    slot_load<T_>(wb + row * row_bytes + (int64_t) (sl / SPB) * BB, sl % SPB, fb[r][s]);
+            for (int k = 0; k < BPL; ++k) {
+                const int bb = lane + k * LPR;
+                if (bb < nblk) {
+                    block_load<TQ>(wa + row * row_bytes + (int64_t) bb * BB, ru[r][k]);
+                    block_load<TQ>(wb + row * row_bytes + (int64_t) bb * BB, rg[r][k]);
                 }
             }
         }
     }
-    ActView av[NC];
+    ActImg img[NC];
 #pragma unroll
-    for (int n = 0; n < NC; ++n) {
-        const uint8_t *base = smem + (n < ncol ? s_xrow[n] : 0) * act_lds_bytes(npad);
-        av[n] = ActView{(const int8_t *) base, (const float *) (base + npad), (const float *) (base + npad) + npad / 32};
-    }
-    float acc[RPG][NC], accg[RPG][NC];
-#pragma unroll
-    for (int r = 0; r < RPG; ++r)
-#pragma unroll
-        for (int n = 0; n < NC; ++n) acc[r][n] = accg[r][n] = 0.0f;
+    for (int n = 0; n < NC; ++n) img[n] = act_img(s_x + (n < ncol ? rs.xrow[n] : 0) * xbytes, npad);
+
 #pragma unroll
     for (int r = 0; r < RPG; ++r) {
-        const int row = row0 + r * G;
-        if (row >= a.F) continue;
-        if constexpr (SPL > 0) {
+        const int row = rowb + r * G + grp;
+        float acc[NC], accg[NC];
 #pragma unroll
-            for (int s = 0; s < SPL; ++s) {
-                const int sl = lane + s * LPR;
-                if (sl < nslots) {
+        for (int n = 0; n < NC; ++n) acc[n] = accg[n] = 0.0f;
+        if constexpr (BPL > 0) {
+#pragma unroll
+            for (int k = 0; k < BPL; ++k) {
+                const int bb = lane + k * LPR;
+                if (bb < nblk) {
 #pragma unroll
                     for (int n = 0; n < NC; ++n) {
-                        if (n < ncol) {
-                            acc[r][n] += slot_dot<T_>(fa[r][s], sl % SPB, (sl / SPB) * 256, av[n]);
-                            accg[r][n] += slot_dot<T_>(fb[r][s], sl % SPB, (sl / SPB) * 256, av[n]);
+                        if (NC == 1 || n < ncol) {
+                            acc[n] += block_dot<TQ>(ru[r][k], img[n], bb * 256);
+                            accg[n] += block_dot<TQ>(rg[r][k], img[n], bb * 256);
                         }
                     }
                 }
             }
         } else {
-            for (int sl = lane; sl < nslots; sl += LPR) {
-                Frag f, g;
-                slot_load<T_>(wa + row * row_bytes + (int64_t) (sl / SPB) * BB, sl % SPB, f);
-                slot_load<T_>(wb + row * row_bytes + (int64_t) (sl / SPB) * BB, sl % SPB, g);
+            for (int bb = lane; bb < nblk; bb += LPR) {
+                BlockRegs<TQ> u, g;
+                block_load<TQ>(wa + row * row_bytes + (int64_t) bb * BB, u);
+                block_load<TQ>(wb + row * row_bytes + (int64_t) bb * BB, g);
 #pragma unroll
                 for (int n = 0; n < NC; ++n) {
-                    if (n < ncol) {
-                        acc[r][n] += slot_dot<T_>(f, sl % SPB, (sl / SPB) * 256, av[n]);
-                        accg[r][n] += slot_dot<T_>(g, sl % SPB, (sl / SPB) * 256, av[n]);
+                    if (NC == 1 || n < ncol) {
+                        acc[n] += block_dot<TQ>(u, img[n], bb * 256);
+                        accg[n] += block_dot<TQ>(g, img[n], bb * 256);
                     }
                 }
             }
         }
+        gate_up_epilogue<LPR, NC>(a, rs, s_act, RPB, r * G + grp, row, lane, acc, accg);
     }
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) {
-        const int row = row0 + r * G;
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            float v = group_sum<LPR>(acc[r][n]);
-            const float gs = group_sum<LPR>(accg[r][n]);
-            v += 0.0f;
-            v *= silu(gs + 0.0f);
-            if (lane == 0 && n < ncol && row < a.F) a.act[(size_t) s_orow[n] * a.F + row] = v;
-        }
-    }
+    __syncthreads();
+    quant_act<NT>(a, rs, s_act, RPB, rowb);
 }
 
-// ---- K3: guard + Q8_1 of act, down GEMV, combine --------------------------------------------------------------------
-constexpr int kDownRows = 8;  // output rows per workgroup
+// LDS-staged form (whole rows of both matrices fit in LDS): the workgroup's 32 up rows and 32 gate rows - two
+// contiguous byte ranges - are moved into LDS with coalesced LDS-DMA loads, then each lane takes whole blocks of
+// its row from LDS. Expert slots that are not 16-byte aligned take the register path inside the same kernel.
+constexpr int kGuRows = 32;
 
+template <int TQ, int LPR, int NC, int NT>
+__global__ __launch_bounds__(NT) void k_gate_up_lds(const LayerArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ RouteLds rs;
+    constexpr int BB = Traits<TQ>::bytes;
+    constexpr int G = NT / LPR;
+    static_assert(G == kGuRows, "one row per lane group");
+    float *s_act = (float *) smem;  // [NC][32]
+    uint8_t *s_x = smem + NC * kGuRows * 4;
+    const int tid = threadIdx.x;
+    const int T = a.T, H = a.H;
+    const int npad = (H + 511) / 512 * 512;
+    const int xbytes = act_lds_bytes(npad);
+    uint8_t *s_w = s_x + T * xbytes;  // [up rows | gate rows]
+
+    dma_to_lds<NT>(s_x, a.xpack, T * xbytes);
+    route_channel<NT>(a, rs);
+    const int e = rs.e;
+    if (e < 0) return;
+    const int ncol = rs.ncol;
+
+    const int nblk = H / 256;
+    const int row_bytes = nblk * BB;
+    const int rowb = blockIdx.x * kGuRows;
+    const uint8_t *slot = (const uint8_t *) a.table[e];
+    const uint8_t *wa = slot + a.up_off + (int64_t) rowb * row_bytes;
+    const uint8_t *wb = slot + a.gate_off + (int64_t) rowb * row_bytes;
+    const int region = kGuRows * row_bytes;  // a multiple of 16 (block sizes are even)
+    const bool staged = (((uintptr_t) wa | (uintptr_t) wb) & 15u) == 0;
+    if (staged) {
+        dma_to_lds<NT>(s_w, wa, region);
+        dma_to_lds<NT>(s_w + region, wb, region);
+    }
+    dma_wait();
+    __syncthreads();
+
+    const int lane = tid % LPR, grp = tid / LPR;
+    const int row = rowb + grp;
+    ActImg img[NC];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) img[n] = act_img(s_x + (n < ncol ? rs.xrow[n] : 0) * xbytes, npad);
+    float acc[NC], accg[NC];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) acc[n] = accg[n] = 0.0f;
+    for (int bb = lane; bb < nblk; bb += LPR) {
+        BlockRegs<TQ> u, g;
+        const int off = grp * row_bytes + bb * BB;
+        if (staged) {
+            lds_block_load<TQ>(s_w + off, u);
+            lds_block_load<TQ>(s_w + region + off, g);
+        } else {
+            block_load<TQ>(wa + off, u);
+            block_load<TQ>(wb + off, g);
+        }
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            if (NC == 1 || n < ncol) {
+                acc[n] += block_dot<TQ>(u, img[n], bb * 256);
+                accg[n] += block_dot<TQ>(g, img[n], bb * 256);
+            }
+        }
+    }
+    gate_up_epilogue<LPR, NC>(a, rs, s_act, kGuRows, grp, row, lane, acc, accg);
+    __syncthreads();
+    quant_act<NT>(a, rs, s_act, kGuRows, rowb);
+}
+
+// ---- K3: (guard) + down GEMV + combine -------------------------------------------------------------------------------
 __device__ __forceinline__ float guard_scale(float amax) {
     float e = amax * (1.0f / 1024.0f);
     e = logf(e);
@@ -265,114 +420,122 @@ __device__ __forceinline__ float guard_scale(float amax) {
     return expf(e);
 }
 
-template <int T_, int LPR, int SPL>
+// Items are (output row, channel) pairs; LPR lanes per item, each lane one or more whole blocks of the row.
+template <int TQ, int LPR, int BPL>
 __global__ __launch_bounds__(256) void k_down_combine(const LayerArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int s_ids[kMaxTok * 16];
-    __shared__ float s_w[kMaxTok * 16], s_e[kMaxTok * 16];
-    __shared__ float s_dexp[kMaxTok * 16][kDownRows];
-    constexpr int SPB = Traits<T_>::slots, BB = Traits<T_>::bytes;
+    __shared__ float s_e[kMaxCh], s_w[kMaxCh];
+    __shared__ float s_dexp[kMaxCh][kDownRows];
+    constexpr int BB = Traits<TQ>::bytes;
     constexpr int G = 256 / LPR;
+    constexpr int BPLX = BPL > 0 ? BPL : 1;
     const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
     const int T = a.T, K = a.K, F = a.F, H = a.H;
     const int CH = T * K;
     const int fpad = (F + 511) / 512 * 512;
+    const int fbytes = act_lds_bytes(fpad);
     const int r0 = blockIdx.x * kDownRows;
-
-    if (tid < CH) {
-        s_ids[tid] = a.ids[tid];
-        s_w[tid] = a.w[tid];
-    }
-    // act rows -> (guard) -> Q8_1 in LDS; one wave per row
-    for (int c = wave; c < CH; c += 4) {
-        const float *src = a.act + (size_t) c * F;
-        float m = 0.0f;
-        for (int i = lane64; i < F; i += kWave) m = fmaxf(m, fabsf(src[i]));
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-        const float e = a.guard ? guard_scale(m) : 1.0f;
-        if (lane64 == 0) {
-            s_e[c] = e;
-            if (blockIdx.x == 0 && a.escale) a.escale[c] = e;
-        }
-        uint8_t *base = smem + c * act_lds_bytes(fpad);
-        int8_t *q = (int8_t *) base;
-        float *d = (float *) (base + fpad);
-        float *s16 = d + fpad / 32;
-        for (int i0 = 0; i0 < fpad; i0 += kWave) {
-            const int i = i0 + lane64;
-            const float v = i < F ? (a.guard ? src[i] / e : src[i]) : 0.0f;
-            float amax = fabsf(v), sum = v;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) {
-                amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
-                sum += __shfl_xor(sum, o, kWave);
-            }
-            const float dd = amax / 127.0f;
-            const int qi = amax == 0.0f ? 0 : (int) (int8_t) roundf(v / dd);
-            int qs = qi;
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1) qs += __shfl_xor(qs, o, kWave);
-            const float dh = half_to_float(float_to_half(dd));
-            q[i] = (int8_t) qi;
-            if (i % 32 == 0) d[i / 32] = dh;
-            if (i % 16 == 0) s16[i / 16] = dh * (float) qs;
-        }
-    }
-    __syncthreads();
-
-    // (row, channel) items; a lane group of LPR lanes takes items grp, grp + G, ...
-    const int nblk = F / 256, nslots = nblk * SPB;
+    const int nblk = F / 256;
     const int64_t row_bytes = (int64_t) nblk * BB;
     const int lane = tid % LPR, grp = tid / LPR;
     const int n_items = kDownRows * CH;
-    for (int it0 = grp; it0 < n_items; it0 += 2 * G) {
-        Frag f[2][SPL > 0 ? SPL : 1];
-        int row_[2], ch_[2];
-        bool ok[2];
+
+    BlockRegs<TQ> rb[BPLX];
+    int ch = 0, row = 0;
+    bool ok = false;
+    const uint8_t *wm = nullptr;
+    auto item = [&](int it) {
+        ch = it % CH;
+        row = r0 + it / CH;
+        ok = it < n_items && row < H;
+        wm = ok ? gload<const uint8_t *>((const uint8_t *) (a.dptr + ch)) : nullptr;
+    };
+    auto load_item = [&]() {
+        if constexpr (BPL > 0) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int it = it0 + u * G;
-            ch_[u] = it % CH;
-            row_[u] = r0 + it / CH;
-            ok[u] = it < n_items && row_[u] < H;
-            if constexpr (SPL > 0) {
-                const uint8_t *wm = (const uint8_t *) a.table[s_ids[ok[u] ? ch_[u] : 0]] + a.down_off;
-#pragma unroll
-                for (int s = 0; s < SPL; ++s) {
-                    const int sl = lane + s * LPR;
-                    if (ok[u] && sl < nslots)
-                        slot_load<T_>(wm + row_[u] * row_bytes + (int64_t) (sl / SPB) * BB, sl % SPB, f[u][s]);
-                }
+            for (int k = 0; k < BPL; ++k) {
+                const int bb = lane + k * LPR;
+                if (ok && bb < nblk) block_load<TQ>(wm + row * row_bytes + (int64_t) bb * BB, rb[k]);
             }
         }
+    };
+    // 1. order of issue matters (a wave's loads complete in order): down pointer, then the act images, then the
+    //    weights; the images reach LDS while the weights are still in flight.
+    item(grp);
+    constexpr int kMaxCopy = 4;  // 16-byte pieces per thread held in registers
+    uint4 cp[kMaxCopy];
+    const int n16 = CH * fbytes / 16;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            float acc = 0.0f;
-            const uint8_t *base = smem + (ok[u] ? ch_[u] : 0) * act_lds_bytes(fpad);
-            const ActView av{(const int8_t *) base, (const float *) (base + fpad), (const float *) (base + fpad) + fpad / 32};
-            if (ok[u]) {
-                if constexpr (SPL > 0) {
+    for (int k = 0; k < kMaxCopy; ++k) {
+        const int i = tid + k * 256;
+        if (i < n16) cp[k] = gload<uint4>(a.apack + (size_t) i * 16);
+    }
+    float wv = 0.0f;
+    if (tid < CH) wv = a.w[tid];
+    load_item();
 #pragma unroll
-                    for (int s = 0; s < SPL; ++s) {
-                        const int sl = lane + s * LPR;
-                        if (sl < nslots) acc += slot_dot<T_>(f[u][s], sl % SPB, (sl / SPB) * 256, av);
-                    }
-                } else {
-                    const uint8_t *wm = (const uint8_t *) a.table[s_ids[ch_[u]]] + a.down_off;
-                    for (int sl = lane; sl < nslots; sl += LPR) {
-                        Frag g;
-                        slot_load<T_>(wm + row_[u] * row_bytes + (int64_t) (sl / SPB) * BB, sl % SPB, g);
-                        acc += slot_dot<T_>(g, sl % SPB, (sl / SPB) * 256, av);
-                    }
-                }
-            }
-            acc = group_sum<LPR>(acc);
-            if (lane == 0 && ok[u]) s_dexp[ch_[u]][row_[u] - r0] = acc;
-        }
+    for (int k = 0; k < kMaxCopy; ++k) {
+        const int i = tid + k * 256;
+        if (i < n16) ((uint4 *) smem)[i] = cp[k];
+    }
+    for (int i = tid + kMaxCopy * 256; i < n16; i += 256) ((uint4 *) smem)[i] = gload<uint4>(a.apack + (size_t) i * 16);
+    if (tid < CH) {
+        s_w[tid] = wv;
+        s_e[tid] = 1.0f;
     }
     __syncthreads();
-    // combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + 0) + x_resid
+    // 2. F16 guard: rows whose scale is not 1 are divided and re-quantised (reference src/kernels.cu:554-577)
+    if (a.guard) {
+        for (int c = wave; c < CH; c += 4) {
+            float m = 0.0f;
+            for (int b = lane64; b < fpad / 32; b += kWave) m = fmaxf(m, a.blk_amax[(size_t) c * (fpad / 32) + b]);
+            m = lanes_max<64>(m);
+            const float e = guard_scale(m);
+            if (lane64 == 0) {
+                s_e[c] = e;
+                if (blockIdx.x == 0) a.escale[c] = e;
+            }
+            if (e != 1.0f) {
+                const float *src = a.act + (size_t) c * F;
+                for (int i0 = 0; i0 < fpad; i0 += kWave) {
+                    const int i = i0 + lane64;
+                    const Q8Lane r = q8_1_lane(i < F ? src[i] / e : 0.0f);
+                    pack_store(smem + c * fbytes, fpad, i, r);
+                }
+            }
+        }
+        __syncthreads();
+    } else if (blockIdx.x == 0 && tid < CH) {
+        a.escale[tid] = 1.0f;
+    }
+    // 3. dot products over (row, channel) items
+    for (int it = grp; it < n_items; it += G) {
+        if (it != grp) {
+            item(it);
+            load_item();
+        }
+        float acc = 0.0f;
+        if (ok) {
+            const ActImg img = act_img(smem + ch * fbytes, fpad);
+            if constexpr (BPL > 0) {
+#pragma unroll
+                for (int k = 0; k < BPL; ++k) {
+                    const int bb = lane + k * LPR;
+                    if (bb < nblk) acc += block_dot<TQ>(rb[k], img, bb * 256);
+                }
+            } else {
+                for (int bb = lane; bb < nblk; bb += LPR) {
+                    BlockRegs<TQ> t;
+                    block_load<TQ>(wm + row * row_bytes + (int64_t) bb * BB, t);
+                    acc += block_dot<TQ>(t, img, bb * 256);
+                }
+            }
+        }
+        acc = lanes_sum<LPR>(acc);
+        if (lane == 0 && ok) s_dexp[ch][row - r0] = acc;
+    }
+    __syncthreads();
+    // 4. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + 0) (+ x_resid)
     if (tid < T * kDownRows) {
         const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
         if (r < H) {
@@ -384,47 +547,199 @@ __global__ __launch_bounds__(256) void k_down_combine(const LayerArgs a) {
     }
 }
 
-template <int T_, int LPR, int SPL>
-int launch_gate_up(const LayerArgs &a, hipStream_t st) {
-    constexpr int RPB = (256 / LPR) * (LPR >= 32 ? 2 : 1);
+// LDS-staged form: the down rows [r0, r0 + 8) of every (token, slot) channel - one contiguous byte range per channel -
+// are gathered into LDS with coalesced LDS-DMA loads right after the act images; each lane then takes whole blocks
+// from LDS. Used when the ranges and the images fit in LDS; unaligned expert slots take global loads in place.
+template <int TQ, int LPR>
+__global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float s_e[kMaxCh], s_w[kMaxCh];
+    __shared__ float s_dexp[kMaxCh][kDownRows];
+    __shared__ const uint8_t *s_dp[kMaxCh];
+    constexpr int BB = Traits<TQ>::bytes;
+    constexpr int G = 256 / LPR;
+    const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
+    const int T = a.T, K = a.K, F = a.F, H = a.H;
+    const int CH = T * K;
+    const int fpad = (F + 511) / 512 * 512;
+    const int fbytes = act_lds_bytes(fpad);
+    const int r0 = blockIdx.x * kDownRows;  // hidden is a multiple of 256: all 8 rows exist
+    const int nblk = F / 256;
+    const int row_bytes = nblk * BB;
+    const int region = kDownRows * row_bytes;  // a multiple of 16
+    uint8_t *s_wt = smem + CH * fbytes;
+
+    // 1. down pointers and combine weights (a barrier waits for every outstanding load, so only these go first)
+    if (tid < CH) {
+        s_dp[tid] = gload<const uint8_t *>((const uint8_t *) (a.dptr + tid)) + (int64_t) r0 * row_bytes;
+        s_w[tid] = a.w[tid];
+        s_e[tid] = 1.0f;
+    }
+    __syncthreads();
+    uintptr_t mis = 0;
+    for (int c = 0; c < CH; ++c) mis |= (uintptr_t) s_dp[c];
+    const bool staged = (mis & 15u) == 0;
+    // 2. act images, then the weights: piece o of the flattened [channel][region] image comes from that channel's slot
+    dma_to_lds<256>(smem, a.apack, CH * fbytes);
+    if (staged)
+        dma_gather_to_lds<256>(s_wt, CH * region, [&](int o) { return s_dp[o / region] + o % region; });
+    dma_wait();
+    __syncthreads();
+    // 3. F16 guard: rows whose scale is not 1 are divided and re-quantised (reference src/kernels.cu:554-577)
+    if (a.guard) {
+        for (int c = wave; c < CH; c += 4) {
+            float m = 0.0f;
+            for (int b = lane64; b < fpad / 32; b += kWave) m = fmaxf(m, a.blk_amax[(size_t) c * (fpad / 32) + b]);
+            m = lanes_max<64>(m);
+            const float e = guard_scale(m);
+            if (lane64 == 0) {
+                s_e[c] = e;
+                if (blockIdx.x == 0) a.escale[c] = e;
+            }
+            if (e != 1.0f) {
+                const float *src = a.act + (size_t) c * F;
+                for (int i0 = 0; i0 < fpad; i0 += kWave) {
+                    const int i = i0 + lane64;
+                    const Q8Lane r = q8_1_lane(i < F ? src[i] / e : 0.0f);
+                    pack_store(smem + c * fbytes, fpad, i, r);
+                }
+            }
+        }
+        __syncthreads();
+    } else if (blockIdx.x == 0 && tid < CH) {
+        a.escale[tid] = 1.0f;
+    }
+    // 4. dot products over (row, channel) items
+    const int lane = tid % LPR, grp = tid / LPR;
+    const int n_items = kDownRows * CH;
+    for (int it = grp; it < n_items; it += G) {
+        const int ch = it % CH, rr = it / CH;
+        const ActImg img = act_img(smem + ch * fbytes, fpad);
+        float acc = 0.0f;
+        for (int bb = lane; bb < nblk; bb += LPR) {
+            BlockRegs<TQ> t;
+            const int off = rr * row_bytes + bb * BB;
+            if (staged) lds_block_load<TQ>(s_wt + ch * region + off, t);
+            else block_load<TQ>(s_dp[ch] + off, t);
+            acc += block_dot<TQ>(t, img, bb * 256);
+        }
+        acc = lanes_sum<LPR>(acc);
+        if (lane == 0) s_dexp[ch][rr] = acc;
+    }
+    __syncthreads();
+    // 5. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + 0) (+ x_resid)
+    if (tid < T * kDownRows) {
+        const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
+        float moe = (s_dexp[t * K][rr] * s_e[t * K]) * s_w[t * K];
+        for (int j = 1; j < K; ++j) moe = moe + (s_dexp[t * K + j][rr] * s_e[t * K + j]) * s_w[t * K + j];
+        moe = moe + 0.0f;
+        a.out[(size_t) t * H + r] = a.x_resid ? moe + a.x_resid[(size_t) t * H + r] : moe;
+    }
+}
+
+// LDS bytes of the staged kernels (0 when they do not fit: the register forms run instead).
+constexpr size_t kLdsBudget = 150 * 1024;
+inline size_t gate_up_lds_bytes(int T, int H, int BB, int NC) {
+    const size_t b = (size_t) NC * kGuRows * 4 + (size_t) T * act_lds_bytes((int) host::pad512(H)) +
+                     2 * (size_t) kGuRows * (H / 256) * BB + 16;
+    return b <= kLdsBudget ? b : 0;
+}
+inline size_t down_lds_bytes(int CH, int F, int BB) {
+    const size_t b = (size_t) CH * act_lds_bytes((int) host::pad512(F)) + (size_t) CH * kDownRows * (F / 256) * BB + 16;
+    return b <= kLdsBudget ? b : 0;
+}
+
+// Lanes per row (a power of two, at most 8) and whole blocks per lane (0: runtime loop) for a row of nblk blocks.
+struct BplShape {
+    int lpr, bpl;
+};
+inline BplShape bpl_shape(int nblk) {
+    int lpr = 1;
+    while (lpr < nblk && lpr < 8) lpr *= 2;
+    const int bpl = (nblk + lpr - 1) / lpr;
+    return {lpr, bpl <= 2 ? bpl : 0};
+}
+
+template <int TQ, int LPR, int BPL, int NC, int NT> int launch_gate_up_nt(const LayerArgs &a, hipStream_t st) {
+    constexpr int RPB = (NT / LPR) * gu_rows_per_group<NT, LPR>();
     const int n_chan = a.T == 1 ? a.K : std::min(a.T * a.K, a.NE);
     const dim3 grid((unsigned) ((a.F + RPB - 1) / RPB), (unsigned) n_chan);
     const int npad = (int) host::pad512(a.H);
-    const size_t lds = (size_t) a.T * act_lds_bytes(npad);
-    if (a.T == 1) hipLaunchKernelGGL((k_gate_up<T_, LPR, SPL, 1>), grid, dim3(256), lds, st, a);
-    else hipLaunchKernelGGL((k_gate_up<T_, LPR, SPL, kMaxTok>), grid, dim3(256), lds, st, a);
+    const size_t lds = (size_t) NC * RPB * 4 + (size_t) a.T * act_lds_bytes(npad);
+    if (lds > 64 * 1024) return host::set_error(host::ERR_SHAPE, "moe_layer: hidden too large for LDS staging");
+    hipLaunchKernelGGL((k_gate_up<TQ, LPR, BPL, NC, NT>), grid, dim3(NT), lds, st, a);
     return host::check_launch("moe gate_up");
 }
 
-template <int T_> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
-    const host::Shape s = host::pick_shape(a.H / 256 * Traits<T_>::slots);
-    if (s.lpr == 64 && s.spl == 1) return launch_gate_up<T_, 64, 1>(a, st);
-    if (s.lpr == 64 && s.spl == 2) return launch_gate_up<T_, 64, 2>(a, st);
-    if (s.lpr == 64 && s.spl == 3) return launch_gate_up<T_, 64, 3>(a, st);
-    if (s.lpr == 32) return launch_gate_up<T_, 32, 1>(a, st);
-    if (s.lpr == 16) return launch_gate_up<T_, 16, 1>(a, st);
-    if (s.lpr == 8) return launch_gate_up<T_, 8, 3>(a, st);
-    if (s.lpr == 4) return launch_gate_up<T_, 4, 3>(a, st);
-    return launch_gate_up<T_, 64, 0>(a, st);
+template <int TQ, int LPR, int BPL> int launch_gate_up(const LayerArgs &a, hipStream_t st) {
+    if (a.T == 1) return launch_gate_up_nt<TQ, LPR, BPL, 1, 256>(a, st);
+    return launch_gate_up_nt<TQ, LPR, BPL, kMaxTok, 256>(a, st);
 }
 
-template <int T_, int LPR, int SPL> int launch_down(const LayerArgs &a, hipStream_t st) {
+template <int TQ, int LPR> int launch_gate_up_b(const LayerArgs &a, int bpl, hipStream_t st) {
+    if (bpl == 1) return launch_gate_up<TQ, LPR, 1>(a, st);
+    if (bpl == 2) return launch_gate_up<TQ, LPR, 2>(a, st);
+    return launch_gate_up<TQ, LPR, 0>(a, st);
+}
+
+template <int TQ, int LPR> int launch_gate_up_lds(const LayerArgs &a, size_t lds, hipStream_t st) {
+    const int n_chan = a.T == 1 ? a.K : std::min(a.T * a.K, a.NE);
+    const dim3 grid((unsigned) (a.F / kGuRows), (unsigned) n_chan);
+    if (a.T == 1) hipLaunchKernelGGL((k_gate_up_lds<TQ, LPR, 1, kGuRows * LPR>), grid, dim3(kGuRows * LPR), lds, st, a);
+    else hipLaunchKernelGGL((k_gate_up_lds<TQ, LPR, kMaxTok, kGuRows * LPR>), grid, dim3(kGuRows * LPR), lds, st, a);
+    return host::check_launch("moe gate_up (lds)");
+}
+
+template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
+    const int nblk = a.H / 256;
+    const size_t lds = gate_up_lds_bytes(a.T, a.H, Traits<TQ>::bytes, a.T == 1 ? 1 : kMaxTok);
+    if (lds) {
+        if (nblk <= 2) return launch_gate_up_lds<TQ, 2>(a, lds, st);
+        if (nblk <= 4) return launch_gate_up_lds<TQ, 4>(a, lds, st);
+        return launch_gate_up_lds<TQ, 8>(a, lds, st);
+    }
+    const BplShape s = bpl_shape(nblk);
+    switch (s.lpr) {
+        case 1: return launch_gate_up_b<TQ, 1>(a, s.bpl, st);
+        case 2: return launch_gate_up_b<TQ, 2>(a, s.bpl, st);
+        case 4: return launch_gate_up_b<TQ, 4>(a, s.bpl, st);
+        default: return launch_gate_up_b<TQ, 8>(a, s.bpl, st);
+    }
+}
+
+template <int TQ, int LPR, int BPL> int launch_down(const LayerArgs &a, hipStream_t st) {
     const dim3 grid((unsigned) ((a.H + kDownRows - 1) / kDownRows));
     const size_t lds = (size_t) a.T * a.K * act_lds_bytes((int) host::pad512(a.F));
-    hipLaunchKernelGGL((k_down_combine<T_, LPR, SPL>), grid, dim3(256), lds, st, a);
+    hipLaunchKernelGGL((k_down_combine<TQ, LPR, BPL>), grid, dim3(256), lds, st, a);
     return host::check_launch("moe down_combine");
 }
 
-template <int T_> int dispatch_down(const LayerArgs &a, hipStream_t st) {
-    const host::Shape s = host::pick_shape(a.F / 256 * Traits<T_>::slots);
-    if (s.lpr == 64 && s.spl == 1) return launch_down<T_, 64, 1>(a, st);
-    if (s.lpr == 64 && s.spl == 2) return launch_down<T_, 64, 2>(a, st);
-    if (s.lpr == 64 && s.spl == 3) return launch_down<T_, 64, 3>(a, st);
-    if (s.lpr == 32) return launch_down<T_, 32, 1>(a, st);
-    if (s.lpr == 16) return launch_down<T_, 16, 1>(a, st);
-    if (s.lpr == 8) return launch_down<T_, 8, 3>(a, st);
-    if (s.lpr == 4) return launch_down<T_, 4, 3>(a, st);
-    return launch_down<T_, 64, 0>(a, st);
+template <int TQ, int LPR> int launch_down_b(const LayerArgs &a, int bpl, hipStream_t st) {
+    if (bpl == 1) return launch_down<TQ, LPR, 1>(a, st);
+    if (bpl == 2) return launch_down<TQ, LPR, 2>(a, st);
+    return launch_down<TQ, LPR, 0>(a, st);
+}
+
+template <int TQ, int LPR> int launch_down_lds(const LayerArgs &a, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((k_down_lds<TQ, LPR>), dim3((unsigned) (a.H / kDownRows)), dim3(256), lds, st, a);
+    return host::check_launch("moe down_combine (lds)");
+}
+
+template <int TQ> int dispatch_down(const LayerArgs &a, hipStream_t st) {
+    const int nblk = a.F / 256;
+    const size_t lds = down_lds_bytes(a.T * a.K, a.F, Traits<TQ>::bytes);
+    if (lds) {
+        if (nblk <= 2) return launch_down_lds<TQ, 2>(a, lds, st);
+        if (nblk <= 4) return launch_down_lds<TQ, 4>(a, lds, st);
+        return launch_down_lds<TQ, 8>(a, lds, st);
+    }
+    const BplShape s = bpl_shape(nblk);
+    switch (s.lpr) {
+        case 1: return launch_down_b<TQ, 1>(a, s.bpl, st);
+        case 2: return launch_down_b<TQ, 2>(a, s.bpl, st);
+        case 4: return launch_down_b<TQ, 4>(a, s.bpl, st);
+        default: return launch_down_b<TQ, 8>(a, s.bpl, st);
+    }
 }
 
 int by_type_gate_up(int t, const LayerArgs &a, hipStream_t st) {
@@ -448,26 +763,39 @@ int by_type_down(int t, const LayerArgs &a, hipStream_t st) {
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+constexpr int kSections = 10;
+
+// Byte sizes of the workspace sections: 0 logits, 1 xq, 2 ids, 3 w, 4 act, 5 escale (documented in fns_hip.h),
+// then internal: 6 xpack, 7 apack, 8 blk_amax, 9 dptr.
+void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
+    const size_t hpad = (size_t) host::pad512(L->hidden), fpad = (size_t) host::pad512(L->inter);
+    const size_t ch = (size_t) n_tok * L->k;
+    sizes[0] = (size_t) n_tok * L->n_expert * 4;
+    sizes[1] = (size_t) n_tok * host::q8_1_row_bytes(L->hidden);
+    sizes[2] = ch * 4;
+    sizes[3] = ch * 4;
+    sizes[4] = ch * L->inter * 4;
+    sizes[5] = ch * 4;
+    sizes[6] = (size_t) n_tok * act_lds_bytes((int) hpad);
+    sizes[7] = ch * act_lds_bytes((int) fpad);
+    sizes[8] = ch * (fpad / 32) * 4;
+    sizes[9] = ch * 8;
+}
 
 }  // namespace
 
 namespace impl {
 
-// Workspace sections (byte offsets, 256-aligned): logits, xq, ids, w, act, escale.
 int moe_workspace_layout(const FnsMoeLayer *L, int n_tok, size_t *offsets, size_t *total) {
     if (!L || n_tok < 1 || n_tok > kMaxTok)
         return host::set_error(host::ERR_SHAPE, "moe_layer: 1 <= n_tok <= %d (larger batches use the MMQ path)", kMaxTok);
+    if (L->k < 1 || L->k > 16 || L->hidden <= 0 || L->inter <= 0 || L->n_expert < 1)
+        return host::set_error(host::ERR_SHAPE, "moe_layer: bad shape");
+    size_t sizes[kSections];
+    section_sizes(L, n_tok, sizes);
     size_t off = 0;
-    const size_t sizes[6] = {
-        (size_t) n_tok * L->n_expert * 4,
-        (size_t) n_tok * host::q8_1_row_bytes(L->hidden),
-        (size_t) n_tok * L->k * 4,
-        (size_t) n_tok * L->k * 4,
-        (size_t) n_tok * L->k * L->inter * 4,
-        (size_t) n_tok * L->k * 4,
-    };
-    for (int i = 0; i < 6; ++i) {
-        if (offsets) offsets[i] = off;
+    for (int i = 0; i < kSections; ++i) {
+        if (offsets && i < 6) offsets[i] = off;
         off += align256(sizes[i]);
     }
     if (total) *total = off;
@@ -479,12 +807,12 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
                    size_t ws_bytes, LayerArgs &a) {
     if (!L || !x || !out || !ws || !L->router_w || !L->table)
         return host::set_error(host::ERR_SHAPE, "moe_layer: null argument");
-    size_t off[6], total;
-    FNS_TRY(moe_workspace_layout(L, n_tok, off, &total));
+    size_t total;
+    FNS_TRY(moe_workspace_layout(L, n_tok, nullptr, &total));
     if (ws_bytes < total) return host::set_error(host::ERR_NOMEM, "moe_layer: workspace %zu < %zu bytes", ws_bytes, total);
-    if (L->hidden <= 0 || L->hidden % 256 || L->inter <= 0 || L->inter % 256 || L->hidden > 16384 || L->inter > 16384)
+    if (L->hidden % 256 || L->inter % 256 || L->hidden > 16384 || L->inter > 16384)
         return host::set_error(host::ERR_SHAPE, "moe_layer: hidden and inter must be positive multiples of 256 (<= 16384)");
-    if (L->n_expert < 1 || L->n_expert > 256 || L->k < 1 || L->k > 16 || L->k > L->n_expert)
+    if (L->n_expert > 256 || L->k > L->n_expert)
         return host::set_error(host::ERR_SHAPE, "moe_layer: 1 <= k <= min(16, n_expert), n_expert <= 256");
     if (L->gating != 0 && L->gating != 1) return host::set_error(host::ERR_SHAPE, "moe_layer: bad gating");
     if (L->router_dtype != 0 && L->router_dtype != T_BF16)
@@ -494,7 +822,14 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     const size_t lds_down = (size_t) n_tok * L->k * act_lds_bytes((int) host::pad512(L->inter));
     if (lds_down > 64 * 1024)
         return host::set_error(host::ERR_SHAPE, "moe_layer: n_tok * k * inter too large for the down kernel's LDS");
-    uint8_t *w8 = (uint8_t *) ws;
+    size_t sizes[kSections];
+    section_sizes(L, n_tok, sizes);
+    uint8_t *sec[kSections];
+    size_t off = 0;
+    for (int i = 0; i < kSections; ++i) {
+        sec[i] = (uint8_t *) ws + off;
+        off += align256(sizes[i]);
+    }
     a = LayerArgs{};
     a.H = L->hidden;
     a.F = L->inter;
@@ -513,20 +848,25 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     a.x = x;
     a.x_resid = x_resid;
     a.out = out;
-    a.logits = (float *) (w8 + off[0]);
-    a.xq = w8 + off[1];
+    a.logits = (float *) sec[0];
+    a.xq = sec[1];
+    a.ids = (int32_t *) sec[2];
+    a.w = (float *) sec[3];
+    a.act = (float *) sec[4];
+    a.escale = (float *) sec[5];
+    a.xpack = sec[6];
+    a.apack = sec[7];
+    a.blk_amax = (float *) sec[8];
+    a.dptr = (const uint8_t **) sec[9];
     a.xq_row_bytes = host::q8_1_row_bytes(L->hidden);
-    a.ids = (int32_t *) (w8 + off[2]);
-    a.w = (float *) (w8 + off[3]);
-    a.act = (float *) (w8 + off[4]);
-    a.escale = (float *) (w8 + off[5]);
     return host::OK;
 }
 
 static int launch_stage(const FnsMoeLayer *L, const LayerArgs &a, int stage, hipStream_t st) {
     if (stage == 0) {
-        const int chunks = (int) (host::pad512(L->hidden) / 256);
-        hipLaunchKernelGGL(k_route_quant, dim3((unsigned) (L->n_expert + chunks * a.T)), dim3(256), 0, st, a);
+        const int chunks = (int) ((host::pad512(L->hidden) + kK1Threads - 1) / kK1Threads);
+        const int n_router_wg = (L->n_expert + kK1Rows - 1) / kK1Rows;
+        hipLaunchKernelGGL(k_route_quant, dim3((unsigned) (n_router_wg + chunks * a.T)), dim3(kK1Threads), 0, st, a);
         return host::check_launch("moe route_quant");
     }
     if (stage == 1) return by_type_gate_up(L->gu_type, a, st);

@@ -18,19 +18,12 @@ using namespace fns::dev;
 
 namespace {
 
-// Quantises one value per lane; lanes 32k .. 32k+31 form block (blk0 + k) of the row `y`.
-__device__ __forceinline__ void q8_1_lane(float v, uint8_t *__restrict__ y, int blk, int i32) {
-    float amax = fabsf(v), sum = v;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
-        sum += __shfl_xor(sum, o, kWave);
-    }
-    const float d = amax / 127.0f;
-    const int8_t q = amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(v / d);
+// Quantises one value per lane; lanes 32k .. 32k+31 form block `blk` of the row `y` (reference 36-byte layout).
+__device__ __forceinline__ void q8_1_store(float v, uint8_t *__restrict__ y, int blk, int i32) {
+    const Q8Lane r = q8_1_lane(v);
     uint8_t *b = y + (size_t) blk * 36;
-    b[4 + i32] = (uint8_t) q;
-    if (i32 == 0) *(uint32_t *) b = float_to_half(d) | (float_to_half(sum) << 16);
+    b[4 + i32] = (uint8_t) (int8_t) r.q;
+    if (i32 == 0) *(uint32_t *) b = float_to_half(r.d) | (float_to_half(r.sum) << 16);
 }
 
 __global__ __launch_bounds__(256) void k_quantize_q8_1(const float *__restrict__ x, uint8_t *__restrict__ xq,
@@ -38,7 +31,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(const float *__restrict__
     const int64_t r = blockIdx.y;
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
     const float v = i < ncols ? x[r * ncols + i] : 0.0f;
-    q8_1_lane(v, xq + r * row_bytes, (int) (i / 32), (int) (i % 32));
+    q8_1_store(v, xq + r * row_bytes, (int) (i / 32), (int) (i % 32));
 }
 
 // RMSNorm of one row (any n that is a multiple of 32) then Q8_1 of the result; one workgroup per row.
@@ -49,8 +42,7 @@ __global__ __launch_bounds__(256) void k_rms_norm_q8_1(const float *__restrict__
     const float *xr = x + (size_t) blockIdx.x * n;
     float s = 0.0f;
     for (int i = threadIdx.x; i < n; i += 256) s += xr[i] * xr[i];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, kWave);
+    s = lanes_sum<64>(s);
     if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = s;
     __syncthreads();
     s = (red[0] + red[1]) + (red[2] + red[3]);
@@ -63,7 +55,7 @@ __global__ __launch_bounds__(256) void k_rms_norm_q8_1(const float *__restrict__
             xi = scale * xr[i] * w[i];
             out[(size_t) blockIdx.x * n + i] = xi;
         }
-        q8_1_lane(xi, y, i / 32, i % 32);
+        q8_1_store(xi, y, i / 32, i % 32);
     }
 }
 
@@ -79,8 +71,7 @@ __device__ __forceinline__ float guard_scale(float amax) {
 }
 
 __device__ __forceinline__ float block_max256(float m, float *red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+    m = lanes_max<64>(m);
     __syncthreads();
     if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = m;
     __syncthreads();
@@ -109,7 +100,7 @@ __global__ __launch_bounds__(256) void k_amax_guard_q8_1(const float *__restrict
     uint8_t *y = xq + (size_t) blockIdx.x * row_bytes;
     for (int i = threadIdx.x; i < npad; i += 256) {
         const float xi = i < n ? r[i] / e : 0.0f;
-        q8_1_lane(xi, y, i / 32, i % 32);
+        q8_1_store(xi, y, i / 32, i % 32);
     }
 }
 

@@ -54,9 +54,7 @@ __global__ __launch_bounds__(256) void k_gemv_router(const void *__restrict__ w,
     }
 #pragma unroll
     for (int c = 0; c < COLS; ++c) {
-        float v = s[c];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+        const float v = lanes_sum<64>(s[c]);
         if (threadIdx.x % 64 == 0) red[threadIdx.x / 64][c] = v;
     }
     __syncthreads();

@@ -319,3 +319,10 @@ def quantize_weights(qtype: int, x: torch.Tensor, out: torch.Tensor | None = Non
         out = torch.empty(*x.shape[:-1], row_bytes(qtype, ncols), dtype=torch.uint8, device=x.device)
     call("fns_hip_quantize_weights", qtype, _p(x.contiguous()), _p(out), nrows, ncols, _s())
     return out
+
+
+def selftest_lanes() -> int:
+    """Bit mask of failing cross-lane exchange checks on the device (0 = all good)."""
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    call("fns_hip_selftest_lanes", _p(bad), _s())
+    return int(bad.item())

@@ -139,6 +139,10 @@ int fns_hip_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, f
 /* ggml's reference K-quant quantisers (quantize_row_q{3,4,5,6}_K_ref) on the device: x f32 [nrows][ncols] -> out. */
 int fns_hip_quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, void *stream);
 
+/* Device self-test of the DPP / lane-permute exchanges the kernels use: writes a bit mask of failing checks to
+ * *bad_mask (device int, zero it first); 0 means every exchange matched the LDS-crossbar shuffle. */
+int fns_hip_selftest_lanes(int *bad_mask, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

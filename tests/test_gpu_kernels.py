@@ -40,6 +40,11 @@ def ids_for(n_expert: int) -> np.ndarray:
     return np.array([i % n_expert for i in REF_IDS], dtype=np.int32)
 
 
+def test_lane_exchange_selftest(ops):
+    """The DPP / permlane-swap xor exchanges equal the LDS-crossbar shuffles (all offsets, butterfly sums)."""
+    assert ops.selftest_lanes() == 0
+
+
 # ---- Q8_1 ----------------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("nrows,ncols", [(1, 2048), (8, 768), (3, 100), (2, 512), (1, 32)])
