@@ -8,10 +8,11 @@ from __future__ import annotations
 
 import ctypes
 import re
+import os
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
-LIB_PATH = PKG_DIR / "libfns_hip.so"
+LIB_PATH = Path(os.environ["FNS_HIP_LIB"]) if os.environ.get("FNS_HIP_LIB") else PKG_DIR / "libfns_hip.so"
 HEADER = PKG_DIR.parent / "include" / "fns_hip.h"
 
 

@@ -65,15 +65,39 @@ __device__ __forceinline__ void dma_gather_to_lds(uint8_t *dst, int bytes, F src
                                              (__attribute__((address_space(3))) void *) (dst + p), 16, 0, 0);
     }
 }
+// One wave's LDS DMA of the bytes [begin, end) of src (rounded outward to 16-byte boundaries) to the same offsets of
+// dst; src and dst 16-byte aligned. Pieces that two waves both cover receive the same bytes from each.
+__device__ __forceinline__ void dma_wave(uint8_t *dst, const uint8_t *src, int begin, int end) {
+    const int lane = threadIdx.x % kWave;
+    const int b = begin & ~15, e = (end + 15) & ~15;
+    for (int p = b; p < e; p += 1024) {
+        if (p + lane * 16 < e)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *) (src + p + lane * 16),
+                                             (__attribute__((address_space(3))) void *) (dst + p), 16, 0, 0);
+    }
+}
+// LDS DMA of `bytes` (a multiple of 16) by waves first_wave .. NW-1 of the workgroup (1 KiB per wave instruction).
+template <int NW>
+__device__ __forceinline__ void dma_waves_from(uint8_t *dst, const uint8_t *src, int bytes, int first_wave) {
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (wave < first_wave) return;
+    for (int p = (wave - first_wave) * 1024; p < bytes; p += (NW - first_wave) * 1024) {
+        if (p + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *) (src + p + lane * 16),
+                                             (__attribute__((address_space(3))) void *) (dst + p), 16, 0, 0);
+    }
+}
 // s_waitcnt vmcnt(0) (gfx9 encoding: expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// 16 bytes at a 2-byte-aligned LDS address: two aligned dword windows joined with funnel shifts.
+// 16 bytes at a 2-byte-aligned address (LDS, or global through a generic pointer): aligned dwords joined with funnel
+// shifts; the fifth dword is read only when the address is not 4-byte aligned, so nothing past the 16 bytes' last
+// dword is touched.
 __device__ __forceinline__ uint4 lds16u(const uint8_t *p) {
     const uintptr_t a = (uintptr_t) p;
     const uint32_t *w = (const uint32_t *) (a & ~(uintptr_t) 3);
     const uint32_t sh = (uint32_t) (a & 3u) * 8u;
-    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = sh ? w[4] : 0u;
     return make_uint4(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh),
                       __builtin_amdgcn_alignbit(w3, w2, sh), __builtin_amdgcn_alignbit(w4, w3, sh));
 }
@@ -105,14 +129,24 @@ __device__ __forceinline__ float ubyte_f(uint32_t w, int k) { return (float) ((w
 __device__ __forceinline__ float sbyte_f(uint32_t w, int k) { return (float) (int) (int8_t) ((w >> (8 * k)) & 0xffu); }
 __device__ __forceinline__ float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
-// Activation row image in LDS (npad columns): int8 q | f32 d[npad/32] | f32 s16[npad/16] | f32 s32[npad/32], with
-// s16 / s32 = d * (sum of the quantised values of the 16 / 32 columns).
+// Activation row image (npad columns, a multiple of 512), kept in LDS and copied there verbatim from global memory:
+//   int8 q, 256 columns then 16 bytes of padding per 256 | f32 d[npad/32] | f32 s16[npad/16] | f32 s32[npad/32]
+// with s16 / s32 = d * (sum of the quantised values of the 16 / 32 columns). The padding puts the 256-column blocks of
+// a row on different LDS banks (lanes taking consecutive blocks read 16-byte pieces that would otherwise all map to
+// the same banks), and img_bytes rounds the image to 64 mod 256 bytes so consecutive images are skewed as well.
+constexpr int kImgQRow = 272;
+__host__ __device__ constexpr int img_q_bytes(int npad) { return npad / 256 * kImgQRow; }
+__host__ __device__ constexpr int img_bytes(int npad) {
+    const int b = img_q_bytes(npad) + (npad / 32 + npad / 16 + npad / 32) * 4;
+    return b + ((64 - b % 256) + 256) % 256;
+}
+__host__ __device__ constexpr int img_q_index(int i) { return i + (i >> 8) * (kImgQRow - 256); }
 struct ActImg {
     const int8_t *q;
     const float *d, *s16, *s32;
 };
 __device__ __forceinline__ ActImg act_img(const uint8_t *base, int npad) {
-    const float *d = (const float *) (base + npad);
+    const float *d = (const float *) (base + img_q_bytes(npad));
     return ActImg{(const int8_t *) base, d, d + npad / 32, d + npad / 32 + npad / 16};
 }
 
@@ -121,6 +155,7 @@ template <int T> __device__ __forceinline__ float block_dot(const BlockRegs<T> &
 constexpr uint32_t kLo4 = 0x0F0F0F0Fu;
 
 template <> __device__ __forceinline__ float block_dot<T_Q4_K>(const BlockRegs<T_Q4_K> &b, const ActImg &x, int col0) {
+    const int8_t *qb = x.q + (col0 >> 8) * kImgQRow;
     const uint4 h = b.v[0];
     const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
     const uint32_t sc_hi = (h.w & kLo4) | ((h.y >> 2) & 0x30303030u);
@@ -131,8 +166,8 @@ template <> __device__ __forceinline__ float block_dot<T_Q4_K>(const BlockRegs<T
         const uint4 q0 = b.v[1 + 2 * g], q1 = b.v[2 + 2 * g];  // qs[32g .. 32g+31]
         const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         const int c = col0 + 64 * g;
-        const int4 a0 = *(const int4 *) (x.q + c), a1 = *(const int4 *) (x.q + c + 16);
-        const int4 e0 = *(const int4 *) (x.q + c + 32), e1 = *(const int4 *) (x.q + c + 48);
+        const int4 a0 = *(const int4 *) (qb + (c - col0)), a1 = *(const int4 *) (qb + (c - col0) + 16);
+        const int4 e0 = *(const int4 *) (qb + (c - col0) + 32), e1 = *(const int4 *) (qb + (c - col0) + 48);
         const int a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
         const int e[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
         int dl = 0, dh = 0;
@@ -153,6 +188,7 @@ template <> __device__ __forceinline__ float block_dot<T_Q4_K>(const BlockRegs<T
 }
 
 template <> __device__ __forceinline__ float block_dot<T_Q5_K>(const BlockRegs<T_Q5_K> &b, const ActImg &x, int col0) {
+    const int8_t *qb = x.q + (col0 >> 8) * kImgQRow;
     const uint4 h = b.v[0];
     const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
     const uint32_t sc_hi = (h.w & kLo4) | ((h.y >> 2) & 0x30303030u);
@@ -164,8 +200,8 @@ template <> __device__ __forceinline__ float block_dot<T_Q5_K>(const BlockRegs<T
         const uint4 q0 = b.v[3 + 2 * g], q1 = b.v[4 + 2 * g];
         const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         const int c = col0 + 64 * g;
-        const int4 a0 = *(const int4 *) (x.q + c), a1 = *(const int4 *) (x.q + c + 16);
-        const int4 e0 = *(const int4 *) (x.q + c + 32), e1 = *(const int4 *) (x.q + c + 48);
+        const int4 a0 = *(const int4 *) (qb + (c - col0)), a1 = *(const int4 *) (qb + (c - col0) + 16);
+        const int4 e0 = *(const int4 *) (qb + (c - col0) + 32), e1 = *(const int4 *) (qb + (c - col0) + 48);
         const int a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
         const int e[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
         int dl = 0, dh = 0;
@@ -194,6 +230,7 @@ __device__ __forceinline__ float group_term(int dotu, float d8, float s16, float
 }
 
 template <> __device__ __forceinline__ float block_dot<T_Q6_K>(const BlockRegs<T_Q6_K> &b, const ActImg &x, int col0) {
+    const int8_t *qb = x.q + (col0 >> 8) * kImgQRow;
     const uint4 sc = b.v[12];  // int8 scales[16]
     float sum = 0.0f;
 #pragma unroll
@@ -209,7 +246,7 @@ template <> __device__ __forceinline__ float block_dot<T_Q6_K>(const BlockRegs<T
 #pragma unroll
             for (int half = 0; half < 2; ++half) {  // l in [16 half, 16 half + 16)
                 const int c = col0 + 128 * n + 32 * kind + 16 * half;
-                const int4 a = *(const int4 *) (x.q + c);
+                const int4 a = *(const int4 *) (qb + (c - col0));
                 const int av[4] = {a.x, a.y, a.z, a.w};
                 int du = 0;
 #pragma unroll
@@ -232,6 +269,7 @@ template <> __device__ __forceinline__ float block_dot<T_Q6_K>(const BlockRegs<T
 }
 
 template <> __device__ __forceinline__ float block_dot<T_Q3_K>(const BlockRegs<T_Q3_K> &b, const ActImg &x, int col0) {
+    const int8_t *qb = x.q + (col0 >> 8) * kImgQRow;
     const uint4 t = b.tail;
     // scale bytes 0..11 start at byte 2 of the tail: realign to words S0 (scales 0-3), S1 (4-7), S2 (8-11)
     const uint32_t S0 = __builtin_amdgcn_alignbit(t.y, t.x, 16), S1 = __builtin_amdgcn_alignbit(t.z, t.y, 16);
@@ -252,7 +290,7 @@ template <> __device__ __forceinline__ float block_dot<T_Q3_K>(const BlockRegs<T
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
                 const int c = col0 + 128 * n + 32 * j + 16 * half;
-                const int4 a = *(const int4 *) (x.q + c);
+                const int4 a = *(const int4 *) (qb + (c - col0));
                 const int av[4] = {a.x, a.y, a.z, a.w};
                 int du = 0;
 #pragma unroll

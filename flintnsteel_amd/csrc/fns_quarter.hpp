@@ -1,0 +1,216 @@
+// fns_quarter.hpp - dot product of one quarter of a 256-value K-quant block (64 consecutive values) with a Q8_1
+// activation row image (fns_block.hpp layout). Quarters let 32 lanes share one row of a 2048-wide matrix (8 blocks x 4
+// quarters), so each lane runs a short dependency chain and many waves share a SIMD; a lane reads only the bytes its
+// quarter needs (header + 32 of the 128 qs bytes for Q4_K, for example).
+//   Q4_K / Q5_K quarter g: sub-blocks 2g (low nibbles of qs[32g..32g+31]) and 2g+1 (high nibbles), each
+//                          d * sc * d8 * (q . a) - dmin * m * (d8 * sum a)
+//   Q6_K quarter 2n+h    : values 128n + 64h .. +63: ql[64n..64n+63] nibble h, qh[32n..32n+31] bit pairs 2h, 2h+1;
+//                          d * sum_g sc_g * (d8 * (u . a) - 32 * d8 * sum a) over its four 16-value groups
+//   Q3_K quarter 2n+h    : values 128n + 64h .. +63: qs[32n..32n+31] bit pairs 2j (j = 2h, 2h+1), hmask bit 4n+j;
+//                          d * sum_g (sc_g - 32) * (d8 * (u . a) - 4 * d8 * sum a)
+// The integer products are exact (v_dot4 on int8 lanes); the zero points (32 for Q6_K, 4 for Q3_K) are folded into
+// the activation sums, as in block_dot.
+#pragma once
+
+#include "fns_block.hpp"
+
+namespace fns::dev {
+
+// Loader policies: Aligned16 for 16-byte-aligned LDS data, Any2 for 2-byte-aligned data (LDS or global, generic).
+struct Aligned16 {
+    static __device__ __forceinline__ uint4 ld(const uint8_t *p) { return *(const uint4 *) p; }
+};
+struct Any2 {
+    static __device__ __forceinline__ uint4 ld(const uint8_t *p) { return lds16u(p); }
+};
+// 4 bytes at a 2-byte-aligned address.
+__device__ __forceinline__ uint32_t ld32u(const uint8_t *p) {
+    const uintptr_t a = (uintptr_t) p;
+    const uint32_t *w = (const uint32_t *) (a & ~(uintptr_t) 3);
+    const uint32_t sh = (uint32_t) (a & 3u) * 8u;
+    const uint32_t w0 = w[0], w1 = sh ? w[1] : 0u;
+    return __builtin_amdgcn_alignbit(w1, w0, sh);
+}
+
+// 64 activation bytes of quarter qt of block bb, as 16 dwords.
+__device__ __forceinline__ void act_quarter(const ActImg &x, int bb, int qt, int a[16]) {
+    const int8_t *p = x.q + bb * kImgQRow + 64 * qt;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int4 v = *(const int4 *) (p + 16 * i);
+        a[4 * i] = v.x;
+        a[4 * i + 1] = v.y;
+        a[4 * i + 2] = v.z;
+        a[4 * i + 3] = v.w;
+    }
+}
+
+template <int T, class L> __device__ __forceinline__ float quarter_dot(const uint8_t *blk, const ActImg &x, int bb, int qt);
+
+// Q4_K / Q5_K share the header decoding: 6-bit scale and min of sub-blocks 2qt, 2qt+1 (bytes k0, k0+1 of the words).
+__device__ __forceinline__ void k4_scales(const uint4 &h, int qt, uint32_t &scw, uint32_t &mw) {
+    const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (h.w & kLo4) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((h.w >> 4) & kLo4) | ((h.z >> 2) & 0x30303030u);
+    scw = qt < 2 ? sc_lo : sc_hi;
+    mw = qt < 2 ? m_lo : m_hi;
+}
+__device__ __forceinline__ float ubyte_dyn(uint32_t w, int k) { return (float) ((w >> (8 * k)) & 0xffu); }
+
+__device__ __forceinline__ float k4_finish(const uint4 &h, const ActImg &x, int bb, int qt, int dl, int dh) {
+    uint32_t scw, mw;
+    k4_scales(h, qt, scw, mw);
+    const int k0 = 2 * (qt & 1);
+    const int b32 = bb * 8 + 2 * qt;
+    float sumd = ubyte_dyn(scw, k0) * x.d[b32] * (float) dl;
+    sumd = fmaf_(ubyte_dyn(scw, k0 + 1) * x.d[b32 + 1], (float) dh, sumd);
+    float summ = ubyte_dyn(mw, k0) * x.s32[b32];
+    summ = fmaf_(ubyte_dyn(mw, k0 + 1), x.s32[b32 + 1], summ);
+    return half_to_float(h.x & 0xffffu) * sumd - half_to_float(h.x >> 16) * summ;
+}
+
+template <> __device__ __forceinline__ float quarter_dot<T_Q4_K, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                            int qt) {
+    const uint4 h = Aligned16::ld(blk);
+    const uint4 q0 = Aligned16::ld(blk + 16 + 32 * qt), q1 = Aligned16::ld(blk + 32 + 32 * qt);
+    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    int a[16];
+    act_quarter(x, bb, qt, a);
+    int dl = 0, dh = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        dl = dot4((int) (q[i] & kLo4), a[i], dl);
+        dh = dot4((int) ((q[i] >> 4) & kLo4), a[8 + i], dh);
+    }
+    return k4_finish(h, x, bb, qt, dl, dh);
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q4_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                       int qt) {
+    const uint4 h = Any2::ld(blk);
+    const uint4 q0 = Any2::ld(blk + 16 + 32 * qt), q1 = Any2::ld(blk + 32 + 32 * qt);
+    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    int a[16];
+    act_quarter(x, bb, qt, a);
+    int dl = 0, dh = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        dl = dot4((int) (q[i] & kLo4), a[i], dl);
+        dh = dot4((int) ((q[i] >> 4) & kLo4), a[8 + i], dh);
+    }
+    return k4_finish(h, x, bb, qt, dl, dh);
+}
+
+template <class L> __device__ __forceinline__ float q5k_quarter(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+    const uint4 h = L::ld(blk);
+    const uint4 h0 = L::ld(blk + 16), h1 = L::ld(blk + 32);
+    const uint4 q0 = L::ld(blk + 48 + 32 * qt), q1 = L::ld(blk + 64 + 32 * qt);
+    const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    int a[16];
+    act_quarter(x, bb, qt, a);
+    int dl = 0, dh = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        // fifth bit: qh bit 2qt (low values) and 2qt+1 (high values), moved to bit 4 of each byte
+        const uint32_t bl = ((qh[i] >> (2 * qt)) & 0x01010101u) << 4;
+        const uint32_t bh = ((qh[i] >> (2 * qt + 1)) & 0x01010101u) << 4;
+        dl = dot4((int) ((q[i] & kLo4) | bl), a[i], dl);
+        dh = dot4((int) (((q[i] >> 4) & kLo4) | bh), a[8 + i], dh);
+    }
+    return k4_finish(h, x, bb, qt, dl, dh);
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q5_K, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                            int qt) {
+    return q5k_quarter<Aligned16>(blk, x, bb, qt);
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q5_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                       int qt) {
+    return q5k_quarter<Any2>(blk, x, bb, qt);
+}
+
+// Q6_K and Q3_K blocks are only 2-byte aligned: both policies read through Any2.
+__device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+    const int n = qt >> 1, hh = qt & 1;
+    const uint4 A0 = lds16u(blk + 64 * n), A1 = lds16u(blk + 64 * n + 16);       // ql[64n .. 64n+31]
+    const uint4 B0 = lds16u(blk + 64 * n + 32), B1 = lds16u(blk + 64 * n + 48);  // ql[64n+32 .. 64n+63]
+    const uint4 Q0 = lds16u(blk + 128 + 32 * n), Q1 = lds16u(blk + 144 + 32 * n);  // qh[32n .. 32n+31]
+    const uint32_t scw = ld32u(blk + 192 + 4 * qt);  // int8 scales of groups 4qt .. 4qt+3
+    const uint32_t dbits = ld32u(blk + 208) & 0xffffu;
+    const uint32_t A[8] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w};
+    const uint32_t B[8] = {B0.x, B0.y, B0.z, B0.w, B1.x, B1.y, B1.z, B1.w};
+    const uint32_t Q[8] = {Q0.x, Q0.y, Q0.z, Q0.w, Q1.x, Q1.y, Q1.z, Q1.w};
+    int a[16];
+    act_quarter(x, bb, qt, a);
+    const int sh = 4 * hh;
+    int du[4] = {0, 0, 0, 0};  // groups: A half 0, A half 1, B half 0, B half 1
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t qh = Q[i] >> sh;
+        const uint32_t ua = ((A[i] >> sh) & kLo4) | ((qh << 4) & 0x30303030u);
+        const uint32_t ub = ((B[i] >> sh) & kLo4) | ((qh << 2) & 0x30303030u);
+        du[i >> 2] = dot4((int) ua, a[i], du[i >> 2]);
+        du[2 + (i >> 2)] = dot4((int) ub, a[8 + i], du[2 + (i >> 2)]);
+    }
+    const int c0 = bb * 256 + 64 * qt;
+    float sum = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int c = c0 + 16 * g;
+        sum = fmaf_(sbyte_f(scw, g), group_term(du[g], x.d[c >> 5], x.s16[c >> 4], 32.0f), sum);
+    }
+    return half_to_float(dbits) * sum;
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q6_K, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                            int qt) {
+    return q6k_quarter(blk, x, bb, qt);
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q6_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                       int qt) {
+    return q6k_quarter(blk, x, bb, qt);
+}
+
+__device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+    const int n = qt >> 1, hh = qt & 1;
+    const uint4 H0 = lds16u(blk), H1 = lds16u(blk + 16);                          // hmask[0 .. 31]
+    const uint4 q0 = lds16u(blk + 32 + 32 * n), q1 = lds16u(blk + 48 + 32 * n);  // qs[32n .. 32n+31]
+    const uint4 t = lds16u(blk + 94);                                             // scales at +2, d at +14
+    const uint32_t HM[8] = {H0.x, H0.y, H0.z, H0.w, H1.x, H1.y, H1.z, H1.w};
+    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const uint32_t S0 = __builtin_amdgcn_alignbit(t.y, t.x, 16), S1 = __builtin_amdgcn_alignbit(t.z, t.y, 16);
+    const uint32_t S2 = __builtin_amdgcn_alignbit(t.w, t.z, 16);
+    // scales of groups 4qt .. 4qt+3: low nibbles from S0 (qt even) or S1 (qt odd), shifted by 4 for qt >= 2; top two
+    // bits from S2 at bit pair qt of each byte
+    const uint32_t lo = ((hh ? S1 : S0) >> (4 * n)) & kLo4;
+    const uint32_t hi = (uint32_t) ((((uint64_t) S2) << 4) >> (2 * qt)) & 0x30303030u;
+    const uint32_t scw = lo | hi;
+    int a[16];
+    act_quarter(x, bb, qt, a);
+    int du[4] = {0, 0, 0, 0};  // groups: j0 half 0, j0 half 1, j1 half 0, j1 half 1 (j0 = 2hh, j1 = 2hh + 1)
+    const int j0 = 2 * hh;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t hm = HM[i] >> (4 * n + j0);
+        const uint32_t u0 = ((q[i] >> (2 * j0)) & 0x03030303u) | ((hm << 2) & 0x04040404u);
+        const uint32_t u1 = ((q[i] >> (2 * j0 + 2)) & 0x03030303u) | ((hm << 1) & 0x04040404u);
+        du[i >> 2] = dot4((int) u0, a[i], du[i >> 2]);
+        du[2 + (i >> 2)] = dot4((int) u1, a[8 + i], du[2 + (i >> 2)]);
+    }
+    const int c0 = bb * 256 + 64 * qt;
+    float sum = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int c = c0 + 16 * g;
+        sum = fmaf_(ubyte_dyn(scw, g) - 32.0f, group_term(du[g], x.d[c >> 5], x.s16[c >> 4], 4.0f), sum);
+    }
+    return half_to_float(t.w >> 16) * sum;
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q3_K, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                            int qt) {
+    return q3k_quarter(blk, x, bb, qt);
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q3_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                       int qt) {
+    return q3k_quarter(blk, x, bb, qt);
+}
+
+}  // namespace fns::dev

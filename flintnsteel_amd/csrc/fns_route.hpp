@@ -87,19 +87,21 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ lg, in
     }
 }
 
-// Gating + top-k + renormalisation for one token by a whole workgroup of NT threads (n_expert <= 256): wave 0
-// computes the probabilities exactly as route_topk_wave (same fp32 operations, so the same bits) into s_p (256
-// entries, -inf past n_expert), then four threads per expert each count, over a contiguous quarter of the experts
-// (float4 LDS reads), how many rank above it (higher p, or equal p and lower index); the expert with rank r < k goes to
-// slot r. Equivalent to k rounds of argmax with ties to the lower index, with no dependent cross-lane chain.
-// Must be called by every thread of the workgroup (it contains barriers). Results: sel[0..k), w[0..k) in LDS.
+// Gating + top-k + renormalisation for one token by a whole workgroup of NT threads (n_expert <= 256). Wave 0
+// computes the probabilities exactly as route_topk_wave (same fp32 operations, so the same bits) and stores for
+// each expert the 64-bit key (bits(p) << 32) | ~e: p >= 0, so the keys order as (p descending, index ascending) and
+// are all distinct. Then eight threads per expert each count the keys above the expert's own over one eighth of the
+// experts; the expert with rank r < k goes to slot r - the same result as k rounds of argmax with ties to the lower
+// index, without a dependent cross-lane chain. Must be called by every thread of the workgroup (it contains
+// barriers). Results: sel[0..k), w[0..k) in LDS.
 template <int NT>
 __device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, int n_expert, int k, int gating, int norm,
-                                                 float *s_p, int *sel, float *pv, float *w) {
-    constexpr int P = 4;               // threads per expert
-    constexpr int EPP = NT / P;        // experts per pass
+                                                 uint64_t *s_key, int *sel, float *pv, float *w) {
+    constexpr int P = 8;         // threads per expert
+    constexpr int EPP = NT / P;  // experts per pass
     const int tid = threadIdx.x, lane = tid % kWave;
     if (tid < kWave) {
+        float p[4];
         if (gating == 0) {
             float v[4], m = -__builtin_inff();
 #pragma unroll
@@ -118,37 +120,38 @@ __device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, i
             s = lanes_sum<64>(s);
             const float inv = 1.0f / s;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) s_p[lane + 64 * j] = lane + 64 * j < n_expert ? ev[j] * inv : -__builtin_inff();
+            for (int j = 0; j < 4; ++j) p[j] = ev[j] * inv;
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int e = lane + 64 * j;
-                s_p[e] = e < n_expert ? 1.0f / (1.0f + fns_expf(-lg[e])) : -__builtin_inff();
+                p[j] = e < n_expert ? 1.0f / (1.0f + fns_expf(-lg[e])) : 0.0f;
             }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            s_key[e] = e < n_expert ? ((uint64_t) __builtin_bit_cast(uint32_t, p[j]) << 32) | (uint32_t) ~e : 0ull;
         }
     }
     __syncthreads();
-    const int quarter = ((n_expert + 4 * P - 1) / (4 * P)) * 4;  // experts per part, multiple of 4
     const int part = tid % P;
+    const int kpl = ((n_expert + 2 * P - 1) / (2 * P)) * 2;  // keys per thread, even (16-byte reads)
     for (int e0 = 0; e0 < n_expert; e0 += EPP) {
         const int e = e0 + tid / P;
-        const float pe = e < n_expert ? s_p[e] : -__builtin_inff();
+        const uint64_t ke = s_key[e < 256 ? e : 255];
         int rank = 0;
-        const int j0 = part * quarter;
-        for (int jj = 0; jj < quarter; jj += 4) {
-            const int j = j0 + jj;
-            if (j < 256) {
-                const float4 p4 = *(const float4 *) (s_p + j);
-                rank += (p4.x > pe || (p4.x == pe && j < e)) ? 1 : 0;
-                rank += (p4.y > pe || (p4.y == pe && j + 1 < e)) ? 1 : 0;
-                rank += (p4.z > pe || (p4.z == pe && j + 2 < e)) ? 1 : 0;
-                rank += (p4.w > pe || (p4.w == pe && j + 3 < e)) ? 1 : 0;
-            }
+        const uint64_t *kp = s_key + part * kpl;
+#pragma unroll 4
+        for (int i = 0; i < kpl; i += 2) {
+            const ulonglong2 kk = *(const ulonglong2 *) (kp + i);
+            rank += kk.x > ke ? 1 : 0;
+            rank += kk.y > ke ? 1 : 0;
         }
         rank = lanes_sum_i<P>(rank);
         if (e < n_expert && part == 0 && rank < k) {
             sel[rank] = e;
-            pv[rank] = pe;
+            pv[rank] = __builtin_bit_cast(float, (uint32_t) (ke >> 32));
         }
     }
     __syncthreads();

@@ -25,11 +25,26 @@
 #include "fns_host.hpp"
 #include "fns_internal.hpp"
 #include "fns_lanes.hpp"
+#include "fns_quarter.hpp"
 #include "fns_route.hpp"
 
 namespace fns {
 
 using namespace fns::dev;
+
+// Phase timestamps for tuning builds (-DFNS_PROBE): FNS_MARK(kernel, workgroup, point) records the 100 MHz wall clock.
+#ifdef FNS_PROBE
+__device__ unsigned long long g_probe[3][4096][6];
+#define FNS_MARK(k, wg, i) \
+    do { \
+        if (threadIdx.x == 0) g_probe[k][wg][i] = wall_clock64(); \
+    } while (0)
+#else
+#define FNS_MARK(k, wg, i) \
+    do { \
+        (void) (wg); \
+    } while (0)
+#endif
 
 namespace {
 
@@ -54,8 +69,8 @@ struct LayerArgs {
     float *w;             // [T][K]
     float *act;           // [T*K][F]
     float *escale;        // [T*K]
-    uint8_t *xpack;       // [T][act_lds_bytes(Hpad)]   Q8_1 of x, LDS image
-    uint8_t *apack;       // [T*K][act_lds_bytes(Fpad)] Q8_1 of act, LDS image
+    uint8_t *xpack;       // [T][img_bytes(Hpad)]   Q8_1 of x, LDS image
+    uint8_t *apack;       // [T*K][img_bytes(Fpad)] Q8_1 of act, LDS image
     float *blk_amax;      // [T*K][Fpad / 32]
     const uint8_t **dptr; // [T*K] down matrix of each (token, slot)
     int64_t xq_row_bytes;
@@ -68,16 +83,12 @@ __device__ __forceinline__ void copy_to_lds(uint8_t *dst, const uint8_t *__restr
     for (int i = tid; i < bytes / 16; i += nt) ((uint4 *) dst)[i] = ((const uint4 *) src)[i];
 }
 
-__device__ __forceinline__ ActView view_of(const uint8_t *base, int npad) {
-    return ActView{(const int8_t *) base, (const float *) (base + npad), (const float *) (base + npad) + npad / 32};
-}
-
 // Writes one lane's Q8_1 value into the LDS-image row `pack` (npad columns) at column i; lanes of one block agree
 // on d and the sums.
 __device__ __forceinline__ void pack_store(uint8_t *pack, int npad, int i, const Q8Lane &r) {
     const float dh = half_to_float(float_to_half(r.d));
-    float *d = (float *) (pack + npad);
-    pack[i] = (uint8_t) (int8_t) r.q;
+    float *d = (float *) (pack + img_q_bytes(npad));
+    pack[img_q_index(i)] = (uint8_t) (int8_t) r.q;
     if (i % 32 == 0) d[i / 32] = dh;
     if (i % 16 == 0) d[npad / 32 + i / 16] = dh * (float) r.qsum16;
     if (i % 32 == 0) d[npad / 32 + npad / 16 + i / 32] = dh * (float) r.qsum32;
@@ -92,6 +103,7 @@ __global__ __launch_bounds__(1024) void k_route_quant(const LayerArgs a) {
     __shared__ float red[kK1Rows][4][kMaxTok];
     const int H = a.H, T = a.T;
     const int n_router_wg = (a.NE + kK1Rows - 1) / kK1Rows;
+    FNS_MARK(0, blockIdx.x, 0);
     if ((int) blockIdx.x < n_router_wg) {
         const int sub = threadIdx.x / 256, t256 = threadIdx.x % 256;
         const int r = blockIdx.x * kK1Rows + sub;
@@ -123,6 +135,7 @@ __global__ __launch_bounds__(1024) void k_route_quant(const LayerArgs a) {
         if (t256 < T && r < a.NE)
             a.logits[(size_t) t256 * a.NE + r] =
                 (red[sub][0][t256] + red[sub][1][t256]) + (red[sub][2][t256] + red[sub][3][t256]);
+        FNS_MARK(0, blockIdx.x, 3);
         return;
     }
     const int npad = (H + 511) / 512 * 512;
@@ -135,7 +148,7 @@ __global__ __launch_bounds__(1024) void k_route_quant(const LayerArgs a) {
         uint8_t *b = a.xq + (size_t) t * a.xq_row_bytes + (size_t) (i / 32) * 36;
         b[4 + i % 32] = (uint8_t) (int8_t) r.q;
         if (i % 32 == 0) *(uint32_t *) b = float_to_half(r.d) | (float_to_half(r.sum) << 16);
-        pack_store(a.xpack + (size_t) t * act_lds_bytes(npad), npad, i, r);
+        pack_store(a.xpack + (size_t) t * img_bytes(npad), npad, i, r);
     }
 }
 
@@ -144,9 +157,10 @@ __global__ __launch_bounds__(1024) void k_route_quant(const LayerArgs a) {
 template <int NT, int LPR> constexpr int gu_rows_per_group() { return (NT / LPR) >= 32 ? 1 : 32 / (NT / LPR); }
 
 // LDS of the routing preamble.
-struct RouteLds {
+struct alignas(16) RouteLds {
+    uint64_t key[256];
     int ids[kMaxCh];
-    float p[256], pv[16], wsel[16];
+    float pv[16], wsel[16];
     int sel[16];
     int wave_cnt[16];
     int e, ncol, xrow[kMaxTok], orow[kMaxTok];
@@ -161,7 +175,7 @@ __device__ __forceinline__ void route_channel(const LayerArgs &a, RouteLds &rs) 
     const int T = a.T, K = a.K;
     const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
     for (int t = 0; t < T; ++t) {
-        route_topk_block<NT>(a.logits + (size_t) t * a.NE, a.NE, K, a.gating, a.norm, rs.p, rs.sel, rs.pv, rs.wsel);
+        route_topk_block<NT>(a.logits + (size_t) t * a.NE, a.NE, K, a.gating, a.norm, rs.key, rs.sel, rs.pv, rs.wsel);
         __syncthreads();
         if (tid < K) {
             rs.ids[t * K + tid] = rs.sel[tid];
@@ -234,7 +248,7 @@ template <int NT>
 __device__ __forceinline__ void quant_act(const LayerArgs &a, const RouteLds &rs, const float *s_act, int RPB, int rowb) {
     const int wave = threadIdx.x / kWave, lane64 = threadIdx.x % kWave;
     const int fpad = (a.F + 511) / 512 * 512;
-    const int fbytes = act_lds_bytes(fpad);
+    const int fbytes = img_bytes(fpad);
     const int nqb = RPB / 32, ncol = rs.ncol;
     for (int p0 = wave * 2; p0 < ncol * nqb; p0 += 2 * (NT / kWave)) {  // uniform per wave: both halves run
         const int p = p0 + lane64 / 32;
@@ -264,7 +278,7 @@ __global__ __launch_bounds__(NT) void k_gate_up(const LayerArgs a) {
     const int tid = threadIdx.x;
     const int T = a.T, H = a.H;
     const int npad = (H + 511) / 512 * 512;
-    const int xbytes = act_lds_bytes(npad);
+    const int xbytes = img_bytes(npad);
 
     for (int t = 0; t < T; ++t) copy_to_lds(s_x + t * xbytes, a.xpack + (size_t) t * xbytes, xbytes, tid, NT);
     route_channel<NT>(a, rs);
@@ -354,11 +368,14 @@ __global__ __launch_bounds__(NT) void k_gate_up_lds(const LayerArgs a) {
     const int tid = threadIdx.x;
     const int T = a.T, H = a.H;
     const int npad = (H + 511) / 512 * 512;
-    const int xbytes = act_lds_bytes(npad);
+    const int xbytes = img_bytes(npad);
     uint8_t *s_w = s_x + T * xbytes;  // [up rows | gate rows]
 
+    const int wgid = blockIdx.y * gridDim.x + blockIdx.x;
+    FNS_MARK(1, wgid, 0);
     dma_to_lds<NT>(s_x, a.xpack, T * xbytes);
     route_channel<NT>(a, rs);
+    FNS_MARK(1, wgid, 1);
     const int e = rs.e;
     if (e < 0) return;
     const int ncol = rs.ncol;
@@ -377,6 +394,7 @@ __global__ __launch_bounds__(NT) void k_gate_up_lds(const LayerArgs a) {
     }
     dma_wait();
     __syncthreads();
+    FNS_MARK(1, wgid, 2);
 
     const int lane = tid % LPR, grp = tid / LPR;
     const int row = rowb + grp;
@@ -406,7 +424,88 @@ __global__ __launch_bounds__(NT) void k_gate_up_lds(const LayerArgs a) {
     }
     gate_up_epilogue<LPR, NC>(a, rs, s_act, kGuRows, grp, row, lane, acc, accg);
     __syncthreads();
+    FNS_MARK(1, wgid, 3);
     quant_act<NT>(a, rs, s_act, kGuRows, rowb);
+    FNS_MARK(1, wgid, 4);
+}
+
+// Quarter-block form (the decode path): 1024 threads, 32 rows per workgroup, 32 lanes per row, each lane one or more
+// 64-value quarters of the row's blocks. Waves 1-15 start the copy of the x images while wave 0 loads the logits;
+// after routing, wave w moves its own two up rows and two gate rows into LDS and waits only for those (no workgroup
+// barrier between the weight loads and the dot products), so waves whose data lands first compute first.
+constexpr int kQThreads = 1024, kQWaves = kQThreads / kWave;
+
+template <int TQ, int NC>
+__global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ RouteLds rs;
+    constexpr int BB = Traits<TQ>::bytes;
+    float *s_act = (float *) smem;  // [NC][32]
+    uint8_t *s_x = smem + NC * kGuRows * 4;
+    const int tid = threadIdx.x, wave = tid / kWave;
+    const int T = a.T, H = a.H;
+    const int npad = (H + 511) / 512 * 512;
+    const int xbytes = img_bytes(npad);
+    uint8_t *s_w = s_x + T * xbytes;  // [32 up rows | 32 gate rows]
+    const int wgid = blockIdx.y * gridDim.x + blockIdx.x;
+    FNS_MARK(1, wgid, 0);
+
+    __shared__ const uint8_t *s_tab[256];
+    // waves 1-15: the x images and the expert table (so the slot address is an LDS read once routing is done)
+    if (wave != 0 && tid - kWave < a.NE) s_tab[tid - kWave] = gload<const uint8_t *>((const uint8_t *) (a.table + (tid - kWave)));
+    dma_waves_from<kQWaves>(s_x, a.xpack, T * xbytes, 1);
+    if (wave != 0) dma_wait();
+    route_channel<kQThreads>(a, rs);  // the x images and the table are complete after its first barrier
+    FNS_MARK(1, wgid, 1);
+    const int e = rs.e;
+    if (e < 0) return;
+    const int ncol = rs.ncol;
+
+    const int nblk = H / 256;
+    const int row_bytes = nblk * BB;
+    const int rowb = blockIdx.x * kGuRows;
+    const uint8_t *slot = s_tab[e];
+    const uint8_t *wa = slot + a.up_off + (int64_t) rowb * row_bytes;
+    const uint8_t *wb = slot + a.gate_off + (int64_t) rowb * row_bytes;
+    const int region = kGuRows * row_bytes;  // a multiple of 16 (block sizes are even)
+    const bool staged = (((uintptr_t) wa | (uintptr_t) wb) & 15u) == 0;
+    const int r2 = 2 * wave;  // this wave's rows r2, r2 + 1
+    if (staged) {
+        dma_wave(s_w, wa, r2 * row_bytes, (r2 + 2) * row_bytes);
+        dma_wave(s_w + region, wb, r2 * row_bytes, (r2 + 2) * row_bytes);
+    }
+    dma_wait();
+    FNS_MARK(1, wgid, 2);
+
+    const int lane = tid % 32;
+    const int rl = r2 + (tid % kWave) / 32, row = rowb + rl;
+    ActImg img[NC];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) img[n] = act_img(s_x + (n < ncol ? rs.xrow[n] : 0) * xbytes, npad);
+    float acc[NC], accg[NC];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) acc[n] = accg[n] = 0.0f;
+    for (int qi = lane; qi < 4 * nblk; qi += 32) {
+        const int bb = qi >> 2, qt = qi & 3;
+        const int off = rl * row_bytes + bb * BB;
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            if (NC == 1 || n < ncol) {
+                if (staged) {
+                    acc[n] += quarter_dot<TQ, Aligned16>(s_w + off, img[n], bb, qt);
+                    accg[n] += quarter_dot<TQ, Aligned16>(s_w + region + off, img[n], bb, qt);
+                } else {
+                    acc[n] += quarter_dot<TQ, Any2>(wa + off, img[n], bb, qt);
+                    accg[n] += quarter_dot<TQ, Any2>(wb + off, img[n], bb, qt);
+                }
+            }
+        }
+    }
+    gate_up_epilogue<32, NC>(a, rs, s_act, kGuRows, rl, row, lane, acc, accg);
+    __syncthreads();
+    FNS_MARK(1, wgid, 3);
+    quant_act<kQThreads>(a, rs, s_act, kGuRows, rowb);
+    FNS_MARK(1, wgid, 4);
 }
 
 // ---- K3: (guard) + down GEMV + combine -------------------------------------------------------------------------------
@@ -433,7 +532,7 @@ __global__ __launch_bounds__(256) void k_down_combine(const LayerArgs a) {
     const int T = a.T, K = a.K, F = a.F, H = a.H;
     const int CH = T * K;
     const int fpad = (F + 511) / 512 * 512;
-    const int fbytes = act_lds_bytes(fpad);
+    const int fbytes = img_bytes(fpad);
     const int r0 = blockIdx.x * kDownRows;
     const int nblk = F / 256;
     const int64_t row_bytes = (int64_t) nblk * BB;
@@ -562,13 +661,14 @@ __global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
     const int T = a.T, K = a.K, F = a.F, H = a.H;
     const int CH = T * K;
     const int fpad = (F + 511) / 512 * 512;
-    const int fbytes = act_lds_bytes(fpad);
+    const int fbytes = img_bytes(fpad);
     const int r0 = blockIdx.x * kDownRows;  // hidden is a multiple of 256: all 8 rows exist
     const int nblk = F / 256;
     const int row_bytes = nblk * BB;
     const int region = kDownRows * row_bytes;  // a multiple of 16
     uint8_t *s_wt = smem + CH * fbytes;
 
+    FNS_MARK(2, blockIdx.x, 0);
     // 1. down pointers and combine weights (a barrier waits for every outstanding load, so only these go first)
     if (tid < CH) {
         s_dp[tid] = gload<const uint8_t *>((const uint8_t *) (a.dptr + tid)) + (int64_t) r0 * row_bytes;
@@ -576,6 +676,7 @@ __global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
         s_e[tid] = 1.0f;
     }
     __syncthreads();
+    FNS_MARK(2, blockIdx.x, 1);
     uintptr_t mis = 0;
     for (int c = 0; c < CH; ++c) mis |= (uintptr_t) s_dp[c];
     const bool staged = (mis & 15u) == 0;
@@ -585,6 +686,7 @@ __global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
         dma_gather_to_lds<256>(s_wt, CH * region, [&](int o) { return s_dp[o / region] + o % region; });
     dma_wait();
     __syncthreads();
+    FNS_MARK(2, blockIdx.x, 2);
     // 3. F16 guard: rows whose scale is not 1 are divided and re-quantised (reference src/kernels.cu:554-577)
     if (a.guard) {
         for (int c = wave; c < CH; c += 4) {
@@ -627,6 +729,7 @@ __global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
         if (lane == 0) s_dexp[ch][rr] = acc;
     }
     __syncthreads();
+    FNS_MARK(2, blockIdx.x, 3);
     // 5. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + 0) (+ x_resid)
     if (tid < T * kDownRows) {
         const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
@@ -635,17 +738,115 @@ __global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
         moe = moe + 0.0f;
         a.out[(size_t) t * H + r] = a.x_resid ? moe + a.x_resid[(size_t) t * H + r] : moe;
     }
+    FNS_MARK(2, blockIdx.x, 4);
+}
+
+// Quarter-block form of the down projection + combine: 1024 threads; the work is 2 * n_chan groups of (channel, four
+// of the workgroup's eight rows), group g taken by wave g % 16. Each wave copies its channel's act image and its four
+// rows into a private LDS area, waits only for its own copies and computes its four rows with 16 lanes per row.
+template <int TQ>
+__global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float s_e[kMaxCh], s_w[kMaxCh];
+    __shared__ float s_dexp[kMaxCh][kDownRows];
+    __shared__ const uint8_t *s_dp[kMaxCh];
+    constexpr int BB = Traits<TQ>::bytes;
+    const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
+    const int T = a.T, K = a.K, F = a.F, H = a.H;
+    const int CH = T * K;
+    const int fpad = (F + 511) / 512 * 512;
+    const int fbytes = img_bytes(fpad);
+    const int r0 = blockIdx.x * kDownRows;  // hidden is a multiple of 256: all 8 rows exist
+    const int nblk = F / 256;
+    const int row_bytes = nblk * BB;
+    const int wbuf = fbytes + 4 * row_bytes + 48;  // image | four rows (+ rounding to 16 bytes, + over-read)
+    uint8_t *priv = smem + wave * ((wbuf + 15) & ~15);
+    FNS_MARK(2, blockIdx.x, 0);
+
+    if (tid < CH) {
+        s_dp[tid] = gload<const uint8_t *>((const uint8_t *) (a.dptr + tid)) + (int64_t) r0 * row_bytes;
+        s_w[tid] = a.w[tid];
+    }
+    __syncthreads();
+    FNS_MARK(2, blockIdx.x, 1);
+    uintptr_t mis = 0;
+    for (int c = 0; c < CH; ++c) mis |= (uintptr_t) s_dp[c];
+    const bool staged = (mis & 15u) == 0;
+    const int sub = lane64 / 16, lane = tid % 16;
+    for (int g = wave; g < 2 * CH; g += kQWaves) {
+        const int ch = g >> 1, rb = 4 * (g & 1);  // rows rb .. rb + 3 of the workgroup's eight
+        if (g != wave) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): earlier reads of the area are done
+        dma_wave(priv, a.apack + (size_t) ch * fbytes, 0, fbytes);
+        const int beg = rb * row_bytes, gs = beg & ~15;
+        if (staged) dma_wave(priv + fbytes - gs, s_dp[ch], beg, beg + 4 * row_bytes);
+        dma_wait();
+        if (g == wave) FNS_MARK(2, blockIdx.x, 2);
+        // F16 guard: a row whose scale is not 1 is divided and re-quantised (reference src/kernels.cu:554-577)
+        float esc = 1.0f;
+        if (a.guard) {
+            float m = 0.0f;
+            for (int b = lane64; b < fpad / 32; b += kWave) m = fmaxf(m, a.blk_amax[(size_t) ch * (fpad / 32) + b]);
+            m = lanes_max<64>(m);
+            esc = guard_scale(m);
+            if (esc != 1.0f) {
+                const float *src = a.act + (size_t) ch * F;
+                for (int i0 = 0; i0 < fpad; i0 += kWave) {
+                    const int i = i0 + lane64;
+                    const Q8Lane r = q8_1_lane(i < F ? src[i] / esc : 0.0f);
+                    pack_store(priv, fpad, i, r);
+                }
+            }
+        }
+        if (lane64 == 0) {
+            s_e[ch] = esc;
+            if (blockIdx.x == 0) a.escale[ch] = esc;
+        }
+        const ActImg img = act_img(priv, fpad);
+        const int rr = rb + sub;
+        float acc = 0.0f;
+        for (int qi = lane; qi < 4 * nblk; qi += 16) {
+            const int bb = qi >> 2, qt = qi & 3;
+            if (staged) acc += quarter_dot<TQ, Aligned16>(priv + fbytes - gs + rr * row_bytes + bb * BB, img, bb, qt);
+            else acc += quarter_dot<TQ, Any2>(s_dp[ch] + rr * row_bytes + bb * BB, img, bb, qt);
+        }
+        acc = lanes_sum<16>(acc);
+        if (lane == 0) s_dexp[ch][rr] = acc;
+    }
+    __syncthreads();
+    FNS_MARK(2, blockIdx.x, 3);
+    // combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + 0) (+ x_resid)
+    if (tid < T * kDownRows) {
+        const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
+        float moe = (s_dexp[t * K][rr] * s_e[t * K]) * s_w[t * K];
+        for (int j = 1; j < K; ++j) moe = moe + (s_dexp[t * K + j][rr] * s_e[t * K + j]) * s_w[t * K + j];
+        moe = moe + 0.0f;
+        a.out[(size_t) t * H + r] = a.x_resid ? moe + a.x_resid[(size_t) t * H + r] : moe;
+    }
+    FNS_MARK(2, blockIdx.x, 4);
 }
 
 // LDS bytes of the staged kernels (0 when they do not fit: the register forms run instead).
 constexpr size_t kLdsBudget = 150 * 1024;
 inline size_t gate_up_lds_bytes(int T, int H, int BB, int NC) {
-    const size_t b = (size_t) NC * kGuRows * 4 + (size_t) T * act_lds_bytes((int) host::pad512(H)) +
+    const size_t b = (size_t) NC * kGuRows * 4 + (size_t) T * img_bytes((int) host::pad512(H)) +
                      2 * (size_t) kGuRows * (H / 256) * BB + 16;
     return b <= kLdsBudget ? b : 0;
 }
+// Quarter forms: sized for kMaxTok tokens whatever the call's n_tok, so a verify call and a decode call of the same
+// layer take the same kernels (and so the same arithmetic).
+inline size_t gate_up_q_lds_bytes(int T, int H, int BB, int NC) {
+    const size_t b = (size_t) NC * kGuRows * 4 + (size_t) T * img_bytes((int) host::pad512(H)) +
+                     2 * (size_t) kGuRows * (H / 256) * BB + 16;
+    return b;
+}
+inline bool gate_up_q_fits(int H, int BB) { return gate_up_q_lds_bytes(kMaxTok, H, BB, kMaxTok) <= kLdsBudget; }
+inline size_t down_q_lds_bytes(int F, int BB) {
+    const size_t wbuf = (size_t) img_bytes((int) host::pad512(F)) + 4 * (size_t) (F / 256) * BB + 48;
+    return kQWaves * ((wbuf + 15) & ~(size_t) 15);
+}
+inline bool down_q_fits(int F, int BB) { return down_q_lds_bytes(F, BB) <= kLdsBudget; }
 inline size_t down_lds_bytes(int CH, int F, int BB) {
-    const size_t b = (size_t) CH * act_lds_bytes((int) host::pad512(F)) + (size_t) CH * kDownRows * (F / 256) * BB + 16;
+    const size_t b = (size_t) CH * img_bytes((int) host::pad512(F)) + (size_t) CH * kDownRows * (F / 256) * BB + 16;
     return b <= kLdsBudget ? b : 0;
 }
 
@@ -665,7 +866,7 @@ template <int TQ, int LPR, int BPL, int NC, int NT> int launch_gate_up_nt(const 
     const int n_chan = a.T == 1 ? a.K : std::min(a.T * a.K, a.NE);
     const dim3 grid((unsigned) ((a.F + RPB - 1) / RPB), (unsigned) n_chan);
     const int npad = (int) host::pad512(a.H);
-    const size_t lds = (size_t) NC * RPB * 4 + (size_t) a.T * act_lds_bytes(npad);
+    const size_t lds = (size_t) NC * RPB * 4 + (size_t) a.T * img_bytes(npad);
     if (lds > 64 * 1024) return host::set_error(host::ERR_SHAPE, "moe_layer: hidden too large for LDS staging");
     hipLaunchKernelGGL((k_gate_up<TQ, LPR, BPL, NC, NT>), grid, dim3(NT), lds, st, a);
     return host::check_launch("moe gate_up");
@@ -692,6 +893,17 @@ template <int TQ, int LPR> int launch_gate_up_lds(const LayerArgs &a, size_t lds
 
 template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
     const int nblk = a.H / 256;
+    if (gate_up_q_fits(a.H, Traits<TQ>::bytes)) {
+        const int n_chan = a.T == 1 ? a.K : std::min(a.T * a.K, a.NE);
+        const dim3 grid((unsigned) (a.F / kGuRows), (unsigned) n_chan);
+        if (a.T == 1)
+            hipLaunchKernelGGL((k_gate_up_q<TQ, 1>), grid, dim3(kQThreads),
+                               gate_up_q_lds_bytes(1, a.H, Traits<TQ>::bytes, 1), st, a);
+        else
+            hipLaunchKernelGGL((k_gate_up_q<TQ, kMaxTok>), grid, dim3(kQThreads),
+                               gate_up_q_lds_bytes(a.T, a.H, Traits<TQ>::bytes, kMaxTok), st, a);
+        return host::check_launch("moe gate_up (quarters)");
+    }
     const size_t lds = gate_up_lds_bytes(a.T, a.H, Traits<TQ>::bytes, a.T == 1 ? 1 : kMaxTok);
     if (lds) {
         if (nblk <= 2) return launch_gate_up_lds<TQ, 2>(a, lds, st);
@@ -709,7 +921,7 @@ template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
 
 template <int TQ, int LPR, int BPL> int launch_down(const LayerArgs &a, hipStream_t st) {
     const dim3 grid((unsigned) ((a.H + kDownRows - 1) / kDownRows));
-    const size_t lds = (size_t) a.T * a.K * act_lds_bytes((int) host::pad512(a.F));
+    const size_t lds = (size_t) a.T * a.K * img_bytes((int) host::pad512(a.F));
     hipLaunchKernelGGL((k_down_combine<TQ, LPR, BPL>), grid, dim3(256), lds, st, a);
     return host::check_launch("moe down_combine");
 }
@@ -727,6 +939,11 @@ template <int TQ, int LPR> int launch_down_lds(const LayerArgs &a, size_t lds, h
 
 template <int TQ> int dispatch_down(const LayerArgs &a, hipStream_t st) {
     const int nblk = a.F / 256;
+    if (down_q_fits(a.F, Traits<TQ>::bytes)) {
+        hipLaunchKernelGGL((k_down_q<TQ>), dim3((unsigned) (a.H / kDownRows)), dim3(kQThreads),
+                           down_q_lds_bytes(a.F, Traits<TQ>::bytes), st, a);
+        return host::check_launch("moe down_combine (quarters)");
+    }
     const size_t lds = down_lds_bytes(a.T * a.K, a.F, Traits<TQ>::bytes);
     if (lds) {
         if (nblk <= 2) return launch_down_lds<TQ, 2>(a, lds, st);
@@ -776,8 +993,8 @@ void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     sizes[3] = ch * 4;
     sizes[4] = ch * L->inter * 4;
     sizes[5] = ch * 4;
-    sizes[6] = (size_t) n_tok * act_lds_bytes((int) hpad);
-    sizes[7] = ch * act_lds_bytes((int) fpad);
+    sizes[6] = (size_t) n_tok * img_bytes((int) hpad);
+    sizes[7] = ch * img_bytes((int) fpad);
     sizes[8] = ch * (fpad / 32) * 4;
     sizes[9] = ch * 8;
 }
@@ -819,7 +1036,7 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
         return host::set_error(host::ERR_TYPE, "moe_layer: router dtype %d not supported", L->router_dtype);
     if (!host::is_kquant(L->gu_type) || !host::is_kquant(L->down_type))
         return host::set_error(host::ERR_TYPE, "moe_layer: expert types %d/%d not supported", L->gu_type, L->down_type);
-    const size_t lds_down = (size_t) n_tok * L->k * act_lds_bytes((int) host::pad512(L->inter));
+    const size_t lds_down = (size_t) n_tok * L->k * img_bytes((int) host::pad512(L->inter));
     if (lds_down > 64 * 1024)
         return host::set_error(host::ERR_SHAPE, "moe_layer: n_tok * k * inter too large for the down kernel's LDS");
     size_t sizes[kSections];
@@ -900,3 +1117,13 @@ int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float
 }  // namespace impl
 
 }  // namespace fns
+
+#ifdef FNS_PROBE
+extern "C" int fns_probe_read(void *host) {
+    return (int) hipMemcpyFromSymbol(host, HIP_SYMBOL(fns::g_probe), sizeof(fns::g_probe));
+}
+extern "C" int fns_probe_clear() {
+    static unsigned long long z[3][4096][6];
+    return (int) hipMemcpyToSymbol(HIP_SYMBOL(fns::g_probe), z, sizeof(z));
+}
+#endif
