@@ -93,10 +93,10 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ lg, in
 // are all distinct. Then eight threads per expert each count the keys above the expert's own over one eighth of the
 // experts; the expert with rank r < k goes to slot r - the same result as k rounds of argmax with ties to the lower
 // index, without a dependent cross-lane chain. Must be called by every thread of the workgroup (it contains
-// barriers). Results: sel[0..k), w[0..k) in LDS.
+// barriers). Results: sel[0..k) and their probabilities pv[0..k) in LDS, visible to the whole workgroup on return.
 template <int NT>
-__device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, int n_expert, int k, int gating, int norm,
-                                                 uint64_t *s_key, int *sel, float *pv, float *w) {
+__device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, int n_expert, int k, int gating,
+                                                 uint64_t *s_key, int *sel, float *pv) {
     constexpr int P = 8;         // threads per expert
     constexpr int EPP = NT / P;  // experts per pass
     const int tid = threadIdx.x, lane = tid % kWave;
@@ -155,11 +155,15 @@ __device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, i
         }
     }
     __syncthreads();
-    if (tid < k) {
-        float sum = 0.0f;
-        for (int r = 0; r < k; ++r) sum += pv[r];
-        w[tid] = norm ? pv[tid] / fmaxf(sum, 6.103515625e-5f) : pv[tid];
-    }
+}
+
+// Combine weight of slot j (0 <= j < k < 16) from the selected probabilities pv[0..k): renormalised by their sum in
+// slot order (floored at 2^-14) when norm is set.
+__device__ __forceinline__ float route_weight(const float *pv, int k, int norm, int j) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sum += r < k ? pv[r] : 0.0f;
+    return norm ? pv[j] / fmaxf(sum, 6.103515625e-5f) : pv[j];
 }
 
 }  // namespace fns::dev

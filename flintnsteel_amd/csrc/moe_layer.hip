@@ -97,9 +97,9 @@ __device__ __forceinline__ void pack_store(uint8_t *pack, int npad, int i, const
 // ---- K1: router rows + Q8_1 of x ----------------------------------------------------------------------------------
 // 1024-thread workgroups: the first ceil(n_expert / 4) each compute four router rows (256 lanes per row), the rest
 // quantise 1024 columns of one token row. Few, wide workgroups start faster than one small workgroup per row.
-constexpr int kK1Threads = 1024, kK1Rows = 4;
+constexpr int kK1Threads = 256, kK1Rows = kK1Threads / 256;
 
-__global__ __launch_bounds__(1024) void k_route_quant(const LayerArgs a) {
+__global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
     __shared__ float red[kK1Rows][4][kMaxTok];
     const int H = a.H, T = a.T;
     const int n_router_wg = (a.NE + kK1Rows - 1) / kK1Rows;
@@ -160,71 +160,74 @@ template <int NT, int LPR> constexpr int gu_rows_per_group() { return (NT / LPR)
 struct alignas(16) RouteLds {
     uint64_t key[256];
     int ids[kMaxCh];
-    float pv[16], wsel[16];
+    float pv[16];
     int sel[16];
     int wave_cnt[16];
     int e, ncol, xrow[kMaxTok], orow[kMaxTok];
 };
 
 // Gating + top-k for every token (workgroup (0, 0) publishes ids, weights and down pointers), then channel
-// blockIdx.y -> expert and its (token, slot) columns: slot order for n_tok = 1, distinct experts ascending for
-// n_tok > 1 (compaction: channel c takes the c-th smallest selected id). Sets rs.e = -1 for an idle channel.
+// blockIdx.y -> expert and its (token, slot) columns (rs.ncol, rs.xrow, rs.orow): slot order for n_tok = 1, distinct
+// experts ascending for n_tok > 1 (compaction: channel c takes the c-th smallest selected id). Returns the expert, or
+// -1 for an idle channel. Every thread of the workgroup must call it.
+__device__ __forceinline__ void publish_route(const LayerArgs &a, const RouteLds &rs, int t, int j) {
+    const int e = rs.sel[j];
+    a.ids[t * a.K + j] = e;
+    a.w[t * a.K + j] = route_weight(rs.pv, a.K, a.norm, j);
+    a.dptr[t * a.K + j] = (const uint8_t *) gload<const char *>((const uint8_t *) (a.table + e)) + a.down_off;
+}
+
 template <int NT>
-__device__ __forceinline__ void route_channel(const LayerArgs &a, RouteLds &rs) {
+__device__ __forceinline__ int route_channel(const LayerArgs &a, RouteLds &rs) {
     const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
     const int T = a.T, K = a.K;
     const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
-    for (int t = 0; t < T; ++t) {
-        route_topk_block<NT>(a.logits + (size_t) t * a.NE, a.NE, K, a.gating, a.norm, rs.key, rs.sel, rs.pv, rs.wsel);
-        __syncthreads();
-        if (tid < K) {
-            rs.ids[t * K + tid] = rs.sel[tid];
-            if (pub) {
-                a.ids[t * K + tid] = rs.sel[tid];
-                a.w[t * K + tid] = rs.wsel[tid];
-                a.dptr[t * K + tid] = (const uint8_t *) a.table[rs.sel[tid]] + a.down_off;
-            }
-        }
-        __syncthreads();
-    }
-    if (tid == 0) rs.e = -1;
-    __syncthreads();
     if (T == 1) {
         if (tid == 0) {
-            rs.e = rs.ids[blockIdx.y];
             rs.ncol = 1;
             rs.xrow[0] = 0;
             rs.orow[0] = blockIdx.y;
         }
-    } else {
-        int base = 0;  // selected experts below e0
-        for (int e0 = 0; e0 < a.NE; e0 += NT) {
-            const int ex = e0 + tid;
-            bool present = false;
-            if (ex < a.NE)
-                for (int i = 0; i < T * K; ++i) present |= rs.ids[i] == ex;
-            const uint64_t m = __ballot(present);
-            if (lane64 == 0) rs.wave_cnt[wave] = __popcll(m);
-            __syncthreads();
-            int rank = base + __popcll(m & ((1ull << lane64) - 1ull));
-            for (int wv = 0; wv < wave; ++wv) rank += rs.wave_cnt[wv];
-            for (int wv = 0; wv < NT / kWave; ++wv) base += rs.wave_cnt[wv];
-            if (present && rank == (int) blockIdx.y) {
-                rs.e = ex;
-                int n = 0;
-                for (int t = 0; t < T; ++t)
-                    for (int j = 0; j < K; ++j)
-                        if (rs.ids[t * K + j] == ex) {
-                            rs.xrow[n] = t;
-                            rs.orow[n] = t * K + j;
-                            ++n;
-                        }
-                rs.ncol = n;
-            }
-            __syncthreads();
+        route_topk_block<NT>(a.logits, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
+        if (pub && tid < K) publish_route(a, rs, 0, tid);
+        return rs.sel[blockIdx.y];
+    }
+    for (int t = 0; t < T; ++t) {
+        route_topk_block<NT>(a.logits + (size_t) t * a.NE, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
+        if (tid < K) {  // wave 0: done before it writes the next token's keys
+            rs.ids[t * K + tid] = rs.sel[tid];
+            if (pub) publish_route(a, rs, t, tid);
         }
     }
+    if (tid == 0) rs.e = -1;
     __syncthreads();
+    int base = 0;  // selected experts below e0
+    for (int e0 = 0; e0 < a.NE; e0 += NT) {
+        const int ex = e0 + tid;
+        bool present = false;
+        if (ex < a.NE)
+            for (int i = 0; i < T * K; ++i) present |= rs.ids[i] == ex;
+        const uint64_t m = __ballot(present);
+        if (lane64 == 0) rs.wave_cnt[wave] = __popcll(m);
+        __syncthreads();
+        int rank = base + __popcll(m & ((1ull << lane64) - 1ull));
+        for (int wv = 0; wv < wave; ++wv) rank += rs.wave_cnt[wv];
+        for (int wv = 0; wv < NT / kWave; ++wv) base += rs.wave_cnt[wv];
+        if (present && rank == (int) blockIdx.y) {
+            rs.e = ex;
+            int n = 0;
+            for (int t = 0; t < T; ++t)
+                for (int j = 0; j < K; ++j)
+                    if (rs.ids[t * K + j] == ex) {
+                        rs.xrow[n] = t;
+                        rs.orow[n] = t * K + j;
+                        ++n;
+                    }
+            rs.ncol = n;
+        }
+        __syncthreads();
+    }
+    return rs.e;
 }
 
 // SwiGLU epilogue of one row (LPR-lane partial sums) and the Q8_1 of the workgroup's RPB act rows per column.
@@ -281,8 +284,7 @@ __global__ __launch_bounds__(NT) void k_gate_up(const LayerArgs a) {
     const int xbytes = img_bytes(npad);
 
     for (int t = 0; t < T; ++t) copy_to_lds(s_x + t * xbytes, a.xpack + (size_t) t * xbytes, xbytes, tid, NT);
-    route_channel<NT>(a, rs);
-    const int e = rs.e;
+    const int e = route_channel<NT>(a, rs);
     if (e < 0) return;  // fewer distinct experts than channels: uniform exit of the whole workgroup
     const int ncol = rs.ncol;
 
@@ -455,9 +457,8 @@ __global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
     if (wave != 0 && tid - kWave < a.NE) s_tab[tid - kWave] = gload<const uint8_t *>((const uint8_t *) (a.table + (tid - kWave)));
     dma_waves_from<kQWaves>(s_x, a.xpack, T * xbytes, 1);
     if (wave != 0) dma_wait();
-    route_channel<kQThreads>(a, rs);  // the x images and the table are complete after its first barrier
+    const int e = route_channel<kQThreads>(a, rs);  // the x images and the table are complete after its first barrier
     FNS_MARK(1, wgid, 1);
-    const int e = rs.e;
     if (e < 0) return;
     const int ncol = rs.ncol;
 
