@@ -73,10 +73,10 @@ template <int W> __device__ __forceinline__ float lanes_max(float v) {
 
 // Q8_1 of one value per lane, 32-lane blocks (lanes 0-31, 32-63): the reference's op order (d = amax / 127,
 // q = roundf(x / d), ds = (d, sum) with xor butterflies 16 .. 1). Returns q; d, sum and the 16-lane integer sum of q
-// (for the K-quant min term) are valid in every lane of the block.
+// (for the K-quant min term) and the block's max |v| are valid in every lane of the block.
 struct Q8Lane {
     int q;
-    float d, sum;
+    float d, sum, amax;
     int qsum16, qsum32;
 };
 __device__ __forceinline__ Q8Lane q8_1_lane(float v) {
@@ -92,6 +92,7 @@ __device__ __forceinline__ Q8Lane q8_1_lane(float v) {
     amax = fmaxf(amax, xor_lane<1>(amax));
     sum += xor_lane<1>(sum);
     Q8Lane r;
+    r.amax = amax;
     r.d = amax / 127.0f;
     r.q = amax == 0.0f ? 0 : (int) (int8_t) roundf(v / r.d);
     r.sum = sum;

@@ -28,6 +28,10 @@
 #include "fns_quarter.hpp"
 #include "fns_route.hpp"
 
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
 namespace fns {
 
 using namespace fns::dev;
@@ -51,6 +55,10 @@ namespace {
 constexpr int kMaxTok = 4;
 constexpr int kMaxCh = kMaxTok * 16;
 constexpr int kDownRows = 8;  // output rows per down workgroup
+constexpr size_t kLdsBudget = 150 * 1024;  // dynamic LDS per workgroup (gfx950: 160 KiB per CU)
+// Fused-kernel synchronisation words, each on its own 256-byte line: 16 group counters, the count of complete groups,
+// and 16 copies of the release flag (workgroups poll copy b % 16, so no line has more than 1/16 of the pollers).
+constexpr int kSyncStride = 64, kSyncGroups = 16, kSyncLines = 2 * kSyncGroups + 1;
 
 struct LayerArgs {
     int H, F, NE, K, T;
@@ -73,7 +81,9 @@ struct LayerArgs {
     uint8_t *apack;       // [T*K][img_bytes(Fpad)] Q8_1 of act, LDS image
     float *blk_amax;      // [T*K][Fpad / 32]
     const uint8_t **dptr; // [T*K] down matrix of each (token, slot)
+    int *sync;            // fused-kernel completion counters and flags, one per 256-byte line (zeroed by the router kernel)
     int64_t xq_row_bytes;
+    int fused;            // the shape fits the fused kernel (n_tok = 1)
 };
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t) b << 16); }
@@ -104,6 +114,7 @@ __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
     const int H = a.H, T = a.T;
     const int n_router_wg = (a.NE + kK1Rows - 1) / kK1Rows;
     FNS_MARK(0, blockIdx.x, 0);
+    if (blockIdx.x == 0 && threadIdx.x < kSyncLines) a.sync[threadIdx.x * kSyncStride] = 0;  // ordered before the next kernel
     if ((int) blockIdx.x < n_router_wg) {
         const int sub = threadIdx.x / 256, t256 = threadIdx.x % 256;
         const int r = blockIdx.x * kK1Rows + sub;
@@ -262,7 +273,7 @@ __device__ __forceinline__ void quant_act(const LayerArgs &a, const RouteLds &rs
         const Q8Lane r = q8_1_lane(v);
         const int c = rs.orow[n];
         if (live && i < fpad) pack_store(a.apack + (size_t) c * fbytes, fpad, i, r);
-        if (live && i % 32 == 0 && i < fpad) a.blk_amax[(size_t) c * (fpad / 32) + i / 32] = r.d * 127.0f;
+        if (live && i % 32 == 0 && i < fpad) a.blk_amax[(size_t) c * (fpad / 32) + i / 32] = r.amax;
     }
 }
 
@@ -826,8 +837,242 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
     FNS_MARK(2, blockIdx.x, 4);
 }
 
+// ---- Fused decode layer (n_tok = 1): routing + gate/up + SwiGLU + down + combine in one kernel -------------------
+// hidden / 8 workgroups of 1024 threads, all resident at once (one per CU; the host checks the occupancy).
+//   producers b < k * inter / 32: gate/up rows [32 u, 32 u + 32) of slot c (b = c (inter / 32) + u), as k_gate_up_q,
+//                                  and their Q8_1 block (the act image and block max, written device-coherent);
+//   every workgroup              : down rows [8 b, 8 b + 8) of all k slots and their combine, as k_down_q.
+// Right after routing each workgroup starts the LDS-DMA of its gate/up rows and its down rows together, so all of the
+// layer's expert bytes are in flight at once. A producer counts its arrival once its act stores have completed (a
+// two-level count: 16 group counters, then complete groups, the last of which raises 16 release flags) and every
+// workgroup waits (bounded) on its flag before it reads the act images with device-scope loads. The router kernel
+// zeroes the counters; a kernel boundary orders that before this kernel. Per-(row, slot) arithmetic is that of the
+// two-kernel path, so results are the same bit for bit.
+constexpr int kFusedRows = 8;
+constexpr int kSpinLimit = 1 << 16;
+constexpr int kCpolDevice = 16;  // cache-policy bits of a device-scope (sc1) load: not served from a stale L2 line
+
+__device__ __forceinline__ void store_dev(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int TGU, int TDN>
+__global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ RouteLds rs;
+    __shared__ const uint8_t *s_tab[256];
+    __shared__ float s_dexp[16][kFusedRows];
+    __shared__ float s_e[16], s_w[16], s_act[kGuRows];
+    __shared__ int s_fail;
+    constexpr int BG = Traits<TGU>::bytes, BD = Traits<TDN>::bytes;
+    const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
+    const int H = a.H, F = a.F, K = a.K;
+    const int npad = (H + 511) / 512 * 512, xbytes = img_bytes(npad);
+    const int fpad = (F + 511) / 512 * 512, fbytes = img_bytes(fpad);
+    const int nbg = H / 256, rbg = nbg * BG;
+    const int nbd = F / 256, rbd = nbd * BD;
+    const int upc = F / kGuRows;                          // producers per slot
+    const bool producer = (int) blockIdx.x < K * upc;
+    const int c = blockIdx.x / upc, u = blockIdx.x % upc;  // meaningful for producers
+    const int r0 = blockIdx.x * kFusedRows;
+    const int gu_region = kGuRows * rbg, dn_region = kFusedRows * rbd;  // multiples of 16
+    uint8_t *s_x = smem;
+    uint8_t *s_a = s_x + xbytes;         // [K] act images
+    uint8_t *s_gu = s_a + K * fbytes;    // [32 up rows | 32 gate rows]
+    uint8_t *s_dn = s_gu + 2 * gu_region;  // [K][8 down rows]
+    FNS_MARK(1, blockIdx.x, 0);
+
+    // 1. waves 1-15: x image and expert table; wave 0: logits. Routing (all selected slots are needed here).
+    if (wave != 0 && tid - kWave < a.NE)
+        s_tab[tid - kWave] = gload<const uint8_t *>((const uint8_t *) (a.table + (tid - kWave)));
+    if (tid == 0) s_fail = 0;
+    dma_waves_from<kQWaves>(s_x, a.xpack, xbytes, 1);
+    if (wave != 0) dma_wait();
+    route_topk_block<kQThreads>(a.logits, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
+    if (blockIdx.x == 0 && tid < K) publish_route(a, rs, 0, tid);
+    if (tid < K) s_w[tid] = route_weight(rs.pv, K, a.norm, tid);
+    FNS_MARK(1, blockIdx.x, 1);
+
+    // 2. weights: each wave its two gate/up rows (producers), then its share of the down rows
+    const uint8_t *slot = s_tab[rs.sel[producer ? c : 0]];
+    const uint8_t *wa = slot + a.up_off + (int64_t) (u * kGuRows) * rbg;
+    const uint8_t *wb = slot + a.gate_off + (int64_t) (u * kGuRows) * rbg;
+    uintptr_t mis = producer ? ((uintptr_t) wa | (uintptr_t) wb) : 0;
+    for (int j = 0; j < K; ++j) mis |= (uintptr_t) (s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd);
+    const bool staged = (mis & 15u) == 0;
+    if (staged) {
+        if (producer) {
+            dma_wave(s_gu, wa, 2 * wave * rbg, (2 * wave + 2) * rbg);
+            dma_wave(s_gu + gu_region, wb, 2 * wave * rbg, (2 * wave + 2) * rbg);
+        }
+        // down: wave w takes pieces [w * dn_piece, (w + 1) * dn_piece) of the flattened [K][dn_region] image
+        const int dn_total = K * dn_region, dn_piece = ((dn_total + kQWaves * 16 - 1) / (kQWaves * 16)) * 16;
+        const int p_lo = wave * dn_piece, p_hi = min(dn_total, p_lo + dn_piece);
+        for (int j = p_lo / dn_region; j < K && j * dn_region < p_hi; ++j) {
+            const int lo = max(p_lo - j * dn_region, 0), hi = min(p_hi - j * dn_region, dn_region);
+            dma_wave(s_dn + j * dn_region, s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd, lo, hi);
+        }
+    }
+    dma_wait();
+    FNS_MARK(1, blockIdx.x, 2);
+
+    // 3. producers: gate/up rows (32 lanes per row, as k_gate_up_q) -> act -> its Q8_1 block, stored device-coherent
+    if (producer) {
+        const int lane = tid % 32, rl = 2 * wave + lane64 / 32, row = u * kGuRows + rl;
+        const ActImg img = act_img(s_x, npad);
+        float acc = 0.0f, accg = 0.0f;
+        for (int qi = lane; qi < 4 * nbg; qi += 32) {
+            const int bb = qi >> 2, qt = qi & 3;
+            const int off = rl * rbg + bb * BG;
+            if (staged) {
+                acc += quarter_dot<TGU, Aligned16>(s_gu + off, img, bb, qt);
+                accg += quarter_dot<TGU, Aligned16>(s_gu + gu_region + off, img, bb, qt);
+            } else {
+                acc += quarter_dot<TGU, Any2>(wa + off, img, bb, qt);
+                accg += quarter_dot<TGU, Any2>(wb + off, img, bb, qt);
+            }
+        }
+        float v = lanes_sum<32>(acc);
+        const float gs = lanes_sum<32>(accg);
+        v += 0.0f;  // fused-GLU epilogue with zero biases (reference src/ggml/ggml_mmvq.cu:240-247)
+        v *= silu(gs + 0.0f);
+        if (lane == 0) {
+            s_act[rl] = v;
+            store_dev(a.act + (size_t) c * F + row, v);
+        }
+        __syncthreads();
+        if (wave == 0) {  // the 32 rows form one Q8_1 block (lanes 0-31; lanes 32-63 quantise zeros, store nothing)
+            const int i = u * kGuRows + lane64 % 32;
+            const Q8Lane r = q8_1_lane(lane64 < 32 ? s_act[lane64] : 0.0f);
+            if (lane64 < 32) {
+                uint8_t *img_g = a.apack + (size_t) c * fbytes;
+                const float dh = half_to_float(float_to_half(r.d));
+                float *dg = (float *) (img_g + img_q_bytes(fpad));
+                // q: 32 bytes = 8 dwords; lane 4j stores dword j, gathered from lanes 4j .. 4j+3
+                const uint32_t qb = (uint32_t) (uint8_t) (int8_t) r.q;
+                uint32_t word = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) word |= (uint32_t) __shfl((int) qb, (lane64 & ~3) + k, 64) << (8 * k);
+                if ((lane64 & 3) == 0) store_dev((uint32_t *) (img_g + img_q_index(i)), word);
+                if (lane64 == 0) {
+                    store_dev(dg + i / 32, dh);
+                    store_dev(dg + fpad / 32 + fpad / 16 + i / 32, dh * (float) r.qsum32);
+                    store_dev(a.blk_amax + (size_t) c * (fpad / 32) + i / 32, r.amax);
+                }
+                if (lane64 % 16 == 0) store_dev(dg + fpad / 32 + i / 16, dh * (float) r.qsum16);
+            }
+        }
+        dma_wait();  // this wave's device-coherent stores have completed
+    }
+    __syncthreads();
+    FNS_MARK(1, blockIdx.x, 3);
+    // 4. arrival (producers) and wait (everyone; bounded: a timeout poisons this workgroup's outputs with NaN)
+    const int nprod = K * upc;
+    if (tid == 0) {
+        int *sy = a.sync;
+        if (producer) {
+            const int g = blockIdx.x % kSyncGroups;
+            const int members = (nprod - g + kSyncGroups - 1) / kSyncGroups;
+            const int groups = nprod < kSyncGroups ? nprod : kSyncGroups;
+            if (__hip_atomic_fetch_add(sy + g * kSyncStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    members - 1 &&
+                __hip_atomic_fetch_add(sy + kSyncGroups * kSyncStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    groups - 1)
+                for (int f = 0; f < kSyncGroups; ++f)
+                    __hip_atomic_store(sy + (kSyncGroups + 1 + f) * kSyncStride, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const int *flag = sy + (kSyncGroups + 1 + blockIdx.x % kSyncGroups) * kSyncStride;
+        int spins = 0;
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+            if (++spins > kSpinLimit) {
+                s_fail = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+        }
+    }
+    __syncthreads();
+    FNS_MARK(2, blockIdx.x, 0);
+    // 5. act images (device-scope LDS-DMA) and the F16 guard: a slot whose scale is not 1 is divided and re-quantised
+    //    (reference src/kernels.cu:554-577)
+    for (int p = wave * 1024; p < K * fbytes; p += kQThreads * 16)
+        if (p + lane64 * 16 < K * fbytes)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *) (a.apack + p + lane64 * 16),
+                (__attribute__((address_space(3))) void *) (s_a + p), 16, 0, kCpolDevice);
+    dma_wait();
+    __syncthreads();
+    if (a.guard) {
+        for (int ch = wave; ch < K; ch += kQWaves) {
+            float m = 0.0f;
+            for (int bl = lane64; bl < fpad / 32; bl += kWave)
+                m = fmaxf(m, __hip_atomic_load(a.blk_amax + (size_t) ch * (fpad / 32) + bl, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT));
+            m = lanes_max<64>(m);
+            const float esc = guard_scale(m);
+            if (lane64 == 0) {
+                s_e[ch] = esc;
+                if (blockIdx.x == 0) a.escale[ch] = esc;
+            }
+            if (esc != 1.0f) {
+                for (int i0 = 0; i0 < fpad; i0 += kWave) {
+                    const int i = i0 + lane64;
+                    const float v = i < F ? __hip_atomic_load(a.act + (size_t) ch * F + i, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT)
+                                          : 0.0f;
+                    const Q8Lane r = q8_1_lane(v / esc);
+                    pack_store(s_a + ch * fbytes, fpad, i, r);
+                }
+            }
+        }
+    } else if (tid < K) {
+        s_e[tid] = 1.0f;
+        if (blockIdx.x == 0) a.escale[tid] = 1.0f;
+    }
+    __syncthreads();
+    FNS_MARK(2, blockIdx.x, 1);
+    // 6. down rows (16 lanes per (row, slot) item, as k_down_q), then the combine in slot order
+    const int lane16 = tid % 16;
+    for (int it = tid / 16; it < kFusedRows * K; it += kQThreads / 16) {
+        const int ch = it / kFusedRows, rr = it % kFusedRows;
+        const ActImg img = act_img(s_a + ch * fbytes, fpad);
+        const uint8_t *gsrc = s_tab[rs.sel[ch]] + a.down_off + (int64_t) (r0 + rr) * rbd;
+        float acc = 0.0f;
+        for (int qi = lane16; qi < 4 * nbd; qi += 16) {
+            const int bb = qi >> 2, qt = qi & 3;
+            if (staged) acc += quarter_dot<TDN, Aligned16>(s_dn + ch * dn_region + rr * rbd + bb * BD, img, bb, qt);
+            else acc += quarter_dot<TDN, Any2>(gsrc + bb * BD, img, bb, qt);
+        }
+        acc = lanes_sum<16>(acc);
+        if (lane16 == 0) s_dexp[ch][rr] = acc;
+    }
+    __syncthreads();
+    if (tid < kFusedRows) {
+        const int r = r0 + tid;
+        float moe = (s_dexp[0][tid] * s_e[0]) * s_w[0];
+        for (int j = 1; j < K; ++j) moe = moe + (s_dexp[j][tid] * s_e[j]) * s_w[j];
+        moe = moe + 0.0f;
+        float o = a.x_resid ? moe + a.x_resid[r] : moe;
+        if (s_fail) o = __builtin_nanf("");
+        a.out[r] = o;
+    }
+    FNS_MARK(2, blockIdx.x, 4);
+}
+
+// Fused-kernel plan for one layer shape (n_tok = 1): LDS bytes, or 0 when the shape does not fit the scheme.
+inline size_t fused_lds(int H, int F, int K, int BG, int BD) {
+    if (F % kGuRows || (int64_t) K * (F / kGuRows) > H / kFusedRows) return 0;  // every producer is a workgroup
+    if (K > 16) return 0;
+    const size_t lds = (size_t) img_bytes((int) host::pad512(H)) + (size_t) K * img_bytes((int) host::pad512(F)) +
+                       2 * (size_t) kGuRows * (H / 256) * BG + (size_t) K * kFusedRows * (F / 256) * BD + 48;
+    return lds <= kLdsBudget ? lds : 0;
+}
+
 // LDS bytes of the staged kernels (0 when they do not fit: the register forms run instead).
-constexpr size_t kLdsBudget = 150 * 1024;
 inline size_t gate_up_lds_bytes(int T, int H, int BB, int NC) {
     const size_t b = (size_t) NC * kGuRows * 4 + (size_t) T * img_bytes((int) host::pad512(H)) +
                      2 * (size_t) kGuRows * (H / 256) * BB + 16;
@@ -960,6 +1205,70 @@ template <int TQ> int dispatch_down(const LayerArgs &a, hipStream_t st) {
     }
 }
 
+// The fused kernel runs only when every workgroup can be resident at once (it waits on other workgroups): the
+// occupancy of each (gate/up type, down type, LDS size) is queried once per device and cached.
+template <int TGU, int TDN> const void *fused_fn() { return (const void *) k_layer_fused<TGU, TDN>; }
+
+template <int TGU> const void *fused_fn_by_down(int tdn) {
+    switch (tdn) {
+        case T_Q3_K: return fused_fn<TGU, T_Q3_K>();
+        case T_Q4_K: return fused_fn<TGU, T_Q4_K>();
+        case T_Q5_K: return fused_fn<TGU, T_Q5_K>();
+        case T_Q6_K: return fused_fn<TGU, T_Q6_K>();
+    }
+    return nullptr;
+}
+const void *fused_kernel(int tgu, int tdn) {
+    switch (tgu) {
+        case T_Q3_K: return fused_fn_by_down<T_Q3_K>(tdn);
+        case T_Q4_K: return fused_fn_by_down<T_Q4_K>(tdn);
+        case T_Q5_K: return fused_fn_by_down<T_Q5_K>(tdn);
+        case T_Q6_K: return fused_fn_by_down<T_Q6_K>(tdn);
+    }
+    return nullptr;
+}
+
+struct ResidencyKey {
+    int dev;
+    const void *fn;
+    size_t lds;
+    int resident;  // workgroups that fit at once on the device
+};
+std::mutex g_res_mu;
+std::vector<ResidencyKey> g_res;
+
+int resident_groups(const void *fn, size_t lds) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lk(g_res_mu);
+    for (const ResidencyKey &k : g_res)
+        if (k.dev == dev && k.fn == fn && k.lds == lds) return k.resident;
+    int n_cu = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kQThreads, lds) != hipSuccess)
+        return 0;
+    g_res.push_back({dev, fn, lds, n_cu * per_cu});
+    return n_cu * per_cu;
+}
+
+// True when this call (n_tok = 1, a shape that fits) takes the fused kernel.
+bool use_fused(const FnsMoeLayer *L, const LayerArgs &a) {
+    if (!a.fused) return false;
+    const size_t lds = fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type));
+    const void *fn = fused_kernel(L->gu_type, L->down_type);
+    return fn && resident_groups(fn, lds) >= a.H / kFusedRows;
+}
+
+int launch_fused(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t st) {
+    const size_t lds = fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type));
+    LayerArgs arg = a;
+    void *args[] = {&arg};
+    const hipError_t e = hipLaunchKernel(fused_kernel(L->gu_type, L->down_type), dim3((unsigned) (a.H / kFusedRows)),
+                                         dim3(kQThreads), args, lds, st);
+    if (e != hipSuccess) return host::set_error(host::ERR_LAUNCH, "moe fused layer: %s", hipGetErrorString(e));
+    return host::check_launch("moe fused layer");
+}
+
 int by_type_gate_up(int t, const LayerArgs &a, hipStream_t st) {
     switch (t) {
         case T_Q3_K: return dispatch_gate_up<T_Q3_K>(a, st);
@@ -981,10 +1290,10 @@ int by_type_down(int t, const LayerArgs &a, hipStream_t st) {
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
-constexpr int kSections = 10;
+constexpr int kSections = 11;
 
 // Byte sizes of the workspace sections: 0 logits, 1 xq, 2 ids, 3 w, 4 act, 5 escale (documented in fns_hip.h),
-// then internal: 6 xpack, 7 apack, 8 blk_amax, 9 dptr.
+// then internal: 6 xpack, 7 apack, 8 blk_amax, 9 dptr, 10 sync.
 void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     const size_t hpad = (size_t) host::pad512(L->hidden), fpad = (size_t) host::pad512(L->inter);
     const size_t ch = (size_t) n_tok * L->k;
@@ -998,6 +1307,7 @@ void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     sizes[7] = ch * img_bytes((int) fpad);
     sizes[8] = ch * (fpad / 32) * 4;
     sizes[9] = ch * 8;
+    sizes[10] = (size_t) kSyncLines * kSyncStride * 4;
 }
 
 }  // namespace
@@ -1076,7 +1386,9 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     a.apack = sec[7];
     a.blk_amax = (float *) sec[8];
     a.dptr = (const uint8_t **) sec[9];
+    a.sync = (int *) sec[10];
     a.xq_row_bytes = host::q8_1_row_bytes(L->hidden);
+    a.fused = n_tok == 1 && fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type)) > 0;
     return host::OK;
 }
 
@@ -1087,8 +1399,9 @@ static int launch_stage(const FnsMoeLayer *L, const LayerArgs &a, int stage, hip
         hipLaunchKernelGGL(k_route_quant, dim3((unsigned) (n_router_wg + chunks * a.T)), dim3(kK1Threads), 0, st, a);
         return host::check_launch("moe route_quant");
     }
-    if (stage == 1) return by_type_gate_up(L->gu_type, a, st);
-    if (stage == 2) return by_type_down(L->down_type, a, st);
+    // n_tok = 1 shapes that fit take the fused kernel as stage 1; stage 2 then has nothing left to do
+    if (stage == 1) return use_fused(L, a) ? launch_fused(L, a, st) : by_type_gate_up(L->gu_type, a, st);
+    if (stage == 2) return use_fused(L, a) ? host::OK : by_type_down(L->down_type, a, st);
     return host::set_error(host::ERR_SHAPE, "moe_layer: stage must be 0 (router), 1 (gate/up) or 2 (down)");
 }
 
