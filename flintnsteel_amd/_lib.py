@@ -49,6 +49,13 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_moe_layer": [_P, _P, _P, _P, _I, _P, _SZ, _P],
     "fns_hip_moe_layer_profiled": [_P, _P, _P, _P, _I, _P, _SZ, _P, _P],
     "fns_hip_moe_layer_stage": [_P, _I, _P, _P, _P, _I, _P, _SZ, _P],
+    "fns_hip_mmq_q8_1_bytes": [_I64, _I64],
+    "fns_hip_mmq_bounds_bytes": [_I64],
+    "fns_hip_mmq": [_I, _P, _I64, _I64, _P, _I64, _P, _P, _P],
+    "fns_hip_mmq_experts": [_I, _P, _SZ, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P, _P],
+    "fns_hip_mmq_compact": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P],
+    "fns_hip_moe_prefill_workspace": [_P, _I64, _P, _P],
+    "fns_hip_moe_prefill": [_P, _P, _P, _P, _I64, _P, _SZ, _P],
     "fns_hip_fill_normal": [_P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F, _F, _P],
     "fns_hip_quantize_weights": [_I, _P, _P, _I64, _I64, _P],
     "fns_hip_selftest_lanes": [_P, _P],
@@ -56,6 +63,8 @@ SIGNATURES: dict[str, list] = {
 _RESTYPE = {
     "fns_hip_last_error": ctypes.c_char_p,
     "fns_hip_q8_1_row_bytes": _SZ,
+    "fns_hip_mmq_q8_1_bytes": _SZ,
+    "fns_hip_mmq_bounds_bytes": _SZ,
 }
 
 _lib = None

@@ -130,4 +130,33 @@ int fns_hip_quantize_weights(int type, const float *x, void *out, int64_t nrows,
 
 int fns_hip_selftest_lanes(int *bad_mask, void *stream) { return impl::selftest_lanes(bad_mask, S(stream)); }
 
+
+size_t fns_hip_mmq_q8_1_bytes(int64_t ncols, int64_t nrows) { return impl::mmq_q8_1_bytes(ncols, nrows); }
+size_t fns_hip_mmq_bounds_bytes(int64_t n_expert) { return impl::mmq_bounds_bytes(n_expert); }
+
+int fns_hip_mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq,
+                float *dst, void *stream) {
+    return impl::mmq(type, w, ncols, nrows, x, n_tok, xq, dst, S(stream));
+}
+
+int fns_hip_mmq_experts(int type, const void *const *table, size_t off, int64_t ncols, int64_t nrows, int64_t n_expert,
+                        const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
+                        int32_t *ids_src1, int32_t *ids_dst, int32_t *expert_bounds, void *xq, float *dst, void *stream) {
+    return impl::mmq_experts(type, (const char *const *) table, off, ncols, nrows, n_expert, x, x_rows_per_tok, n_tok,
+                             ids, n_used, ids_src1, ids_dst, expert_bounds, xq, dst, S(stream));
+}
+
+int fns_hip_mmq_compact(const int32_t *ids, int64_t n_tok, int64_t n_used, int64_t n_expert, int64_t x_rows_per_tok,
+                        int32_t *ids_src1, int32_t *ids_dst, int32_t *expert_bounds, void *stream) {
+    return impl::mmq_compact(ids, n_tok, n_used, n_expert, x_rows_per_tok, ids_src1, ids_dst, expert_bounds, S(stream));
+}
+
+int fns_hip_moe_prefill_workspace(const FnsMoeLayer *layer, int64_t n_tok, size_t *offsets, size_t *total_bytes) {
+    return impl::moe_prefill_workspace(layer, n_tok, offsets, total_bytes);
+}
+
+int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int64_t n_tok,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+    return impl::moe_prefill(layer, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream));
+}
 }  // extern "C"

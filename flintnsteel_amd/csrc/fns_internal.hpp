@@ -48,6 +48,25 @@ int moe_layer(const FnsMoeLayer *L, const float *x, const float *x_resid, float 
 int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float *x_resid, float *out, int n_tok,
                     void *ws, size_t ws_bytes, hipStream_t st);
 
+size_t mmq_image_bytes(int64_t ncols);
+size_t mmq_q8_1_bytes(int64_t ncols, int64_t nrows);
+size_t mmq_bounds_bytes(int64_t n_expert);
+int mmq_quant_image(const float *x, int64_t ncols, int64_t rows, void *xpack, hipStream_t st);
+int mmq_compact(const int32_t *ids, int64_t n_tok, int64_t k, int64_t n_expert, int64_t x_rows_per_tok,
+                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, hipStream_t st);
+int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t off_b, bool glu, int64_t ncols,
+                     int64_t nrows, int64_t n_expert, const void *xpack, int64_t n_pairs, const int32_t *ids_src1,
+                     const int32_t *ids_dst, const int32_t *bounds, float *dst, void *out_pack, float *act_out,
+                     hipStream_t st);
+int mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq, float *dst,
+        hipStream_t st);
+int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, int64_t n_expert,
+                const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
+                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, void *xq, float *dst, hipStream_t st);
+int moe_prefill_workspace(const FnsMoeLayer *L, int64_t n_tok, size_t *offsets, size_t *total);
+int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int64_t n_tok, void *ws,
+                size_t ws_bytes, hipStream_t st);
+
 int fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t st);
 int quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, hipStream_t st);
 

@@ -38,7 +38,7 @@ using namespace fns::dev;
 
 // Phase timestamps for tuning builds (-DFNS_PROBE): FNS_MARK(kernel, workgroup, point) records the 100 MHz wall clock.
 #ifdef FNS_PROBE
-__device__ unsigned long long g_probe[3][4096][6];
+__device__ unsigned long long g_probe[3][4096][16];
 #define FNS_MARK(k, wg, i) \
     do { \
         if (threadIdx.x == 0) g_probe[k][wg][i] = wall_clock64(); \
@@ -65,6 +65,7 @@ struct LayerArgs {
     int gating, norm, guard;
     int router_dtype;
     const void *router_w;
+    const float *router_bias;  // [NE] or null: added to the logits
     const char *const *table;
     int64_t gate_off, up_off, down_off;
     const float *x;        // [T][H]
@@ -120,32 +121,53 @@ __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
         const int r = blockIdx.x * kK1Rows + sub;
         float s[kMaxTok] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (r < a.NE) {
-            for (int i = t256; i < H / 4; i += 256) {
-                float4 wv;
-                if (a.router_dtype == T_BF16) {
-                    const uint2 pk = ((const uint2 *) ((const uint16_t *) a.router_w + (size_t) r * H))[i];
-                    wv = make_float4(bf16f(pk.x & 0xffff), bf16f(pk.x >> 16), bf16f(pk.y & 0xffff), bf16f(pk.y >> 16));
-                } else {
-                    wv = ((const float4 *) ((const float *) a.router_w + (size_t) r * H))[i];
+            // four 16-byte pieces of the row per lane per pass, every load of a pass issued before the first use
+            for (int i0 = t256; i0 < H / 4; i0 += 4 * 256) {
+                float4 wv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int i = i0 + 256 * u;
+                    if (i < H / 4) {
+                        if (a.router_dtype == T_BF16) {
+                            const uint2 pk = ((const uint2 *) ((const uint16_t *) a.router_w + (size_t) r * H))[i];
+                            wv[u] = make_float4(bf16f(pk.x & 0xffff), bf16f(pk.x >> 16), bf16f(pk.y & 0xffff),
+                                                bf16f(pk.y >> 16));
+                        } else {
+                            wv[u] = ((const float4 *) ((const float *) a.router_w + (size_t) r * H))[i];
+                        }
+                    } else {
+                        wv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    }
                 }
 #pragma unroll
                 for (int t = 0; t < kMaxTok; ++t) {
                     if (t < T) {
-                        const float4 xv = ((const float4 *) (a.x + (size_t) t * H))[i];
-                        s[t] += wv.x * xv.x + wv.y * xv.y + wv.z * xv.z + wv.w * xv.w;
+                        float4 xv[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const int i = i0 + 256 * u;
+                            xv[u] = i < H / 4 ? ((const float4 *) (a.x + (size_t) t * H))[i]
+                                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            s[t] += wv[u].x * xv[u].x + wv[u].y * xv[u].y + wv[u].z * xv[u].z + wv[u].w * xv[u].w;
                     }
                 }
             }
         }
 #pragma unroll
         for (int t = 0; t < kMaxTok; ++t) {
-            const float v = lanes_sum<64>(s[t]);
-            if (t256 % 64 == 0) red[sub][t256 / 64][t] = v;
+            if (t < T) {
+                const float v = lanes_sum<64>(s[t]);
+                if (t256 % 64 == 0) red[sub][t256 / 64][t] = v;
+            }
         }
         __syncthreads();
-        if (t256 < T && r < a.NE)
-            a.logits[(size_t) t256 * a.NE + r] =
-                (red[sub][0][t256] + red[sub][1][t256]) + (red[sub][2][t256] + red[sub][3][t256]);
+        if (t256 < T && r < a.NE) {
+            const float lg = (red[sub][0][t256] + red[sub][1][t256]) + (red[sub][2][t256] + red[sub][3][t256]);
+            a.logits[(size_t) t256 * a.NE + r] = a.router_bias ? lg + a.router_bias[r] : lg;
+        }
         FNS_MARK(0, blockIdx.x, 3);
         return;
     }
@@ -891,6 +913,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     if (tid == 0) s_fail = 0;
     dma_waves_from<kQWaves>(s_x, a.xpack, xbytes, 1);
     if (wave != 0) dma_wait();
+    FNS_MARK(1, blockIdx.x, 4);
     route_topk_block<kQThreads>(a.logits, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
     if (blockIdx.x == 0 && tid < K) publish_route(a, rs, 0, tid);
     if (tid < K) s_w[tid] = route_weight(rs.pv, K, a.norm, tid);
@@ -935,6 +958,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
                 accg += quarter_dot<TGU, Any2>(wb + off, img, bb, qt);
             }
         }
+        FNS_MARK(1, blockIdx.x, 5);
         float v = lanes_sum<32>(acc);
         const float gs = lanes_sum<32>(accg);
         v += 0.0f;  // fused-GLU epilogue with zero biases (reference src/ggml/ggml_mmvq.cu:240-247)
@@ -944,6 +968,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
             store_dev(a.act + (size_t) c * F + row, v);
         }
         __syncthreads();
+        FNS_MARK(1, blockIdx.x, 6);
         if (wave == 0) {  // the 32 rows form one Q8_1 block (lanes 0-31; lanes 32-63 quantise zeros, store nothing)
             const int i = u * kGuRows + lane64 % 32;
             const Q8Lane r = q8_1_lane(lane64 < 32 ? s_act[lane64] : 0.0f);
@@ -965,6 +990,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
                 if (lane64 % 16 == 0) store_dev(dg + fpad / 32 + i / 16, dh * (float) r.qsum16);
             }
         }
+        FNS_MARK(1, blockIdx.x, 7);
         dma_wait();  // this wave's device-coherent stores have completed
     }
     __syncthreads();
@@ -996,7 +1022,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         }
     }
     __syncthreads();
-    FNS_MARK(2, blockIdx.x, 0);
+    FNS_MARK(1, blockIdx.x, 8);
     // 5. act images (device-scope LDS-DMA) and the F16 guard: a slot whose scale is not 1 is divided and re-quantised
     //    (reference src/kernels.cu:554-577)
     for (int p = wave * 1024; p < K * fbytes; p += kQThreads * 16)
@@ -1006,6 +1032,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
                 (__attribute__((address_space(3))) void *) (s_a + p), 16, 0, kCpolDevice);
     dma_wait();
     __syncthreads();
+    FNS_MARK(1, blockIdx.x, 9);
     if (a.guard) {
         for (int ch = wave; ch < K; ch += kQWaves) {
             float m = 0.0f;
@@ -1034,7 +1061,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         if (blockIdx.x == 0) a.escale[tid] = 1.0f;
     }
     __syncthreads();
-    FNS_MARK(2, blockIdx.x, 1);
+    FNS_MARK(1, blockIdx.x, 10);
     // 6. down rows (16 lanes per (row, slot) item, as k_down_q), then the combine in slot order
     const int lane16 = tid % 16;
     for (int it = tid / 16; it < kFusedRows * K; it += kQThreads / 16) {
@@ -1050,7 +1077,9 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         acc = lanes_sum<16>(acc);
         if (lane16 == 0) s_dexp[ch][rr] = acc;
     }
+    FNS_MARK(1, blockIdx.x, 11);
     __syncthreads();
+    FNS_MARK(1, blockIdx.x, 12);
     if (tid < kFusedRows) {
         const int r = r0 + tid;
         float moe = (s_dexp[0][tid] * s_e[0]) * s_w[0];
@@ -1060,7 +1089,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         if (s_fail) o = __builtin_nanf("");
         a.out[r] = o;
     }
-    FNS_MARK(2, blockIdx.x, 4);
+    FNS_MARK(1, blockIdx.x, 13);
 }
 
 // Fused-kernel plan for one layer shape (n_tok = 1): LDS bytes, or 0 when the shape does not fit the scheme.
@@ -1369,6 +1398,7 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     a.guard = L->guard;
     a.router_dtype = L->router_dtype;
     a.router_w = L->router_w;
+    a.router_bias = L->router_bias;
     a.table = (const char *const *) L->table;
     a.gate_off = (int64_t) L->gate_off;
     a.up_off = (int64_t) L->up_off;
@@ -1437,7 +1467,7 @@ extern "C" int fns_probe_read(void *host) {
     return (int) hipMemcpyFromSymbol(host, HIP_SYMBOL(fns::g_probe), sizeof(fns::g_probe));
 }
 extern "C" int fns_probe_clear() {
-    static unsigned long long z[3][4096][6];
+    static unsigned long long z[3][4096][16];
     return (int) hipMemcpyToSymbol(HIP_SYMBOL(fns::g_probe), z, sizeof(z));
 }
 #endif

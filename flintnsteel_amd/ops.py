@@ -241,7 +241,7 @@ class MoeLayerDesc(ctypes.Structure):
         ("router_dtype", ctypes.c_int), ("router_w", ctypes.c_void_p),
         ("gu_type", ctypes.c_int), ("down_type", ctypes.c_int),
         ("table", ctypes.c_void_p), ("gate_off", ctypes.c_size_t), ("up_off", ctypes.c_size_t),
-        ("down_off", ctypes.c_size_t),
+        ("down_off", ctypes.c_size_t), ("router_bias", ctypes.c_void_p),
     ]
 
 
@@ -252,11 +252,13 @@ class MoeLayer:
     """One MoE FFN layer resident in HBM: fp32/bf16 router + expert slots, run by fns_hip_moe_layer."""
 
     def __init__(self, router_w: torch.Tensor, slots: ExpertSlots, gu_type: int, down_type: int, hidden: int,
-                 inter: int, k: int, gating: int = GATING_SOFTMAX, norm: bool = True, guard: bool = False):
-        self.router_w, self.slots = router_w, slots
+                 inter: int, k: int, gating: int = GATING_SOFTMAX, norm: bool = True, guard: bool = False,
+                 router_bias: torch.Tensor | None = None):
+        self.router_w, self.slots, self.router_bias = router_w, slots, router_bias
         self.desc = MoeLayerDesc(hidden, inter, slots.n_expert, k, gating, int(norm), int(guard),
                                  _dtype_code(router_w), router_w.data_ptr(), gu_type, down_type,
-                                 slots.table.data_ptr(), slots.gate_off, slots.up_off, slots.down_off)
+                                 slots.table.data_ptr(), slots.gate_off, slots.up_off, slots.down_off,
+                                 router_bias.data_ptr() if router_bias is not None else None)
 
     def workspace_layout(self, n_tok: int):
         offs = (ctypes.c_size_t * 6)()
@@ -304,6 +306,86 @@ class MoeLayer:
             n = int(np.prod(shape)) * torch.tensor([], dtype=dt).element_size()
             out[name] = ws[off:off + n].view(dt).view(*shape)
         return out
+
+
+PREFILL_SECTIONS = ("logits", "ids", "w", "xpack", "apack", "dexp")
+
+
+class MoePrefill:
+    """Prefill (batched) form of a MoeLayer: fns_hip_moe_prefill over n_tok tokens."""
+
+    def __init__(self, layer: MoeLayer):
+        self.layer = layer
+
+    def workspace_layout(self, n_tok: int):
+        offs = (ctypes.c_size_t * 6)()
+        total = ctypes.c_size_t()
+        call("fns_hip_moe_prefill_workspace", ctypes.byref(self.layer.desc), n_tok, offs, ctypes.byref(total))
+        return list(offs), total.value
+
+    def workspace(self, n_tok: int) -> torch.Tensor:
+        return torch.zeros(self.workspace_layout(n_tok)[1], dtype=torch.uint8, device="cuda")
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
+                 x_resid: torch.Tensor | None = None) -> torch.Tensor:
+        x = x.contiguous()
+        n_tok = x.numel() // self.layer.desc.hidden
+        out = torch.empty_like(x) if out is None else out
+        ws = self.workspace(n_tok) if ws is None else ws
+        call("fns_hip_moe_prefill", ctypes.byref(self.layer.desc), _p(x), _p(x_resid), _p(out), n_tok, _p(ws),
+             ws.numel(), _s())
+        return out
+
+    def trace(self, ws: torch.Tensor, n_tok: int) -> dict:
+        offs, _ = self.workspace_layout(n_tok)
+        d = self.layer.desc
+        spec = {"logits": (torch.float32, (n_tok, d.n_expert)), "ids": (torch.int32, (n_tok, d.k)),
+                "w": (torch.float32, (n_tok, d.k)), "dexp": (torch.float32, (n_tok, d.k, d.hidden))}
+        out = {}
+        for name, (dt, shape) in spec.items():
+            off = offs[PREFILL_SECTIONS.index(name)]
+            n = int(np.prod(shape)) * torch.tensor([], dtype=dt).element_size()
+            out[name] = ws[off: off + n].view(dt).view(*shape)
+        return out
+
+
+def mmq_q8_1_bytes(ncols: int, nrows: int) -> int:
+    return int(lib().fns_hip_mmq_q8_1_bytes(ncols, nrows))
+
+
+def mmq(qtype: int, w: torch.Tensor, ncols: int, nrows: int, x: torch.Tensor) -> torch.Tensor:
+    x = x.contiguous()
+    n_tok = x.numel() // ncols
+    xq = torch.zeros(mmq_q8_1_bytes(ncols, n_tok), dtype=torch.uint8, device=x.device)
+    dst = _empty_f32(n_tok, nrows, like=x)
+    call("fns_hip_mmq", qtype, _p(w), ncols, nrows, _p(x), n_tok, _p(xq), _p(dst), _s())
+    return dst
+
+
+def mmq_compact(ids: torch.Tensor, n_expert: int, x_rows_per_tok: int = 1):
+    """-> (bounds [n_expert + 1], ids_src1, ids_dst) of the stable expert sort."""
+    n_tok, k = ids.shape
+    src = torch.empty(n_tok * k, dtype=torch.int32, device=ids.device)
+    dst = torch.empty_like(src)
+    bounds = torch.empty(int(lib().fns_hip_mmq_bounds_bytes(n_expert)) // 4, dtype=torch.int32, device=ids.device)
+    call("fns_hip_mmq_compact", _p(ids.contiguous()), n_tok, k, n_expert, x_rows_per_tok, _p(src), _p(dst),
+         _p(bounds), _s())
+    return bounds[: n_expert + 1], src, dst
+
+
+def mmq_experts(qtype: int, table: torch.Tensor, off: int, ncols: int, nrows: int, n_expert: int, x: torch.Tensor,
+                x_rows_per_tok: int, ids: torch.Tensor) -> torch.Tensor:
+    """dst [n_tok][n_used][nrows] = W_e . q8_1(x[t][j % x_rows_per_tok])."""
+    n_tok, n_used = ids.shape
+    x = x.contiguous()
+    src = torch.empty(n_tok * n_used, dtype=torch.int32, device=x.device)
+    dst_ids = torch.empty_like(src)
+    bounds = torch.empty(int(lib().fns_hip_mmq_bounds_bytes(n_expert)) // 4, dtype=torch.int32, device=x.device)
+    xq = torch.zeros(mmq_q8_1_bytes(ncols, n_tok * x_rows_per_tok), dtype=torch.uint8, device=x.device)
+    dst = _empty_f32(n_tok, n_used, nrows, like=x)
+    call("fns_hip_mmq_experts", qtype, _p(table), off, ncols, nrows, n_expert, _p(x), x_rows_per_tok, n_tok,
+         _p(ids.contiguous()), n_used, _p(src), _p(dst_ids), _p(bounds), _p(xq), _p(dst), _s())
+    return dst
 
 
 def fill_normal(out: torch.Tensor, seed: int, offset: int = 0, mean: float = 0.0, std: float = 1.0) -> torch.Tensor:

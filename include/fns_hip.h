@@ -118,6 +118,7 @@ typedef struct FnsMoeLayer {
     int gu_type, down_type;
     const void *const *table;
     size_t gate_off, up_off, down_off;
+    const float *router_bias; /* NULL or f32 [n_expert], added to the logits before gating (selection and weights) */
 } FnsMoeLayer;
 
 int fns_hip_moe_workspace_layout(const FnsMoeLayer *layer, int n_tok, size_t *offsets, size_t *total_bytes);
@@ -132,6 +133,38 @@ int fns_hip_moe_layer_profiled(const FnsMoeLayer *layer, const float *x, const f
  * per-stage tracing (the reference's FNS_TRACE nodes, src/engine.cu:590-599) and per-kernel timing. */
 int fns_hip_moe_layer_stage(const FnsMoeLayer *layer, int stage, const float *x, const float *x_resid, float *out,
                             int n_tok, void *workspace, size_t workspace_bytes, void *stream);
+
+/* --- prefill / batched expert GEMM (MMQ) ---
+ * Q8_1 activation rows for the MMQ path are kept as "images" (int8 values, then per-32 scale and scaled sums in
+ * f32): fns_hip_mmq_q8_1_bytes(ncols, nrows) bytes hold nrows of them. */
+/* include/fns/ggml_kernels.h:53-54 mmq_q8_1_bytes */
+size_t fns_hip_mmq_q8_1_bytes(int64_t ncols, int64_t nrows);
+/* bytes of MmqIdsScratch::expert_bounds for n_expert experts (bounds + tile-group prefix) */
+size_t fns_hip_mmq_bounds_bytes(int64_t n_expert);
+/* include/fns/ggml_kernels.h:56-58 mmq: dst[t][nrows] = W . q8_1(x[t]), x f32 [n_tok][ncols]; xq scratch of
+ * fns_hip_mmq_q8_1_bytes(ncols, n_tok) bytes. ncols a multiple of 256, nrows of 64. */
+int fns_hip_mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq,
+                float *dst, void *stream);
+/* include/fns/ggml_kernels.h:60-69 MmqIdsScratch + mmq_experts: dst[t][j][nrows] = W_e . q8_1(x[t][j % x_rows_per_tok]),
+ * e = ids[t][j]; expert e's matrix at table[e] + off. Scratch: ids_src1 / ids_dst n_tok * n_used int32, expert_bounds
+ * fns_hip_mmq_bounds_bytes(n_expert), xq fns_hip_mmq_q8_1_bytes(ncols, n_tok * x_rows_per_tok). */
+int fns_hip_mmq_experts(int type, const void *const *table, size_t off, int64_t ncols, int64_t nrows, int64_t n_expert,
+                        const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
+                        int32_t *ids_src1, int32_t *ids_dst, int32_t *expert_bounds, void *xq, float *dst, void *stream);
+/* Expert-id compaction alone (ggml mm_ids_helper semantics; reference src/ggml/ggml_mmq.cu:110-111): pairs
+ * p = t * n_used + j sorted by expert, stable; ids_dst[q] = p, ids_src1[q] = (x_rows_per_tok == 1 ? t : p),
+ * expert_bounds[e] = first sorted position of expert e (e <= n_expert), followed by the tile-group prefix. */
+int fns_hip_mmq_compact(const int32_t *ids, int64_t n_tok, int64_t n_used, int64_t n_expert, int64_t x_rows_per_tok,
+                        int32_t *ids_src1, int32_t *ids_dst, int32_t *expert_bounds, void *stream);
+
+/* Prefill MoE layer for n_tok tokens (n_tok * k <= 65536): the MoE section of the reference's Engine::prefill_chunk
+ * (src/engine.cu:340-357: batch router, route_topk_batch, mmq_experts gate / up, swiglu, amax_guard, mmq_experts down,
+ * moe_combine_batch), out[t] = sum_j w[t][j] * e[t][j] * down_e(q8_1(act[t][j] / e[t][j])) (+ x_resid[t]).
+ * workspace: fns_hip_moe_prefill_workspace() bytes; sections (byte offsets in offsets[6]): 0 logits f32 [n_tok][n_expert],
+ * 1 ids i32 [n_tok][k], 2 w f32 [n_tok][k], 3 x images, 4 act images [n_tok * k], 5 down outputs f32 [n_tok][k][hidden]. */
+int fns_hip_moe_prefill_workspace(const FnsMoeLayer *layer, int64_t n_tok, size_t *offsets, size_t *total_bytes);
+int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int64_t n_tok,
+                        void *workspace, size_t workspace_bytes, void *stream);
 
 /* --- seeded synthetic data on the device (benchmarks and large tests) ---
  * out[i] = mean + std * N(0,1), Philox-4x32-10 counter (offset + i) / 4 and Box-Muller; offset % 4 == 0. */
