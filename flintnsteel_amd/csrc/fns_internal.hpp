@@ -35,6 +35,8 @@ int mmvq_experts(int type, const char *const *table, size_t off, int64_t ncols, 
                  int64_t n_xq, const int32_t *ids, int64_t n_ids, float *dst, hipStream_t st);
 
 int gemv_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int cols, hipStream_t st);
+int gemm_router_bias(int dtype, const void *w, const float *bias, const float *x, float *y, int ncols, int nrows,
+                     int n_tok, hipStream_t st);
 int gemm_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int n_tok, hipStream_t st);
 int route_topk(const float *logits, int32_t *ids, float *w, int n_expert, int k, int n_tok, int gating, int norm,
                hipStream_t st);

@@ -39,7 +39,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kMmqThreads = 256;   // 4 waves
 constexpr int kMmqRows = 64;       // weight rows per workgroup (16 per wave)
-constexpr int kMmqTok = 128;       // activation rows per workgroup (8 MFMA tiles of 16)
+constexpr int kMmqTok = 64;        // activation rows per workgroup (4 MFMA tiles of 16)
 constexpr int kMmqTiles = kMmqTok / 16;
 constexpr int kMmqStride = 288;    // LDS bytes per staged activation row (256 + 32: spreads the A-fragment reads)
 constexpr int kCompactThreads = 1024;
@@ -241,20 +241,27 @@ template <int T> constexpr int groups_of() { return (T == T_Q6_K || T == T_Q3_K)
 
 template <int T> __device__ __forceinline__ SubB<T> sub_b(const WFrag<T> &f, int s, int kg);
 
+// Sub-block index s may be a runtime value: fragments and scale bytes are picked with selects and shifts (no
+// dynamically indexed register arrays).
+__device__ __forceinline__ uint2 sel4(uint2 a, uint2 b, uint2 c, uint2 d, int i) { return i == 0 ? a : i == 1 ? b : i == 2 ? c : d; }
+__device__ __forceinline__ uint32_t byte_dyn(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+// 6-bit scale and min of sub-block s of a Q4_K / Q5_K block (ggml get_scale_min_k4); h.y, h.z, h.w = scales[0..11].
 __device__ __forceinline__ void k4_sc_m(const uint4 &h, int s, int &sc, int &m) {
-    const uint8_t *b = (const uint8_t *) &h + 4;  // scales[12]
+    const int i = s & 3;
     if (s < 4) {
-        sc = b[s] & 63;
-        m = b[s + 4] & 63;
+        sc = (int) (byte_dyn(h.y, i) & 63u);
+        m = (int) (byte_dyn(h.z, i) & 63u);
     } else {
-        sc = (b[s + 4] & 0xF) | ((b[s - 4] >> 6) << 4);
-        m = (b[s + 4] >> 4) | ((b[s] >> 6) << 4);
+        const uint32_t b8 = byte_dyn(h.w, i);
+        sc = (int) ((b8 & 0xFu) | ((byte_dyn(h.y, i) >> 6) << 4));
+        m = (int) ((b8 >> 4) | ((byte_dyn(h.z, i) >> 6) << 4));
     }
 }
 
 template <> __device__ __forceinline__ SubB<T_Q4_K> sub_b<T_Q4_K>(const WFrag<T_Q4_K> &f, int s, int kg) {
     SubB<T_Q4_K> r;
-    const uint2 q = f.q[s >> 1];
+    const uint2 q = sel4(f.q[0], f.q[1], f.q[2], f.q[3], s >> 1);
     const int sh = 4 * (s & 1);
     r.b[0] = pack_long((q.x >> sh) & kLo4, (q.y >> sh) & kLo4);
     int sc, m;
@@ -265,7 +272,7 @@ template <> __device__ __forceinline__ SubB<T_Q4_K> sub_b<T_Q4_K>(const WFrag<T_
 }
 template <> __device__ __forceinline__ SubB<T_Q5_K> sub_b<T_Q5_K>(const WFrag<T_Q5_K> &f, int s, int kg) {
     SubB<T_Q5_K> r;
-    const uint2 q = f.q[s >> 1];
+    const uint2 q = sel4(f.q[0], f.q[1], f.q[2], f.q[3], s >> 1);
     const int sh = 4 * (s & 1);
     r.b[0] = pack_long(((q.x >> sh) & kLo4) | (((f.qh.x >> s) & 0x01010101u) << 4),
                        ((q.y >> sh) & kLo4) | (((f.qh.y >> s) & 0x01010101u) << 4));
@@ -280,7 +287,7 @@ template <> __device__ __forceinline__ SubB<T_Q5_K> sub_b<T_Q5_K>(const WFrag<T_
 template <> __device__ __forceinline__ SubB<T_Q6_K> sub_b<T_Q6_K>(const WFrag<T_Q6_K> &f, int s, int kg) {
     SubB<T_Q6_K> r;
     const int n = s >> 2, qq = s & 3;
-    const uint2 ql = f.ql[2 * n + (qq & 1)], qh = f.qh[n];
+    const uint2 ql = sel4(f.ql[0], f.ql[1], f.ql[2], f.ql[3], 2 * n + (qq & 1)), qh = n == 0 ? f.qh[0] : f.qh[1];
     const int shl = 4 * (qq >> 1), shh = 2 * qq;
     const uint32_t lo = bytes_sub<32>((int) (((ql.x >> shl) & kLo4) | (((qh.x >> shh) & 0x03030303u) << 4)));
     const uint32_t hi = bytes_sub<32>((int) (((ql.y >> shl) & kLo4) | (((qh.y >> shh) & 0x03030303u) << 4)));
@@ -288,10 +295,10 @@ template <> __device__ __forceinline__ SubB<T_Q6_K> sub_b<T_Q6_K>(const WFrag<T_
     r.b[0] = kg < 2 ? v : 0;
     r.b[1] = kg < 2 ? 0 : v;
     const float d = half_to_float(f.d);
-    const int g0 = 8 * n + 2 * qq;
+    const int g0 = 8 * n + 2 * qq;  // even: both groups in one word
     const uint32_t w0 = word(f.sc, g0 >> 2);
-    r.ws[0] = d * (float) (int8_t) ((w0 >> (8 * (g0 & 3))) & 0xffu);
-    r.ws[1] = d * (float) (int8_t) ((w0 >> (8 * ((g0 + 1) & 3))) & 0xffu);
+    r.ws[0] = d * (float) (int8_t) byte_dyn(w0, g0 & 3);
+    r.ws[1] = d * (float) (int8_t) byte_dyn(w0, (g0 & 3) + 1);
     r.wm = 0.0f;
     return r;
 }
@@ -300,7 +307,7 @@ template <> __device__ __forceinline__ SubB<T_Q6_K> sub_b<T_Q6_K>(const WFrag<T_
 template <> __device__ __forceinline__ SubB<T_Q3_K> sub_b<T_Q3_K>(const WFrag<T_Q3_K> &f, int s, int kg) {
     SubB<T_Q3_K> r;
     const int n = s >> 2, j = s & 3;
-    const uint2 q = f.qs[n];
+    const uint2 q = n == 0 ? f.qs[0] : f.qs[1];
     const int hs = 4 * n + j;
     const uint32_t lo = bytes_sub<4>((int) (((q.x >> (2 * j)) & 0x03030303u) | (((f.hm.x >> hs) & 0x01010101u) << 2)));
     const uint32_t hi = bytes_sub<4>((int) (((q.y >> (2 * j)) & 0x03030303u) | (((f.hm.y >> hs) & 0x01010101u) << 2)));
@@ -308,11 +315,16 @@ template <> __device__ __forceinline__ SubB<T_Q3_K> sub_b<T_Q3_K>(const WFrag<T_
     r.b[0] = kg < 2 ? v : 0;
     r.b[1] = kg < 2 ? 0 : v;
     const float d = half_to_float(f.tail.w >> 16);
+    // tail = block bytes 94..109: scales[i] is tail byte 2 + i
+    const uint32_t hi_w = (f.tail.z >> 16) | (f.tail.w << 16);  // scales[8..11]
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int g = 8 * n + 2 * j + h;
-        const uint32_t lo4 = g < 8 ? (byte_of(f.tail, 2 + g) & 0xFu) : (byte_of(f.tail, 2 + g - 8) >> 4);
-        const uint32_t hi2 = (byte_of(f.tail, 2 + 8 + (g & 3)) >> (2 * (g >> 2))) & 3u;
+        const int lb = (g & 7) + 2;  // tail byte of scales[g & 7]
+        const uint32_t lw = lb < 4 ? f.tail.x : lb < 8 ? f.tail.y : f.tail.z;
+        const uint32_t b = byte_dyn(lw, lb & 3);
+        const uint32_t lo4 = g < 8 ? (b & 0xFu) : (b >> 4);
+        const uint32_t hi2 = (byte_dyn(hi_w, g & 3) >> (2 * (g >> 2))) & 3u;
         r.ws[h] = d * (float) ((int) (lo4 | (hi2 << 4)) - 32);
     }
     r.wm = 0.0f;
@@ -322,13 +334,13 @@ template <> __device__ __forceinline__ SubB<T_Q3_K> sub_b<T_Q3_K>(const WFrag<T_
 // LDS of one workgroup: the activation superblock chunk [kMmqTok][kMmqStride] int8 and its per-sub-block d8 and
 // d8 * sum(q8) transposed to [8][kMmqTok]; reused as the act tile [kMmqTok][kMmqRows] f32 by the GLU epilogue.
 struct alignas(16) MmqLds {
-    uint8_t q[kMmqTok * kMmqStride];
-    float d8[8][kMmqTok];
-    float s8[8][kMmqTok];
+    uint8_t q[2][kMmqTok * kMmqStride];  // double-buffered: chunk kb + 1 lands while chunk kb is computed
+    float d8[2][8][kMmqTok];
+    float s8[2][8][kMmqTok];
     int src[kMmqTok];
     int dst[kMmqTok];
 };
-static_assert(sizeof(float) * kMmqTok * kMmqRows <= kMmqTok * kMmqStride, "act tile fits the chunk buffer");
+static_assert(sizeof(float) * kMmqTok * kMmqRows <= 2 * kMmqTok * kMmqStride, "act tile fits the chunk buffers");
 
 template <int T, bool GLU>
 __global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
@@ -384,46 +396,65 @@ __global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
     if constexpr (GLU) wfrag_load<T>(wb, kg, fb);
     __syncthreads();  // L.src / L.dst
 
-    for (int kb = 0; kb < nb; ++kb) {
-        // stage the chunk: q rows by LDS-DMA (18 pieces of 16 bytes per row: the 256 q bytes + 32 bytes of padding
-        // read from what follows them in the same image row), d8 / d8 * sum(q8) transposed with plain loads
-        const int nrow = ntile * 16;
-        dma_gather_to_lds<kMmqThreads>(L.q, nrow * kMmqStride, [&](int p) {
+    // staging of superblock chunk kb into buffer kb & 1: q rows by LDS-DMA (18 pieces of 16 bytes per row: the 256 q
+    // bytes + 32 bytes of padding read from what follows them in the same image row); d8 and d8 * sum(q8) of the
+    // chunk's 8 sub-blocks through registers (loaded here, stored transposed by store_scales)
+    const int nrow = ntile * 16;
+    auto stage_q = [&](int kb) {
+        dma_gather_to_lds<kMmqThreads>(L.q[kb & 1], nrow * kMmqStride, [&](int p) {
             const int i = p / kMmqStride, o = p % kMmqStride;
             return a.xpack + (size_t) L.src[i] * a.x_img + kb * kImgQRow + o;
         });
+    };
+    float sv[8];
+    auto load_scales = [&](int kb) {
         if (tid < 2 * kMmqTok) {
             const int i = tid >> 1, which = tid & 1;
-            float v[8];
             if (i < cnt) {
                 const float *f = (const float *) (a.xpack + (size_t) L.src[i] * a.x_img + qbytes) +
                                  (which ? npad / 32 + npad / 16 : 0) + 8 * kb;
                 const float4 v0 = *(const float4 *) f, v1 = *(const float4 *) (f + 4);
-                v[0] = v0.x, v[1] = v0.y, v[2] = v0.z, v[3] = v0.w, v[4] = v1.x, v[5] = v1.y, v[6] = v1.z, v[7] = v1.w;
+                sv[0] = v0.x, sv[1] = v0.y, sv[2] = v0.z, sv[3] = v0.w;
+                sv[4] = v1.x, sv[5] = v1.y, sv[6] = v1.z, sv[7] = v1.w;
             } else {
 #pragma unroll
-                for (int s = 0; s < 8; ++s) v[s] = 0.0f;
+                for (int s = 0; s < 8; ++s) sv[s] = 0.0f;
             }
-#pragma unroll
-            for (int s = 0; s < 8; ++s) (which ? L.s8 : L.d8)[s][i] = v[s];
         }
-        // next block's weights in flight while this one is computed
-        if (kb + 1 < nb) {
+    };
+    auto store_scales = [&](int kb) {
+        if (tid < 2 * kMmqTok) {
+            const int i = tid >> 1, which = tid & 1;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) (which ? L.s8[kb & 1] : L.d8[kb & 1])[s][i] = sv[s];
+        }
+    };
+    stage_q(0);
+    load_scales(0);
+    store_scales(0);
+    dma_wait();
+    __syncthreads();
+
+    for (int kb = 0; kb < nb; ++kb) {
+        const int cur = kb & 1;
+        if (kb + 1 < nb) {  // next chunk and next block's weights in flight while this one is computed
+            stage_q(kb + 1);
+            load_scales(kb + 1);
             wfrag_load<T>(wa + (int64_t) (kb + 1) * BB, kg, na);
             if constexpr (GLU) wfrag_load<T>(wb + (int64_t) (kb + 1) * BB, kg, nb2);
         }
-        dma_wait();
-        __syncthreads();
+#pragma unroll 1
+        for (int s2 = 0; s2 < 8; s2 += 2)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int s = s2; s < s2 + 2; ++s) {
             const SubB<T> ba = sub_b<T>(fa, s, kg);
             SubB<T> bu;
             if constexpr (GLU) bu = sub_b<T>(fb, s, kg);
 #pragma unroll
             for (int t = 0; t < kMmqTiles; ++t) {
                 if (t < ntile) {
-                    const long av = *(const long *) (L.q + (t * 16 + jl) * kMmqStride + 32 * s + 8 * kg);
-                    const float4 d8 = *(const float4 *) &L.d8[s][t * 16 + 4 * kg];
+                    const long av = *(const long *) (L.q[cur] + (t * 16 + jl) * kMmqStride + 32 * s + 8 * kg);
+                    const float4 d8 = *(const float4 *) &L.d8[cur][s][t * 16 + 4 * kg];
                     const float dd[4] = {d8.x, d8.y, d8.z, d8.w};
 #pragma unroll
                     for (int g = 0; g < NG; ++g) {
@@ -438,7 +469,7 @@ __global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
                         }
                     }
                     if constexpr (NG == 1) {
-                        const float4 s8 = *(const float4 *) &L.s8[s][t * 16 + 4 * kg];
+                        const float4 s8 = *(const float4 *) &L.s8[cur][s][t * 16 + 4 * kg];
                         const float ss[4] = {s8.x, s8.y, s8.z, s8.w};
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
@@ -449,9 +480,13 @@ __global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
                 }
             }
         }
-        fa = na;
-        if constexpr (GLU) fb = nb2;
-        __syncthreads();  // the chunk buffer is rewritten next iteration
+        if (kb + 1 < nb) {
+            store_scales(kb + 1);
+            fa = na;
+            if constexpr (GLU) fb = nb2;
+        }
+        dma_wait();
+        __syncthreads();  // chunk kb + 1 visible; buffer kb & 1 free for chunk kb + 2
     }
 
     if constexpr (!GLU) {
@@ -465,7 +500,7 @@ __global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
     } else {
         // act = up * silu(gate) (reference src/ggml/ggml_mmvq.cu:240-247 epilogue with zero biases), staged as
         // [token][64 rows] f32, then one Q8_1 block per (token, 32 rows) into the act image rows.
-        float *act = (float *) L.q;
+        float *act = (float *) &L.q[0][0];
 #pragma unroll
         for (int t = 0; t < kMmqTiles; ++t)
 #pragma unroll
@@ -629,14 +664,6 @@ void prefill_sizes(const FnsMoeLayer *L, int64_t T, size_t *sz) {
     sz[9] = L->guard ? (size_t) P * L->inter * 4 : 0;     // f32 act (F16 guard only)
     sz[10] = (size_t) P * 4;                              // escale
 }
-__global__ void k_add_bias(float *logits, const float *bias, int n_expert, int n) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) logits[i] += bias[i % n_expert];
-}
-__global__ void k_fill1(float *p, int n) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) p[i] = 1.0f;
-}
 }  // namespace
 
 int moe_prefill_workspace(const FnsMoeLayer *L, int64_t n_tok, size_t *offsets, size_t *total) {
@@ -676,13 +703,8 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
     const int64_t P = n_tok * L->k;
     const char *const *table = (const char *const *) L->table;
 
-    FNS_TRY(gemm_router(L->router_dtype, L->router_w, x, logits, L->hidden, L->n_expert, (int) n_tok, st));
-    if (L->router_bias) {
-        const int n = (int) (n_tok * L->n_expert);
-        hipLaunchKernelGGL(k_add_bias, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, logits, L->router_bias,
-                           L->n_expert, n);
-        FNS_TRY(host::check_launch("moe_prefill bias"));
-    }
+    FNS_TRY(gemm_router_bias(L->router_dtype, L->router_w, L->router_bias, x, logits, L->hidden, L->n_expert, (int) n_tok,
+                             st));
     FNS_TRY(route_topk(logits, ids, w, L->n_expert, L->k, (int) n_tok, L->gating, L->norm_w, st));
     FNS_TRY(mmq_compact(ids, n_tok, L->k, L->n_expert, 1, src1, dstr, bounds, st));
     FNS_TRY(mmq_quant_image(x, L->hidden, n_tok, sec[3], st));
@@ -691,15 +713,12 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
     if (L->guard) {  // whole-row amax: a second pass over the f32 act rows (reference src/kernels.cu:534-552)
         FNS_TRY(amax_guard(act, escale, L->inter, (int) P, st));
         FNS_TRY(mmq_quant_image(act, L->inter, P, sec[4], st));
-    } else {
-        hipLaunchKernelGGL(k_fill1, dim3((unsigned) ((P + 255) / 256)), dim3(256), 0, st, escale, (int) P);
-        FNS_TRY(host::check_launch("moe_prefill escale"));
     }
-    // down: one act row per (token, slot); the sorted order of gate/up is reused with rows p = t k + j
-    FNS_TRY(mmq_compact(ids, n_tok, L->k, L->n_expert, L->k, src1, dstr, bounds, st));
+    // down: one act row per (token, slot), in the same expert order as gate/up: the sorted rows are the pairs
+    // themselves (activation row = output row = p), so the gate/up sort is reused with ids_dst as the source list
     FNS_TRY(mmq_gemm_experts(L->down_type, table, L->down_off, 0, false, L->inter, L->hidden, L->n_expert, sec[4], P,
-                             src1, dstr, bounds, dexp, nullptr, nullptr, st));
-    return moe_combine(dexp, escale, w, nullptr, x_resid, out, L->hidden, L->k, (int) n_tok, st);
+                             dstr, dstr, bounds, dexp, nullptr, nullptr, st));
+    return moe_combine(dexp, L->guard ? escale : nullptr, w, nullptr, x_resid, out, L->hidden, L->k, (int) n_tok, st);
 }
 
 }  // namespace impl

@@ -63,55 +63,64 @@ __global__ __launch_bounds__(256) void k_gemv_router(const void *__restrict__ w,
             (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
 }
 
-// Batch router GEMM y[t][e] = sum_i W[e][i] x[t][i]: 64 x 64 output tile per workgroup, k-chunks of 16 staged in LDS,
-// 4 x 4 outputs per lane. BF16: W is bf16 and x is rounded to bf16 first (the reference's cuBLAS BF16 path).
+// Batch router GEMM y[t][e] = sum_i W[e][i] x[t][i] (+ bias[e]) on fp32 MFMA (v_mfma_f32_16x16x4_f32): a workgroup
+// computes 16 tokens x 64 experts, wave w the experts e0 + 16 w .. +15. Lane (i = lane % 16, kk = lane / 16) loads 16
+// consecutive columns' worth of A (x row i) and B (W row i) as float4 at column k0 + 4 kk, and MFMA m of the chunk
+// takes element m of both: the four MFMAs cover the 16 columns once (the same permutation of k on both operands).
+// BF16: W is bf16 and x is rounded to bf16 first (the reference's cuBLAS BF16 path, src/prefill_kernels.cu:217-233).
+typedef float v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld4_guard(const float *row, int k, int ncols) {
+    if (k + 3 < ncols) return *(const float4 *) (row + k);
+    float v[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) v[m] = k + m < ncols ? row[k + m] : 0.0f;
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float4 ld4_bf16_guard(const uint16_t *row, int k, int ncols) {
+    float v[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) v[m] = k + m < ncols ? bf16_to_float(row[k + m]) : 0.0f;
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float round_bf16(float v) {
+    uint32_t b = __builtin_bit_cast(uint32_t, v);
+    b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+    return __builtin_bit_cast(float, b);
+}
 template <bool BF16>
-__global__ __launch_bounds__(256) void k_gemm_router(const void *__restrict__ w, const float *__restrict__ x,
-                                                     float *__restrict__ y, int ncols, int nrows, int n_tok) {
-    __shared__ float xs[16][68], ws[16][68];
-    const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
-    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < ncols; k0 += 16) {
-        for (int i = threadIdx.x; i < 64 * 16; i += 256) {
-            const int rr = i / 16, kk = i % 16;
-            const int t = t0 + rr, e = e0 + rr, k = k0 + kk;
-            float xv = (t < n_tok && k < ncols) ? x[(size_t) t * ncols + k] : 0.0f;
-            float wv = 0.0f;
-            if (e < nrows && k < ncols) {
-                if constexpr (BF16) wv = bf16_to_float(((const uint16_t *) w)[(size_t) e * ncols + k]);
-                else wv = ((const float *) w)[(size_t) e * ncols + k];
-            }
-            if constexpr (BF16) {  // round x to bf16, nearest even
-                uint32_t b = __builtin_bit_cast(uint32_t, xv);
-                b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
-                xv = __builtin_bit_cast(float, b);
-            }
-            xs[kk][rr] = xv;
-            ws[kk][rr] = wv;
+__global__ __launch_bounds__(256) void k_gemm_router(const void *__restrict__ w, const float *__restrict__ bias,
+                                                     const float *__restrict__ x, float *__restrict__ y, int ncols,
+                                                     int nrows, int n_tok) {
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, il = lane % 16, kk = lane / 16;
+    const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 64 + wave * 16;
+    const int ta = min(t0 + il, n_tok - 1), ea = min(e0 + il, nrows - 1);  // clamped rows (results discarded)
+    const float *xr = x + (size_t) ta * ncols;
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < ncols; k0 += 64) {
+        float4 a[4], b[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int k = k0 + 16 * u + 4 * kk;
+            a[u] = ld4_guard(xr, k, ncols);
+            if constexpr (BF16) b[u] = ld4_bf16_guard((const uint16_t *) w + (size_t) ea * ncols, k, ncols);
+            else b[u] = ld4_guard((const float *) w + (size_t) ea * ncols, k, ncols);
         }
-        __syncthreads();
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-            float a[4], b[4];
+        for (int u = 0; u < 4; ++u) {
+            float av[4] = {a[u].x, a[u].y, a[u].z, a[u].w}, bv[4] = {b[u].x, b[u].y, b[u].z, b[u].w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = xs[kk][ty * 4 + i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = ws[kk][tx * 4 + j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+            for (int m = 0; m < 4; ++m) {
+                const float xa = BF16 ? round_bf16(av[m]) : av[m];
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, bv[m], acc, 0, 0, 0);
+            }
         }
-        __syncthreads();
     }
+    const int e = e0 + il;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = t0 + ty * 4 + i, e = e0 + tx * 4 + j;
-            if (t < n_tok && e < nrows) y[(size_t) t * nrows + e] = acc[i][j];
-        }
+    for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 4 * kk + r;
+        if (t < n_tok && e < nrows) y[(size_t) t * nrows + e] = bias ? acc[r] + bias[e] : acc[r];
+    }
 }
 
 }  // namespace
@@ -172,15 +181,20 @@ int gemv_router(int dtype, const void *w, const float *x, float *y, int ncols, i
     return host::set_error(host::ERR_TYPE, "gemv: router dtype %d not supported (f32 = 0, bf16 = 30)", dtype);
 }
 
-int gemm_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int n_tok, hipStream_t st) {
+int gemm_router_bias(int dtype, const void *w, const float *bias, const float *x, float *y, int ncols, int nrows,
+                     int n_tok, hipStream_t st) {
     if (!w || !x || !y || ncols <= 0 || nrows <= 0 || n_tok < 0)
         return host::set_error(host::ERR_SHAPE, "gemm_router: bad arguments");
     if (n_tok == 0) return host::OK;
-    const dim3 g((unsigned) ((n_tok + 63) / 64), (unsigned) ((nrows + 63) / 64));
-    if (dtype == T_BF16) hipLaunchKernelGGL(k_gemm_router<true>, g, dim3(256), 0, st, w, x, y, ncols, nrows, n_tok);
-    else if (dtype == 0) hipLaunchKernelGGL(k_gemm_router<false>, g, dim3(256), 0, st, w, x, y, ncols, nrows, n_tok);
+    const dim3 g((unsigned) ((n_tok + 15) / 16), (unsigned) ((nrows + 63) / 64));
+    if (dtype == T_BF16) hipLaunchKernelGGL(k_gemm_router<true>, g, dim3(256), 0, st, w, bias, x, y, ncols, nrows, n_tok);
+    else if (dtype == 0) hipLaunchKernelGGL(k_gemm_router<false>, g, dim3(256), 0, st, w, bias, x, y, ncols, nrows, n_tok);
     else return host::set_error(host::ERR_TYPE, "gemm_router: dtype %d not supported", dtype);
     return host::check_launch("gemm_router");
+}
+
+int gemm_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int n_tok, hipStream_t st) {
+    return gemm_router_bias(dtype, w, nullptr, x, y, ncols, nrows, n_tok, st);
 }
 
 int route_topk(const float *logits, int32_t *ids, float *w, int n_expert, int k, int n_tok, int gating, int norm,
