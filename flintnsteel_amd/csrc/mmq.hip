@@ -36,6 +36,7 @@ using namespace fns::dev;
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kMmqThreads = 256;   // 4 waves
 constexpr int kMmqRows = 64;       // weight rows per workgroup (16 per wave)
@@ -331,6 +332,21 @@ template <> __device__ __forceinline__ SubB<T_Q3_K> sub_b<T_Q3_K>(const WFrag<T_
     return r;
 }
 
+// -dmin * m_s of sub-blocks kg and kg + 4 of this lane's row (Q4_K / Q5_K): the B operand of the fp32 MFMAs that add
+// the min term of a whole block at once.
+template <int T> __device__ __forceinline__ void neg_min_pair(const WFrag<T> &f, int kg, float &m0, float &m1) {
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        int sc, m;
+        const float dmin = half_to_float(f.h.x >> 16);
+        k4_sc_m(f.h, kg, sc, m);
+        m0 = -(dmin * (float) m);
+        k4_sc_m(f.h, kg + 4, sc, m);
+        m1 = -(dmin * (float) m);
+    } else {
+        m0 = m1 = 0.0f;
+    }
+}
+
 // LDS of one workgroup: the activation superblock chunk [kMmqTok][kMmqStride] int8 and its per-sub-block d8 and
 // d8 * sum(q8) transposed to [8][kMmqTok]; reused as the act tile [kMmqTok][kMmqRows] f32 by the GLU epilogue.
 struct alignas(16) MmqLds {
@@ -385,27 +401,42 @@ __global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
     const int npad = (a.ncols + 511) / 512 * 512;
     const int qbytes = img_q_bytes(npad);
 
-    float acc[kMmqTiles][4], accu[kMmqTiles][4];
+    v4f acc[kMmqTiles], accu[kMmqTiles];
 #pragma unroll
-    for (int t = 0; t < kMmqTiles; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] = accu[t][r] = 0.0f;
+    for (int t = 0; t < kMmqTiles; ++t) acc[t] = accu[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
     WFrag<T> fa, fb, na, nb2;
     wfrag_load<T>(wa, kg, fa);
     if constexpr (GLU) wfrag_load<T>(wb, kg, fb);
     __syncthreads();  // L.src / L.dst
 
-    // staging of superblock chunk kb into buffer kb & 1: q rows by LDS-DMA (18 pieces of 16 bytes per row: the 256 q
-    // bytes + 32 bytes of padding read from what follows them in the same image row); d8 and d8 * sum(q8) of the
-    // chunk's 8 sub-blocks through registers (loaded here, stored transposed by store_scales)
-    const int nrow = ntile * 16;
-    auto stage_q = [&](int kb) {
-        dma_gather_to_lds<kMmqThreads>(L.q[kb & 1], nrow * kMmqStride, [&](int p) {
-            const int i = p / kMmqStride, o = p % kMmqStride;
-            return a.xpack + (size_t) L.src[i] * a.x_img + kb * kImgQRow + o;
-        });
-    };
+    // staging of superblock chunk kb into buffer kb & 1 through registers (an LDS-DMA would make every LDS read of the
+    // compute loop wait for the prefetch): 18 pieces of 16 bytes per row - the 256 q bytes + 32 bytes of padding read
+    // from what follows them in the same image row - loaded by load_q, written by store_q after the compute; d8 and
+    // d8 * sum(q8) of the chunk's 8 sub-blocks likewise (load_scales / store_scales, stored transposed)
+    const int nrow = ntile * 16, npiece = nrow * (kMmqStride / 16);
+    constexpr int kPieces = (kMmqTok * (kMmqStride / 16) + kMmqThreads - 1) / kMmqThreads;
+    uint4 qv0, qv1, qv2, qv3, qv4;  // kPieces = 5 pieces per thread (named: keeps them out of scratch)
+    static_assert(kPieces == 5, "staging registers");
+#define FNS_LOAD_Q(kb)                                                                                              \
+    do {                                                                                                            \
+        uint4 *dstv[5] = {&qv0, &qv1, &qv2, &qv3, &qv4};                                                            \
+        _Pragma("unroll") for (int u = 0; u < kPieces; ++u) {                                                       \
+            const int p = tid + u * kMmqThreads;                                                                    \
+            if (p < npiece) {                                                                                       \
+                const int i = p / (kMmqStride / 16), o = 16 * (p % (kMmqStride / 16));                              \
+                *dstv[u] = *(const uint4 *) (a.xpack + (size_t) L.src[i] * a.x_img + (kb) * kImgQRow + o);          \
+            }                                                                                                       \
+        }                                                                                                           \
+    } while (0)
+#define FNS_STORE_Q(kb)                                                                                             \
+    do {                                                                                                            \
+        const uint4 srcv[5] = {qv0, qv1, qv2, qv3, qv4};                                                            \
+        _Pragma("unroll") for (int u = 0; u < kPieces; ++u) {                                                       \
+            const int p = tid + u * kMmqThreads;                                                                    \
+            if (p < npiece) *(uint4 *) (L.q[(kb) & 1] + 16 * p) = srcv[u];                                          \
+        }                                                                                                           \
+    } while (0)
     float sv[8];
     auto load_scales = [&](int kb) {
         if (tid < 2 * kMmqTok) {
@@ -429,16 +460,19 @@ __global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
             for (int s = 0; s < 8; ++s) (which ? L.s8[kb & 1] : L.d8[kb & 1])[s][i] = sv[s];
         }
     };
-    stage_q(0);
+    FNS_LOAD_Q(0);
     load_scales(0);
+    FNS_STORE_Q(0);
     store_scales(0);
+    // every load of the prologue (fa / fb included) complete before the loop: the compiler's wait analysis merges the
+    // loop-entry state into every iteration, and a pending fa there would put a full wait in front of each sub-block
     dma_wait();
     __syncthreads();
 
     for (int kb = 0; kb < nb; ++kb) {
         const int cur = kb & 1;
         if (kb + 1 < nb) {  // next chunk and next block's weights in flight while this one is computed
-            stage_q(kb + 1);
+            FNS_LOAD_Q(kb + 1);
             load_scales(kb + 1);
             wfrag_load<T>(wa + (int64_t) (kb + 1) * BB, kg, na);
             if constexpr (GLU) wfrag_load<T>(wb + (int64_t) (kb + 1) * BB, kg, nb2);
@@ -468,27 +502,39 @@ __global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
                             if constexpr (GLU) accu[t][r] = fmaf_((float) cu[r], bu.ws[g] * dd[r], accu[t][r]);
                         }
                     }
-                    if constexpr (NG == 1) {
-                        const float4 s8 = *(const float4 *) &L.s8[cur][s][t * 16 + 4 * kg];
-                        const float ss[4] = {s8.x, s8.y, s8.z, s8.w};
+                }
+            }
+        }
+        if constexpr (NG == 1) {
+            // min term of the whole block: acc[token][row] -= sum_s dmin m_s (d8 sum q8)_s as two fp32 MFMAs
+            // (A = d8 sum q8 of sub-blocks kg, kg + 4 per token, B = -dmin m of the same sub-blocks per row)
+            float ma0, ma1, mb0 = 0.0f, mb1 = 0.0f;
+            neg_min_pair<T>(fa, kg, ma0, ma1);
+            if constexpr (GLU) neg_min_pair<T>(fb, kg, mb0, mb1);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            acc[t][r] = fmaf_(-ba.wm, ss[r], acc[t][r]);
-                            if constexpr (GLU) accu[t][r] = fmaf_(-bu.wm, ss[r], accu[t][r]);
-                        }
+            for (int t = 0; t < kMmqTiles; ++t) {
+                if (t < ntile) {
+                    const float x0 = L.s8[cur][kg][t * 16 + jl], x1 = L.s8[cur][kg + 4][t * 16 + jl];
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0, ma0, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1, ma1, acc[t], 0, 0, 0);
+                    if constexpr (GLU) {
+                        accu[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0, mb0, accu[t], 0, 0, 0);
+                        accu[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1, mb1, accu[t], 0, 0, 0);
                     }
                 }
             }
         }
         if (kb + 1 < nb) {
+            FNS_STORE_Q(kb + 1);
             store_scales(kb + 1);
             fa = na;
             if constexpr (GLU) fb = nb2;
         }
-        dma_wait();
         __syncthreads();  // chunk kb + 1 visible; buffer kb & 1 free for chunk kb + 2
     }
 
+#undef FNS_LOAD_Q
+#undef FNS_STORE_Q
     if constexpr (!GLU) {
 #pragma unroll
         for (int t = 0; t < kMmqTiles; ++t)

@@ -91,12 +91,15 @@ template <bool BF16>
 __global__ __launch_bounds__(256) void k_gemm_router(const void *__restrict__ w, const float *__restrict__ bias,
                                                      const float *__restrict__ x, float *__restrict__ y, int ncols,
                                                      int nrows, int n_tok) {
+    // 16 tokens x 16 experts per workgroup; the 4 waves split the columns (wave w: chunks of 64 columns w, w + 4, ...)
+    // and their partial tiles are added in wave order through LDS.
+    __shared__ v4f part[4][64];
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, il = lane % 16, kk = lane / 16;
-    const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 64 + wave * 16;
+    const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
     const int ta = min(t0 + il, n_tok - 1), ea = min(e0 + il, nrows - 1);  // clamped rows (results discarded)
     const float *xr = x + (size_t) ta * ncols;
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k0 = 0; k0 < ncols; k0 += 64) {
+    for (int k0 = wave * 64; k0 < ncols; k0 += 4 * 64) {
         float4 a[4], b[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -115,11 +118,19 @@ __global__ __launch_bounds__(256) void k_gemm_router(const void *__restrict__ w,
             }
         }
     }
-    const int e = e0 + il;
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        v4f s = part[0][lane];
+        s += part[1][lane];
+        s += part[2][lane];
+        s += part[3][lane];
+        const int e = e0 + il;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int t = t0 + 4 * kk + r;
-        if (t < n_tok && e < nrows) y[(size_t) t * nrows + e] = bias ? acc[r] + bias[e] : acc[r];
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 4 * kk + r;
+            if (t < n_tok && e < nrows) y[(size_t) t * nrows + e] = bias ? s[r] + bias[e] : s[r];
+        }
     }
 }
 
@@ -186,7 +197,7 @@ int gemm_router_bias(int dtype, const void *w, const float *bias, const float *x
     if (!w || !x || !y || ncols <= 0 || nrows <= 0 || n_tok < 0)
         return host::set_error(host::ERR_SHAPE, "gemm_router: bad arguments");
     if (n_tok == 0) return host::OK;
-    const dim3 g((unsigned) ((n_tok + 15) / 16), (unsigned) ((nrows + 63) / 64));
+    const dim3 g((unsigned) ((n_tok + 15) / 16), (unsigned) ((nrows + 15) / 16));
     if (dtype == T_BF16) hipLaunchKernelGGL(k_gemm_router<true>, g, dim3(256), 0, st, w, bias, x, y, ncols, nrows, n_tok);
     else if (dtype == 0) hipLaunchKernelGGL(k_gemm_router<false>, g, dim3(256), 0, st, w, bias, x, y, ncols, nrows, n_tok);
     else return host::set_error(host::ERR_TYPE, "gemm_router: dtype %d not supported", dtype);
