@@ -54,6 +54,8 @@ namespace {
 
 constexpr int kMaxTok = 4;
 constexpr int kMaxCh = kMaxTok * 16;
+// Channel table entry (n_tok > 1): expert, number of (token, slot) columns, their token rows and output rows.
+constexpr int kChanInts = 2 + 2 * kMaxTok;
 constexpr int kDownRows = 8;  // output rows per down workgroup
 constexpr size_t kLdsBudget = 150 * 1024;  // dynamic LDS per workgroup (gfx950: 160 KiB per CU)
 // Fused-kernel synchronisation words, each on its own 256-byte line: 16 group counters, the count of complete groups,
@@ -83,6 +85,7 @@ struct LayerArgs {
     float *blk_amax;      // [T*K][Fpad / 32]
     const uint8_t **dptr; // [T*K] down matrix of each (token, slot)
     int *sync;            // fused-kernel completion counters and flags, one per 256-byte line (zeroed by the router kernel)
+    int *chan;            // n_tok > 1: [kMaxCh][kChanInts] channel table, then n_distinct, then the router arrival count
     int64_t xq_row_bytes;
     int fused;            // the shape fits the fused kernel (n_tok = 1)
 };
@@ -105,10 +108,12 @@ __device__ __forceinline__ void pack_store(uint8_t *pack, int npad, int i, const
     if (i % 32 == 0) d[npad / 32 + npad / 16 + i / 32] = dh * (float) r.qsum32;
 }
 
+__device__ void route_all(const LayerArgs &a);
+
 // ---- K1: router rows + Q8_1 of x ----------------------------------------------------------------------------------
 // 1024-thread workgroups: the first ceil(n_expert / 4) each compute four router rows (256 lanes per row), the rest
 // quantise 1024 columns of one token row. Few, wide workgroups start faster than one small workgroup per row.
-constexpr int kK1Threads = 256, kK1Rows = kK1Threads / 256;
+constexpr int kK1Threads = 1024, kK1Rows = kK1Threads / 256;
 
 __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
     __shared__ float red[kK1Rows][4][kMaxTok];
@@ -166,9 +171,26 @@ __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
         __syncthreads();
         if (t256 < T && r < a.NE) {
             const float lg = (red[sub][0][t256] + red[sub][1][t256]) + (red[sub][2][t256] + red[sub][3][t256]);
-            a.logits[(size_t) t256 * a.NE + r] = a.router_bias ? lg + a.router_bias[r] : lg;
+            const float v = a.router_bias ? lg + a.router_bias[r] : lg;
+            if (T > 1) __hip_atomic_store(a.logits + (size_t) t256 * a.NE + r, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else a.logits[(size_t) t256 * a.NE + r] = v;
         }
         FNS_MARK(0, blockIdx.x, 3);
+        if (T > 1) {  // the last router workgroup to finish routes every token (it resets the arrival count)
+            // the logits went out as device-coherent stores; the wait below makes them complete before the arrival
+            __shared__ int s_last;
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            int *done = a.chan + kMaxCh * kChanInts + 1;
+            if (threadIdx.x == 0)
+                s_last = __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_router_wg - 1;
+            __syncthreads();
+            if (s_last) {
+                FNS_MARK(0, blockIdx.x, 4);
+                route_all(a);
+                if (threadIdx.x == 0) __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
         return;
     }
     const int npad = (H + 511) / 512 * 512;
@@ -225,42 +247,151 @@ __device__ __forceinline__ int route_channel(const LayerArgs &a, RouteLds &rs) {
         if (pub && tid < K) publish_route(a, rs, 0, tid);
         return rs.sel[blockIdx.y];
     }
-    for (int t = 0; t < T; ++t) {
-        route_topk_block<NT>(a.logits + (size_t) t * a.NE, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
-        if (tid < K) {  // wave 0: done before it writes the next token's keys
-            rs.ids[t * K + tid] = rs.sel[tid];
-            if (pub) publish_route(a, rs, t, tid);
+    // n_tok > 1: routing and compaction were done once by the router kernel; read this channel's entry
+    if (tid == 0) {
+        const int n_distinct = a.chan[kMaxCh * kChanInts];
+        const int c = blockIdx.y;
+        if (c < n_distinct) {
+            const int *en = a.chan + c * kChanInts;
+            rs.e = en[0];
+            rs.ncol = en[1];
+            for (int i = 0; i < kMaxTok; ++i) {
+                rs.xrow[i] = en[2 + i];
+                rs.orow[i] = en[2 + kMaxTok + i];
+            }
+        } else {
+            rs.e = -1;
+            rs.ncol = 0;
         }
     }
-    if (tid == 0) rs.e = -1;
     __syncthreads();
-    int base = 0;  // selected experts below e0
-    for (int e0 = 0; e0 < a.NE; e0 += NT) {
-        const int ex = e0 + tid;
-        bool present = false;
-        if (ex < a.NE)
-            for (int i = 0; i < T * K; ++i) present |= rs.ids[i] == ex;
-        const uint64_t m = __ballot(present);
-        if (lane64 == 0) rs.wave_cnt[wave] = __popcll(m);
-        __syncthreads();
-        int rank = base + __popcll(m & ((1ull << lane64) - 1ull));
-        for (int wv = 0; wv < wave; ++wv) rank += rs.wave_cnt[wv];
-        for (int wv = 0; wv < NT / kWave; ++wv) base += rs.wave_cnt[wv];
-        if (present && rank == (int) blockIdx.y) {
-            rs.e = ex;
-            int n = 0;
-            for (int t = 0; t < T; ++t)
-                for (int j = 0; j < K; ++j)
-                    if (rs.ids[t * K + j] == ex) {
-                        rs.xrow[n] = t;
-                        rs.orow[n] = t * K + j;
-                        ++n;
-                    }
-            rs.ncol = n;
-        }
-        __syncthreads();
-    }
+    (void) wave;
+    (void) lane64;
+    (void) pub;
     return rs.e;
+}
+
+// Routing of n_tok > 1 tokens, run once by the last router workgroup to finish (kK1Threads = 1024 threads): wave t
+// computes token t's probabilities with route_topk_block's fp32 operations (same bits as the batch-1 routing) as
+// 64-bit keys (bits(p) << 32) | ~e; every (token, expert) pair is then ranked by tpp threads counting the keys above
+// its own (the rank r < k is the slot); the weights follow route_weight (slot-order sum). The distinct experts are
+// listed in ascending order with their (token, slot) columns - the channel table the gate/up workgroups read (ggml
+// mm_ids_helper-style compaction: each distinct expert's weights are read once per call) - and ids, weights and down
+// pointers are published.
+__device__ void route_all(const LayerArgs &a) {
+    __shared__ uint64_t s_key[kMaxTok][256];
+    __shared__ int s_sel[kMaxTok][16];
+    __shared__ float s_pv[kMaxTok][16];
+    __shared__ int8_t s_col[256][kMaxTok];  // slot + 1 of expert e in token t's selection, 0 if not selected
+    __shared__ int s_wcnt[kK1Threads / kWave];
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int T = a.T, K = a.K, NE = a.NE;
+    for (int i = tid; i < 256 * kMaxTok; i += kK1Threads) (&s_col[0][0])[i] = 0;
+    if (wave < T) {  // device-scope loads: the logits were written by other workgroups
+        float v[4], p[4], m = -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            v[j] = e < NE ? __hip_atomic_load(a.logits + (size_t) wave * NE + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : -__builtin_inff();
+            m = fmaxf(m, v[j]);
+        }
+        if (a.gating == 0) {
+            m = lanes_max<64>(m);
+            float ev[4], sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ev[j] = lane + 64 * j < NE ? fns_expf(v[j] - m) : 0.0f;
+                sum = sum + ev[j];
+            }
+            sum = lanes_sum<64>(sum);
+            const float inv = 1.0f / sum;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = ev[j] * inv;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = lane + 64 * j < NE ? 1.0f / (1.0f + fns_expf(-v[j])) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            s_key[wave][e] = e < NE ? ((uint64_t) __builtin_bit_cast(uint32_t, p[j]) << 32) | (uint32_t) ~e : 0ull;
+        }
+    }
+    __syncthreads();
+    FNS_MARK(0, blockIdx.x, 5);
+    // ranks: tpp threads per (token, expert) pair, pair = tid / tpp, keys part + tpp i
+    const int npairs = T * NE;
+    int tpp = 1;
+    while (tpp < 8 && 2 * tpp * npairs <= kK1Threads) tpp *= 2;
+    for (int q0 = 0; q0 < npairs * tpp; q0 += kK1Threads) {  // wave-uniform trip count
+        const int q = q0 + tid, pair = q / tpp, part = q % tpp;
+        const bool live = pair < npairs;
+        const int t = live ? pair / NE : 0, e = live ? pair % NE : 0;
+        const uint64_t own = s_key[t][e];
+        // part takes keys [part * span, part * span + span) of the token's 256 (span: NE / tpp rounded up to 32; zero
+        // keys past NE never count); each batch of 16 reads is issued before its first compare
+        const int span = ((NE + tpp - 1) / tpp + 31) / 32 * 32;
+        const ulonglong2 *kp = (const ulonglong2 *) &s_key[t][part * span];
+        int rank = 0;
+        for (int c0 = 0; c0 < span / 2; c0 += 16) {
+            ulonglong2 kk[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) kk[c] = kp[c0 + c];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) rank += (kk[c].x > own ? 1 : 0) + (kk[c].y > own ? 1 : 0);
+        }
+        if (!live) rank = 0;
+        switch (tpp) {
+            case 8: rank = lanes_sum_i<8>(rank); break;
+            case 4: rank = lanes_sum_i<4>(rank); break;
+            case 2: rank = lanes_sum_i<2>(rank); break;
+            default: break;
+        }
+        if (live && part == 0 && rank < K) {
+            s_sel[t][rank] = e;
+            s_pv[t][rank] = __builtin_bit_cast(float, (uint32_t) (own >> 32));
+        }
+    }
+    __syncthreads();
+    FNS_MARK(0, blockIdx.x, 6);
+    if (tid < T * K) {  // (token, slot): ids, weights, down pointers
+        const int t = tid / K, j = tid % K, e = s_sel[t][j];
+        a.ids[tid] = e;
+        a.w[tid] = route_weight(s_pv[t], K, a.norm, j);
+        a.dptr[tid] = (const uint8_t *) gload<const char *>((const uint8_t *) (a.table + e)) + a.down_off;
+        s_col[e][t] = (int8_t) (j + 1);
+    }
+    __syncthreads();
+    FNS_MARK(0, blockIdx.x, 8);
+    // distinct experts, ascending: expert ex = tid
+    const int ex = tid;
+    bool present = false;
+    if (ex < NE)
+        for (int t = 0; t < T; ++t) present |= s_col[ex][t] != 0;
+    const uint64_t m = __ballot(present);
+    if (lane == 0) s_wcnt[wave] = __popcll(m);
+    __syncthreads();
+    int rank = __popcll(m & ((1ull << lane) - 1ull));
+    for (int w = 0; w < wave; ++w) rank += s_wcnt[w];
+    if (present) {
+        int *en = a.chan + rank * kChanInts;
+        int n = 0;
+        for (int t = 0; t < T; ++t)
+            if (s_col[ex][t]) {
+                en[2 + n] = t;
+                en[2 + kMaxTok + n] = t * K + s_col[ex][t] - 1;
+                ++n;
+            }
+        en[0] = ex;
+        en[1] = n;
+    }
+    if (tid == 0) {
+        int total = 0;
+        for (int w = 0; w < kK1Threads / kWave; ++w) total += s_wcnt[w];
+        a.chan[kMaxCh * kChanInts] = total;
+    }
+    FNS_MARK(0, blockIdx.x, 7);
 }
 
 // SwiGLU epilogue of one row (LPR-lane partial sums) and the Q8_1 of the workgroup's RPB act rows per column.
@@ -1319,10 +1450,10 @@ int by_type_down(int t, const LayerArgs &a, hipStream_t st) {
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
-constexpr int kSections = 11;
+constexpr int kSections = 12;
 
 // Byte sizes of the workspace sections: 0 logits, 1 xq, 2 ids, 3 w, 4 act, 5 escale (documented in fns_hip.h),
-// then internal: 6 xpack, 7 apack, 8 blk_amax, 9 dptr, 10 sync.
+// then internal: 6 xpack, 7 apack, 8 blk_amax, 9 dptr, 10 sync, 11 channel table + arrival count (n_tok > 1).
 void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     const size_t hpad = (size_t) host::pad512(L->hidden), fpad = (size_t) host::pad512(L->inter);
     const size_t ch = (size_t) n_tok * L->k;
@@ -1337,6 +1468,7 @@ void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     sizes[8] = ch * (fpad / 32) * 4;
     sizes[9] = ch * 8;
     sizes[10] = (size_t) kSyncLines * kSyncStride * 4;
+    sizes[11] = (size_t) (kMaxCh * kChanInts + 2) * 4;
 }
 
 }  // namespace
@@ -1417,6 +1549,7 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     a.blk_amax = (float *) sec[8];
     a.dptr = (const uint8_t **) sec[9];
     a.sync = (int *) sec[10];
+    a.chan = (int *) sec[11];
     a.xq_row_bytes = host::q8_1_row_bytes(L->hidden);
     a.fused = n_tok == 1 && fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type)) > 0;
     return host::OK;
