@@ -359,7 +359,7 @@ struct alignas(16) MmqLds {
 static_assert(sizeof(float) * kMmqTok * kMmqRows <= 2 * kMmqTok * kMmqStride, "act tile fits the chunk buffers");
 
 template <int T, bool GLU>
-__global__ __launch_bounds__(kMmqThreads) void k_mmq(const MmqArgs a) {
+__global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU ? 3 : 1, GLU ? 4 : 8))) void k_mmq(const MmqArgs a) {
     extern __shared__ __align__(16) uint8_t smem_raw[];
     MmqLds &L = *(MmqLds *) smem_raw;
     constexpr int BB = Traits<T>::bytes, NG = groups_of<T>();
