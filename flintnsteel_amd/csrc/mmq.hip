@@ -418,15 +418,26 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
     constexpr int kPieces = (kMmqTok * (kMmqStride / 16) + kMmqThreads - 1) / kMmqThreads;
     uint4 qv0, qv1, qv2, qv3, qv4;  // kPieces = 5 pieces per thread (named: keeps them out of scratch)
     static_assert(kPieces == 5, "staging registers");
+    // byte offset (from a.xpack) of each of this thread's staging pieces in chunk 0; chunk kb adds kb * kImgQRow
+    uint32_t qo0 = 0, qo1 = 0, qo2 = 0, qo3 = 0, qo4 = 0;
+    {
+        uint32_t *qo[5] = {&qo0, &qo1, &qo2, &qo3, &qo4};
+#pragma unroll
+        for (int u = 0; u < kPieces; ++u) {
+            const int p = tid + u * kMmqThreads;
+            if (p < npiece) {
+                const int i = p / (kMmqStride / 16), o = 16 * (p % (kMmqStride / 16));
+                *qo[u] = (uint32_t) ((size_t) L.src[i] * a.x_img + o);
+            }
+        }
+    }
 #define FNS_LOAD_Q(kb)                                                                                              \
     do {                                                                                                            \
         uint4 *dstv[5] = {&qv0, &qv1, &qv2, &qv3, &qv4};                                                            \
+        const uint32_t offv[5] = {qo0, qo1, qo2, qo3, qo4};                                                         \
         _Pragma("unroll") for (int u = 0; u < kPieces; ++u) {                                                       \
-            const int p = tid + u * kMmqThreads;                                                                    \
-            if (p < npiece) {                                                                                       \
-                const int i = p / (kMmqStride / 16), o = 16 * (p % (kMmqStride / 16));                              \
-                *dstv[u] = *(const uint4 *) (a.xpack + (size_t) L.src[i] * a.x_img + (kb) * kImgQRow + o);          \
-            }                                                                                                       \
+            if (tid + u * kMmqThreads < npiece)                                                                     \
+                *dstv[u] = *(const uint4 *) (a.xpack + offv[u] + (kb) * kImgQRow);                                  \
         }                                                                                                           \
     } while (0)
 #define FNS_STORE_Q(kb)                                                                                             \
@@ -438,12 +449,14 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
         }                                                                                                           \
     } while (0)
     float sv[8];
+    const float *sbase = nullptr;  // this thread's d8 (even) or d8 * sum(q8) (odd thread) row of its token
+    if (tid < 2 * kMmqTok && (tid >> 1) < cnt)
+        sbase = (const float *) (a.xpack + (size_t) L.src[tid >> 1] * a.x_img + qbytes) +
+                ((tid & 1) ? npad / 32 + npad / 16 : 0);
     auto load_scales = [&](int kb) {
         if (tid < 2 * kMmqTok) {
-            const int i = tid >> 1, which = tid & 1;
-            if (i < cnt) {
-                const float *f = (const float *) (a.xpack + (size_t) L.src[i] * a.x_img + qbytes) +
-                                 (which ? npad / 32 + npad / 16 : 0) + 8 * kb;
+            if (sbase) {
+                const float *f = sbase + 8 * kb;
                 const float4 v0 = *(const float4 *) f, v1 = *(const float4 *) (f + 4);
                 sv[0] = v0.x, sv[1] = v0.y, sv[2] = v0.z, sv[3] = v0.w;
                 sv[4] = v1.x, sv[5] = v1.y, sv[6] = v1.z, sv[7] = v1.w;
