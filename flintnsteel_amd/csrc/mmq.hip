@@ -490,10 +490,9 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
             wfrag_load<T>(wa + (int64_t) (kb + 1) * BB, kg, na);
             if constexpr (GLU) wfrag_load<T>(wb + (int64_t) (kb + 1) * BB, kg, nb2);
         }
-#pragma unroll 1
-        for (int s2 = 0; s2 < 8; s2 += 2)
 #pragma unroll
-        for (int s = s2; s < s2 + 2; ++s) {
+        for (int s = 0; s < 8; ++s) {
+            if (s % 2 == 0) __builtin_amdgcn_sched_barrier(0);  // pairs of sub-blocks: bounded live ranges
             const SubB<T> ba = sub_b<T>(fa, s, kg);
             SubB<T> bu;
             if constexpr (GLU) bu = sub_b<T>(fb, s, kg);
