@@ -38,8 +38,9 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kMmqThreads = 256;   // 4 waves
-constexpr int kMmqRows = 64;       // weight rows per workgroup (16 per wave)
+constexpr int kMmqThreads = 256;   // gate/up launch: 4 waves
+constexpr int kMmqRows = 64;       // gate/up launch: weight rows per workgroup (16 per wave)
+constexpr int kMmqWavesWide = 8;   // plain launch (down / dense) when nrows allows: 8 waves, 128 rows per workgroup
 constexpr int kMmqTok = 64;        // activation rows per workgroup (4 MFMA tiles of 16)
 constexpr int kMmqTiles = kMmqTok / 16;
 constexpr int kMmqStride = 288;    // LDS bytes per staged activation row (256 + 32: spreads the A-fragment reads)
@@ -358,8 +359,10 @@ struct alignas(16) MmqLds {
 };
 static_assert(sizeof(float) * kMmqTok * kMmqRows <= 2 * kMmqTok * kMmqStride, "act tile fits the chunk buffers");
 
-template <int T, bool GLU>
-__global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU ? 3 : 1, GLU ? 4 : 8))) void k_mmq(const MmqArgs a) {
+template <int T, bool GLU, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(GLU ? 3 : 1, GLU ? 4 : 8))) void k_mmq(const MmqArgs a) {
+    constexpr int NT = NW * 64, ROWS = NW * 16;  // threads, weight rows per workgroup
+    static_assert(!GLU || NW == 4, "the gate/up epilogue assumes 64 rows per workgroup");
     extern __shared__ __align__(16) uint8_t smem_raw[];
     MmqLds &L = *(MmqLds *) smem_raw;
     constexpr int BB = Traits<T>::bytes, NG = groups_of<T>();
@@ -386,14 +389,14 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
     }
     if (cnt <= 0) return;
     const int ntile = (cnt + 15) / 16;
-    for (int i = tid; i < kMmqTok; i += kMmqThreads) {
+    for (int i = tid; i < kMmqTok; i += NT) {
         const int q = seg + min(i, cnt - 1);
         L.src[i] = a.src ? a.src[q] : q;
         L.dst[i] = a.dst_rows ? a.dst_rows[q] : q;
     }
 
     const uint8_t *wbase = a.table ? (const uint8_t *) gload<const char *>((const uint8_t *) (a.table + e)) : a.w_dense;
-    const int row = blockIdx.y * kMmqRows + wave * 16 + jl;  // this lane's weight row
+    const int row = blockIdx.y * ROWS + wave * 16 + jl;  // this lane's weight row
     const int nb = a.ncols / 256;
     const int64_t row_bytes = (int64_t) nb * BB;
     const uint8_t *wa = wbase + a.off_a + (int64_t) row * row_bytes;
@@ -415,16 +418,16 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
     // from what follows them in the same image row - loaded by load_q, written by store_q after the compute; d8 and
     // d8 * sum(q8) of the chunk's 8 sub-blocks likewise (load_scales / store_scales, stored transposed)
     const int nrow = ntile * 16, npiece = nrow * (kMmqStride / 16);
-    constexpr int kPieces = (kMmqTok * (kMmqStride / 16) + kMmqThreads - 1) / kMmqThreads;
+    constexpr int kPieces = (kMmqTok * (kMmqStride / 16) + NT - 1) / NT;
     uint4 qv0, qv1, qv2, qv3, qv4;  // kPieces = 5 pieces per thread (named: keeps them out of scratch)
-    static_assert(kPieces == 5, "staging registers");
+    static_assert(kPieces <= 5, "staging registers");
     // byte offset (from a.xpack) of each of this thread's staging pieces in chunk 0; chunk kb adds kb * kImgQRow
     uint32_t qo0 = 0, qo1 = 0, qo2 = 0, qo3 = 0, qo4 = 0;
     {
         uint32_t *qo[5] = {&qo0, &qo1, &qo2, &qo3, &qo4};
 #pragma unroll
         for (int u = 0; u < kPieces; ++u) {
-            const int p = tid + u * kMmqThreads;
+            const int p = tid + u * NT;
             if (p < npiece) {
                 const int i = p / (kMmqStride / 16), o = 16 * (p % (kMmqStride / 16));
                 *qo[u] = (uint32_t) ((size_t) L.src[i] * a.x_img + o);
@@ -436,7 +439,7 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
         uint4 *dstv[5] = {&qv0, &qv1, &qv2, &qv3, &qv4};                                                            \
         const uint32_t offv[5] = {qo0, qo1, qo2, qo3, qo4};                                                         \
         _Pragma("unroll") for (int u = 0; u < kPieces; ++u) {                                                       \
-            if (tid + u * kMmqThreads < npiece)                                                                     \
+            if (tid + u * NT < npiece)                                                                              \
                 *dstv[u] = *(const uint4 *) (a.xpack + offv[u] + (kb) * kImgQRow);                                  \
         }                                                                                                           \
     } while (0)
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
     do {                                                                                                            \
         const uint4 srcv[5] = {qv0, qv1, qv2, qv3, qv4};                                                            \
         _Pragma("unroll") for (int u = 0; u < kPieces; ++u) {                                                       \
-            const int p = tid + u * kMmqThreads;                                                                    \
+            const int p = tid + u * NT;                                                                             \
             if (p < npiece) *(uint4 *) (L.q[(kb) & 1] + 16 * p) = srcv[u];                                          \
         }                                                                                                           \
     } while (0)
@@ -572,7 +575,7 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
             }
         __syncthreads();
         const int fpad = (a.nrows + 511) / 512 * 512;
-        for (int p0 = wave * 2; p0 < 2 * cnt; p0 += 2 * (kMmqThreads / kWave)) {  // wave-uniform trip count
+        for (int p0 = wave * 2; p0 < 2 * cnt; p0 += 2 * NW) {  // wave-uniform trip count
             const int p = p0 + lane / 32;
             const bool live = p < 2 * cnt;
             const int i = live ? p >> 1 : 0, half = p & 1;
@@ -587,24 +590,28 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(GLU
     }
 }
 
-template <bool GLU> const void *mmq_kernel(int type) {
+template <bool GLU, int NW> const void *mmq_kernel(int type) {
     switch (type) {
-        case T_Q3_K: return (const void *) k_mmq<T_Q3_K, GLU>;
-        case T_Q4_K: return (const void *) k_mmq<T_Q4_K, GLU>;
-        case T_Q5_K: return (const void *) k_mmq<T_Q5_K, GLU>;
-        case T_Q6_K: return (const void *) k_mmq<T_Q6_K, GLU>;
+        case T_Q3_K: return (const void *) k_mmq<T_Q3_K, GLU, NW>;
+        case T_Q4_K: return (const void *) k_mmq<T_Q4_K, GLU, NW>;
+        case T_Q5_K: return (const void *) k_mmq<T_Q5_K, GLU, NW>;
+        case T_Q6_K: return (const void *) k_mmq<T_Q6_K, GLU, NW>;
     }
     return nullptr;
 }
 
 int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
-    const void *fn = glu ? mmq_kernel<true>(type) : mmq_kernel<false>(type);
+    // the plain launch takes 128 rows per workgroup when nrows allows: twice the weight rows per staged activation
+    const bool wide = !glu && a.nrows % (16 * kMmqWavesWide) == 0;
+    const int nw = glu || !wide ? 4 : kMmqWavesWide;
+    const void *fn = glu ? mmq_kernel<true, 4>(type) : wide ? mmq_kernel<false, kMmqWavesWide>(type)
+                                                            : mmq_kernel<false, 4>(type);
     if (!fn) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
     if (groups <= 0) return host::OK;
     MmqArgs arg = a;
     void *args[] = {&arg};
-    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) groups, (unsigned) (a.nrows / kMmqRows)),
-                                         dim3(kMmqThreads), args, sizeof(MmqLds), st);
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) groups, (unsigned) (a.nrows / (16 * nw))),
+                                         dim3(64 * nw), args, sizeof(MmqLds), st);
     if (e != hipSuccess) return host::set_error(host::ERR_LAUNCH, "mmq: %s", hipGetErrorString(e));
     return host::check_launch("mmq");
 }
