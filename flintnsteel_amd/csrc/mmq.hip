@@ -12,8 +12,8 @@
 //     result is scaled once: acc += float(I) * (d * sc_s * d8) - dmin * m_s * (d8 * sum q8). For the 16-value scale
 //     groups of Q6_K / Q3_K the B operand is split in two masked halves (one MFMA per group); their zero points
 //     (32, 4) are subtracted from the codes on the way into the int8 operand, so they need no activation sums.
-//   * A workgroup (4 waves) owns 64 weight rows (16 per wave) of one expert and up to 128 of that expert's rows of
-//     activations (8 tiles of 16): each weight byte is read from HBM once per 128 routed rows. Activations are staged
+//   * A workgroup (4 or 8 waves) owns 64 or 128 weight rows (16 per wave) of one expert and up to 64 of that expert's
+//     rows of activations (4 tiles of 16): each weight byte is read from HBM once per 64 routed rows. Activations are staged
 //     per 256-column superblock in LDS (LDS-DMA of the gathered Q8_1 image rows, 288-byte row stride so the 16 rows of
 //     an A fragment read spread over the banks); weights go straight to VGPRs, one superblock ahead.
 //   * Gate/up: both matrices in one pass (two accumulators per output), then act = up * silu(gate) and its Q8_1 blocks
@@ -47,7 +47,7 @@ constexpr int kMmqStride = 288;    // LDS bytes per staged activation row (256 +
 constexpr int kCompactThreads = 1024;
 
 // ---- scratch layout of the expert path --------------------------------------------------------------------------
-// bounds[n_expert + 1] (sorted-row offset of each expert), then gprefix[n_expert + 1] (prefix of ceil(n_e / 128):
+// bounds[n_expert + 1] (sorted-row offset of each expert), then gprefix[n_expert + 1] (prefix of ceil(n_e / 64):
 // the workgroup-group index of each expert's first tile group).
 inline size_t bounds_bytes(int64_t n_expert) { return (size_t) 2 * (n_expert + 1) * 4; }
 
@@ -349,7 +349,7 @@ template <int T> __device__ __forceinline__ void neg_min_pair(const WFrag<T> &f,
 }
 
 // LDS of one workgroup: the activation superblock chunk [kMmqTok][kMmqStride] int8 and its per-sub-block d8 and
-// d8 * sum(q8) transposed to [8][kMmqTok]; reused as the act tile [kMmqTok][kMmqRows] f32 by the GLU epilogue.
+// d8 * sum(q8) transposed to [8][kMmqTok]; reused as the act tile [kMmqTok][rows] f32 by the GLU epilogue.
 struct alignas(16) MmqLds {
     uint8_t q[2][kMmqTok * kMmqStride];  // double-buffered: chunk kb + 1 lands while chunk kb is computed
     float d8[2][8][kMmqTok];
@@ -357,12 +357,11 @@ struct alignas(16) MmqLds {
     int src[kMmqTok];
     int dst[kMmqTok];
 };
-static_assert(sizeof(float) * kMmqTok * kMmqRows <= 2 * kMmqTok * kMmqStride, "act tile fits the chunk buffers");
 
 template <int T, bool GLU, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(GLU ? 3 : 1, GLU ? 4 : 8))) void k_mmq(const MmqArgs a) {
     constexpr int NT = NW * 64, ROWS = NW * 16;  // threads, weight rows per workgroup
-    static_assert(!GLU || NW == 4, "the gate/up epilogue assumes 64 rows per workgroup");
+    static_assert(sizeof(float) * kMmqTok * ROWS <= sizeof(MmqLds::q), "act tile fits the chunk buffers");
     extern __shared__ __align__(16) uint8_t smem_raw[];
     MmqLds &L = *(MmqLds *) smem_raw;
     constexpr int BB = Traits<T>::bytes, NG = groups_of<T>();
@@ -560,7 +559,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(GLU ? 3
             }
     } else {
         // act = up * silu(gate) (reference src/ggml/ggml_mmvq.cu:240-247 epilogue with zero biases), staged as
-        // [token][64 rows] f32, then one Q8_1 block per (token, 32 rows) into the act image rows.
+        // [token][ROWS] f32, then one Q8_1 block per (token, 32 rows) into the act image rows.
+        constexpr int NB = ROWS / 32;  // Q8_1 blocks per token
         float *act = (float *) &L.q[0][0];
 #pragma unroll
         for (int t = 0; t < kMmqTiles; ++t)
@@ -570,17 +570,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(GLU ? 3
                 if (t < ntile) {
                     float v = accu[t][r] + 0.0f;
                     v *= silu(acc[t][r] + 0.0f);
-                    act[i * kMmqRows + wave * 16 + jl] = v;
+                    act[i * ROWS + wave * 16 + jl] = v;
                 }
             }
         __syncthreads();
         const int fpad = (a.nrows + 511) / 512 * 512;
-        for (int p0 = wave * 2; p0 < 2 * cnt; p0 += 2 * NW) {  // wave-uniform trip count
+        for (int p0 = wave * 2; p0 < NB * cnt; p0 += 2 * NW) {  // wave-uniform trip count
             const int p = p0 + lane / 32;
-            const bool live = p < 2 * cnt;
-            const int i = live ? p >> 1 : 0, half = p & 1;
-            const int col = blockIdx.y * kMmqRows + 32 * half + lane % 32;
-            const float v = live ? act[i * kMmqRows + 32 * half + lane % 32] : 0.0f;
+            const bool live = p < NB * cnt;
+            const int i = live ? p / NB : 0, blk = p % NB;
+            const int col = blockIdx.y * ROWS + 32 * blk + lane % 32;
+            const float v = live ? act[i * ROWS + 32 * blk + lane % 32] : 0.0f;
             const Q8Lane q = q8_1_lane(v);
             if (live) {
                 img_store(a.out_pack + (size_t) L.dst[i] * a.out_img, fpad, col, q);
@@ -602,10 +602,11 @@ template <bool GLU, int NW> const void *mmq_kernel(int type) {
 
 int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
     // the plain launch takes 128 rows per workgroup when nrows allows: twice the weight rows per staged activation
+    // (the gate/up launch stays at 4 waves: at 8 its register budget leaves one workgroup per CU - measured slower)
     const bool wide = !glu && a.nrows % (16 * kMmqWavesWide) == 0;
-    const int nw = glu || !wide ? 4 : kMmqWavesWide;
-    const void *fn = glu ? mmq_kernel<true, 4>(type) : wide ? mmq_kernel<false, kMmqWavesWide>(type)
-                                                            : mmq_kernel<false, 4>(type);
+    const int nw = wide ? kMmqWavesWide : 4;
+    const void *fn = glu ? mmq_kernel<true, 4>(type)
+                         : (wide ? mmq_kernel<false, kMmqWavesWide>(type) : mmq_kernel<false, 4>(type));
     if (!fn) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
     if (groups <= 0) return host::OK;
     MmqArgs arg = a;
