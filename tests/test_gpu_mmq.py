@@ -159,3 +159,46 @@ def test_moe_prefill_config4_sample(ops):
     slots_np = {k: layer.slots.view(k).cpu().numpy() for k in ("gate", "up", "down")}
     ref = _oracle_layer_tokens(layer, slots_np, xh, toks, ids, w, orc.Q4_K, orc.Q4_K, H, F) + host(resid)[toks]
     assert_close(out[toks], ref, "config-4 prefill sample", max_tol=1e-3, l2_tol=1e-4)
+
+
+def test_moe_prefill_guard_bf16_sigmoid_residual(ops):
+    """The Flint-style prefill: bf16 router, sigmoid gating, F16 guard active (act amax > 1024: the act rows are
+    divided by e = 2^ceil(log2(amax / 1024)) before Q8_1 and the combine multiplies back; reference
+    src/kernels.cu:534-577, src/engine.cu:349-357), residual added; 33 tokens against the float64 chain."""
+    from flintnsteel_amd import synth
+    H, F, NE, K, T = 512, 256, 32, 6, 33
+    base = synth.build_layer(H, F, NE, K, orc.Q4_K, orc.Q6_K, seed=5, layer=77, std=0.5)
+    router_bf16 = base.router_w.to(torch.bfloat16)
+    layer = ops.MoeLayer(router_bf16, base.slots, orc.Q4_K, orc.Q6_K, H, F, K, gating=ops.GATING_SIGMOID, guard=True)
+    pre = ops.MoePrefill(layer)
+    x = synth.activations(T, H, seed=5, layer=78) * 40.0
+    resid = synth.activations(T, H, seed=5, layer=79)
+    ws = pre.workspace(T)
+    out = host(pre(x, ws=ws, x_resid=resid))
+    tr = {k: host(v) for k, v in pre.trace(ws, T).items()}
+    xh = host(x)
+    # router: bf16 weights, x rounded to bf16 (the reference's cuBLAS BF16 path), fp32 accumulation
+    w32 = router_bf16.float().cpu().numpy()
+    xb = torch.from_numpy(xh).to(torch.bfloat16).float().numpy()
+    logits_ref = orc.router_f32(w32, xb)
+    assert np.abs(tr["logits"] - logits_ref).max() <= 1e-4 * np.abs(logits_ref).max()
+    ids, w, _, _ = orc.route_topk(tr["logits"], K, 1, True)
+    assert np.array_equal(ids, tr["ids"]) and np.array_equal(w, tr["w"])
+    slots = {k: base.slots.view(k).cpu().numpy() for k in ("gate", "up", "down")}
+    xq = orc.quantize_q8_1(xh)
+    ref = np.zeros((T, H))
+    guarded = 0
+    for t in range(T):
+        for j in range(K):
+            e = int(ids[t, j])
+            g = orc.mmvq_experts(orc.Q4_K, [slots["gate"][e].reshape(F, -1)], H, F, xq[t:t + 1], 1, 1, np.zeros(1, np.int32))
+            u = orc.mmvq_experts(orc.Q4_K, [slots["up"][e].reshape(F, -1)], H, F, xq[t:t + 1], 1, 1, np.zeros(1, np.int32))
+            act = orc.swiglu(g, u).astype(np.float32)[0]
+            esc = orc.amax_guard_scale(act)
+            guarded += esc > 1.0
+            aq = orc.quantize_q8_1((act / esc)[None].astype(np.float32))
+            d = orc.mmvq_experts(orc.Q6_K, [slots["down"][e].reshape(H, -1)], F, H, aq, 1, 1, np.zeros(1, np.int32))[0]
+            ref[t] += d * esc * float(w[t, j])
+    assert guarded > 0, "test needs act rows with amax > 1024"
+    ref += host(resid)
+    assert_close(out, ref, "guarded bf16 sigmoid prefill", max_tol=1e-3, l2_tol=1e-4)
