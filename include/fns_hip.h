@@ -105,7 +105,8 @@ int fns_hip_moe_combine(const float *dexp, const float *escale, const float *w, 
  *   act[t][j] = up_{e_j} . q8_1(x[t]) * silu(gate_{e_j} . q8_1(x[t])), (ids, w) = top-k of gating(router . x[t]).
  * Expert e's slot is table[e] (device array) with gate/up/down matrices at the byte offsets below (GGUF blocks).
  * For n_tok > 1 the selected experts are compacted: each distinct expert's weights are read once per call.
- * workspace: fns_hip_moe_workspace_layout() bytes, device memory, sections (byte offsets in offsets[6]):
+ * workspace: fns_hip_moe_workspace_layout() bytes, device memory, zero-filled once before its first use (it holds an
+ * arrival counter that the library keeps consistent from call to call), sections (byte offsets in offsets[6]):
  *   0 logits f32 [n_tok][n_expert], 1 xq Q8_1 [n_tok][q8_1_row_bytes(hidden)], 2 ids i32 [n_tok][k],
  *   3 w f32 [n_tok][k], 4 act f32 [n_tok*k][inter], 5 escale f32 [n_tok*k]. */
 typedef struct FnsMoeLayer {
