@@ -148,7 +148,8 @@ int fns_hip_mmq_experts(int type, const void *const *table, size_t off, int64_t 
 
 int fns_hip_mmq_compact(const int32_t *ids, int64_t n_tok, int64_t n_used, int64_t n_expert, int64_t x_rows_per_tok,
                         int32_t *ids_src1, int32_t *ids_dst, int32_t *expert_bounds, void *stream) {
-    return impl::mmq_compact(ids, n_tok, n_used, n_expert, x_rows_per_tok, ids_src1, ids_dst, expert_bounds, S(stream));
+    return impl::mmq_compact(ids, n_tok, n_used, n_expert, x_rows_per_tok, ids_src1, ids_dst, expert_bounds,
+                             expert_bounds + n_expert + 1, S(stream));
 }
 
 int fns_hip_moe_prefill_workspace(const FnsMoeLayer *layer, int64_t n_tok, size_t *offsets, size_t *total_bytes) {

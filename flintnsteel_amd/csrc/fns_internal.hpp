@@ -55,11 +55,11 @@ size_t mmq_q8_1_bytes(int64_t ncols, int64_t nrows);
 size_t mmq_bounds_bytes(int64_t n_expert);
 int mmq_quant_image(const float *x, int64_t ncols, int64_t rows, void *xpack, hipStream_t st);
 int mmq_compact(const int32_t *ids, int64_t n_tok, int64_t k, int64_t n_expert, int64_t x_rows_per_tok,
-                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, hipStream_t st);
+                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, int32_t *gprefix, hipStream_t st);
 int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t off_b, bool glu, int64_t ncols,
                      int64_t nrows, int64_t n_expert, const void *xpack, int64_t n_pairs, const int32_t *ids_src1,
-                     const int32_t *ids_dst, const int32_t *bounds, float *dst, void *out_pack, float *act_out,
-                     hipStream_t st);
+                     const int32_t *ids_dst, const int32_t *bounds, const int32_t *gprefix, float *dst, void *out_pack,
+                     float *act_out, hipStream_t st);
 int mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq, float *dst,
         hipStream_t st);
 int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, int64_t n_expert,

@@ -643,21 +643,21 @@ int mmq_quant_image(const float *x, int64_t ncols, int64_t rows, void *xpack, hi
 }
 
 int mmq_compact(const int32_t *ids, int64_t n_tok, int64_t k, int64_t n_expert, int64_t x_rows_per_tok,
-                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, hipStream_t st) {
-    if (!ids || !ids_src1 || !ids_dst || !bounds || n_tok < 0 || k < 1 || n_expert < 1 || n_expert > 256 ||
+                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, int32_t *gprefix, hipStream_t st) {
+    if (!ids || !ids_src1 || !ids_dst || !bounds || !gprefix || n_tok < 0 || k < 1 || n_expert < 1 || n_expert > 256 ||
         n_tok * k > (1 << 20) || (x_rows_per_tok != 1 && x_rows_per_tok != k))
         return host::set_error(host::ERR_SHAPE, "mmq compaction: bad arguments");
     hipLaunchKernelGGL(k_mmq_compact, dim3(1), dim3(kCompactThreads), 0, st, ids, (int) (n_tok * k), (int) k,
-                       (int) n_expert, (int) x_rows_per_tok, ids_src1, ids_dst, bounds, bounds + n_expert + 1);
+                       (int) n_expert, (int) x_rows_per_tok, ids_src1, ids_dst, bounds, gprefix);
     return host::check_launch("mmq compaction");
 }
 
 int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t off_b, bool glu, int64_t ncols,
                      int64_t nrows, int64_t n_expert, const void *xpack, int64_t n_pairs, const int32_t *ids_src1,
-                     const int32_t *ids_dst, const int32_t *bounds, float *dst, void *out_pack, float *act_out,
-                     hipStream_t st) {
+                     const int32_t *ids_dst, const int32_t *bounds, const int32_t *gprefix, float *dst, void *out_pack,
+                     float *act_out, hipStream_t st) {
     FNS_TRY(check_mmq_shape(type, ncols, nrows));
-    if (!table || !xpack || !bounds || (!glu && !dst) || (glu && !out_pack) || n_expert < 1 || n_expert > 256)
+    if (!table || !xpack || !bounds || !gprefix || (!glu && !dst) || (glu && !out_pack) || n_expert < 1 || n_expert > 256)
         return host::set_error(host::ERR_SHAPE, "mmq_experts: bad arguments");
     MmqArgs a{};
     a.table = table;
@@ -669,7 +669,7 @@ int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t of
     a.xpack = (const uint8_t *) xpack;
     a.x_img = (int64_t) mmq_image_bytes(ncols);
     a.bounds = bounds;
-    a.gprefix = bounds + n_expert + 1;
+    a.gprefix = gprefix;
     a.src = ids_src1;
     a.dst_rows = ids_dst;
     a.dst = dst;
@@ -703,10 +703,14 @@ int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, i
     FNS_TRY(check_mmq_shape(type, ncols, nrows));
     if (!x || !xq || n_used < 1 || n_tok < 0) return host::set_error(host::ERR_SHAPE, "mmq_experts: bad arguments");
     if (n_tok == 0) return host::OK;
-    FNS_TRY(mmq_compact(ids, n_tok, n_used, n_expert, x_rows_per_tok, ids_src1, ids_dst, bounds, st));
-    FNS_TRY(mmq_quant_image(x, ncols, n_tok * x_rows_per_tok, xq, st));
+    // bounds holds n_expert + 1 ints (the reference's MmqIdsScratch sizing); the tile-group prefix of the GEMM goes in
+    // the slack that mmq_q8_1_bytes adds after the activation images (4096 bytes >= 257 ints)
+    const int64_t rows = n_tok * x_rows_per_tok;
+    int32_t *gprefix = (int32_t *) ((uint8_t *) xq + (size_t) rows * mmq_image_bytes(ncols));
+    FNS_TRY(mmq_compact(ids, n_tok, n_used, n_expert, x_rows_per_tok, ids_src1, ids_dst, bounds, gprefix, st));
+    FNS_TRY(mmq_quant_image(x, ncols, rows, xq, st));
     return mmq_gemm_experts(type, table, off, 0, false, ncols, nrows, n_expert, xq, n_tok * n_used, ids_src1, ids_dst,
-                            bounds, dst, nullptr, nullptr, st);
+                            bounds, gprefix, dst, nullptr, nullptr, st);
 }
 
 // ---- prefill MoE layer ----------------------------------------------------------------------------------------
@@ -772,10 +776,11 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
     FNS_TRY(gemm_router_bias(L->router_dtype, L->router_w, L->router_bias, x, logits, L->hidden, L->n_expert, (int) n_tok,
                              st));
     FNS_TRY(route_topk(logits, ids, w, L->n_expert, L->k, (int) n_tok, L->gating, L->norm_w, st));
-    FNS_TRY(mmq_compact(ids, n_tok, L->k, L->n_expert, 1, src1, dstr, bounds, st));
+    FNS_TRY(mmq_compact(ids, n_tok, L->k, L->n_expert, 1, src1, dstr, bounds, bounds + L->n_expert + 1, st));
     FNS_TRY(mmq_quant_image(x, L->hidden, n_tok, sec[3], st));
     FNS_TRY(mmq_gemm_experts(L->gu_type, table, L->gate_off, L->up_off, true, L->hidden, L->inter, L->n_expert, sec[3],
-                             P, src1, dstr, bounds, nullptr, sec[4], L->guard ? act : nullptr, st));
+                             P, src1, dstr, bounds, bounds + L->n_expert + 1, nullptr, sec[4], L->guard ? act : nullptr,
+                             st));
     if (L->guard) {  // whole-row amax: a second pass over the f32 act rows (reference src/kernels.cu:534-552)
         FNS_TRY(amax_guard(act, escale, L->inter, (int) P, st));
         FNS_TRY(mmq_quant_image(act, L->inter, P, sec[4], st));
@@ -783,7 +788,7 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
     // down: one act row per (token, slot), in the same expert order as gate/up: the sorted rows are the pairs
     // themselves (activation row = output row = p), so the gate/up sort is reused with ids_dst as the source list
     FNS_TRY(mmq_gemm_experts(L->down_type, table, L->down_off, 0, false, L->inter, L->hidden, L->n_expert, sec[4], P,
-                             dstr, dstr, bounds, dexp, nullptr, nullptr, st));
+                             dstr, dstr, bounds, bounds + L->n_expert + 1, dexp, nullptr, nullptr, st));
     return moe_combine(dexp, L->guard ? escale : nullptr, w, nullptr, x_resid, out, L->hidden, L->k, (int) n_tok, st);
 }
 

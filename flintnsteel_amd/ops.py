@@ -380,7 +380,7 @@ def mmq_experts(qtype: int, table: torch.Tensor, off: int, ncols: int, nrows: in
     x = x.contiguous()
     src = torch.empty(n_tok * n_used, dtype=torch.int32, device=x.device)
     dst_ids = torch.empty_like(src)
-    bounds = torch.empty(int(lib().fns_hip_mmq_bounds_bytes(n_expert)) // 4, dtype=torch.int32, device=x.device)
+    bounds = torch.empty(n_expert + 1, dtype=torch.int32, device=x.device)   # the reference's MmqIdsScratch sizing
     xq = torch.zeros(mmq_q8_1_bytes(ncols, n_tok * x_rows_per_tok), dtype=torch.uint8, device=x.device)
     dst = _empty_f32(n_tok, n_used, nrows, like=x)
     call("fns_hip_mmq_experts", qtype, _p(table), off, ncols, nrows, n_expert, _p(x), x_rows_per_tok, n_tok,

@@ -83,13 +83,13 @@ void mmq(ggml_type type, const void *w, int64_t ncols, int64_t nrows, const floa
          float *dst, hipStream_t stream);
 
 // Scratch of the expert path for at most n_tok tokens and n_used experts per token: ids_src1 and ids_dst
-// n_tok*n_used (+128) int32, expert_bounds n_expert+1 int32 (+ 2 x n_expert+1 int32 of tile bookkeeping),
-// xq mmq_q8_1_bytes(ncols_max, n_tok*n_used) bytes. Reference: include/fns/ggml_kernels.h:60-65.
+// n_tok*n_used (+128) int32, expert_bounds n_expert+1 int32, xq mmq_q8_1_bytes(ncols_max, n_tok*n_used) bytes (its
+// slack also holds the GEMM's tile-group prefix). Reference: include/fns/ggml_kernels.h:60-65, src/engine.cu:228-231.
 struct MmqIdsScratch {
     int32_t *ids_src1 = nullptr, *ids_dst = nullptr, *expert_bounds = nullptr;
     void *xq = nullptr;
 };
-// Bytes of expert_bounds needed by mmq_experts (n_expert + 1 bounds plus the tile table).
+// Bytes of the bounds buffer of the standalone compaction (fns_hip_mmq_compact: n_expert + 1 bounds + tile prefix).
 size_t mmq_bounds_bytes(int64_t n_expert);
 
 // dst[t][j][r] = (W_e . x[t][j % x_rows_per_tok])[r], e = ids[t][j], j < n_used; expert e's matrix at table[e] + off.

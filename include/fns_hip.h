@@ -140,21 +140,23 @@ int fns_hip_moe_layer_stage(const FnsMoeLayer *layer, int stage, const float *x,
  * f32): fns_hip_mmq_q8_1_bytes(ncols, nrows) bytes hold nrows of them. */
 /* include/fns/ggml_kernels.h:53-54 mmq_q8_1_bytes */
 size_t fns_hip_mmq_q8_1_bytes(int64_t ncols, int64_t nrows);
-/* bytes of MmqIdsScratch::expert_bounds for n_expert experts (bounds + tile-group prefix) */
+/* bytes of the expert_bounds buffer of fns_hip_mmq_compact for n_expert experts (bounds + tile-group prefix) */
 size_t fns_hip_mmq_bounds_bytes(int64_t n_expert);
 /* include/fns/ggml_kernels.h:56-58 mmq: dst[t][nrows] = W . q8_1(x[t]), x f32 [n_tok][ncols]; xq scratch of
  * fns_hip_mmq_q8_1_bytes(ncols, n_tok) bytes. ncols a multiple of 256, nrows of 64. */
 int fns_hip_mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq,
                 float *dst, void *stream);
 /* include/fns/ggml_kernels.h:60-69 MmqIdsScratch + mmq_experts: dst[t][j][nrows] = W_e . q8_1(x[t][j % x_rows_per_tok]),
- * e = ids[t][j]; expert e's matrix at table[e] + off. Scratch: ids_src1 / ids_dst n_tok * n_used int32, expert_bounds
- * fns_hip_mmq_bounds_bytes(n_expert), xq fns_hip_mmq_q8_1_bytes(ncols, n_tok * x_rows_per_tok). */
+ * e = ids[t][j]; expert e's matrix at table[e] + off. Scratch (the reference's MmqIdsScratch sizing): ids_src1 /
+ * ids_dst n_tok * n_used int32, expert_bounds n_expert + 1 int32, xq fns_hip_mmq_q8_1_bytes(ncols, n_tok * x_rows_per_tok)
+ * bytes. */
 int fns_hip_mmq_experts(int type, const void *const *table, size_t off, int64_t ncols, int64_t nrows, int64_t n_expert,
                         const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
                         int32_t *ids_src1, int32_t *ids_dst, int32_t *expert_bounds, void *xq, float *dst, void *stream);
 /* Expert-id compaction alone (ggml mm_ids_helper semantics; reference src/ggml/ggml_mmq.cu:110-111): pairs
  * p = t * n_used + j sorted by expert, stable; ids_dst[q] = p, ids_src1[q] = (x_rows_per_tok == 1 ? t : p),
- * expert_bounds[e] = first sorted position of expert e (e <= n_expert), followed by the tile-group prefix. */
+ * expert_bounds[e] = first sorted position of expert e (e <= n_expert), followed by the tile-group prefix
+ * (fns_hip_mmq_bounds_bytes(n_expert) bytes in all). */
 int fns_hip_mmq_compact(const int32_t *ids, int64_t n_tok, int64_t n_used, int64_t n_expert, int64_t x_rows_per_tok,
                         int32_t *ids_src1, int32_t *ids_dst, int32_t *expert_bounds, void *stream);
 

@@ -86,6 +86,40 @@ def test_mmq_experts_down_like(ops, qtype):
     assert_close(got.reshape(T * K, nrows), ref, f"mmq_experts down-like {orc.TYPE_NAMES[qtype]}")
 
 
+def test_mmq_experts_reference_scratch_sizes(ops):
+    """The scratch sizes the reference engine allocates (src/engine.cu:228-231: ids n_tok*k + 128, expert_bounds
+    n_expert + 1, xq mmq_q8_1_bytes(max(E, F), n_tok*k)) are enough: nothing is written past any of them."""
+    from flintnsteel_amd._lib import call
+    T, K, NE, ncols, nrows, xr = 90, 4, 64, 512, 128, 4
+    rng = np.random.default_rng(9)
+    mats = make_expert_mats(orc.Q4_K, NE, nrows, ncols, 901)
+    x = gaussian(rng, (T, xr, ncols), 0.5)
+    ids = distinct_ids(rng, T, K, NE)
+    canary = 1 << 12
+    src = torch.full((T * K + 128 + canary,), -7, dtype=torch.int32, device="cuda")
+    dsti = torch.full_like(src, -7)
+    bounds = torch.full((NE + 1 + canary,), -7, dtype=torch.int32, device="cuda")
+    xq_bytes = ops.mmq_q8_1_bytes(ncols, T * K)
+    xq = torch.full((xq_bytes + 4 * canary,), 0x5A, dtype=torch.uint8, device="cuda")
+    dst = torch.empty(T, K, nrows, dtype=torch.float32, device="cuda")
+    md = dev(mats)
+    xd = dev(x)
+    idd = dev(ids)
+    call("fns_hip_mmq_experts", orc.Q4_K, table_of(md).data_ptr(), 0, ncols, nrows, NE, xd.data_ptr(), xr, T,
+         idd.data_ptr(), K, src.data_ptr(), dsti.data_ptr(), bounds.data_ptr(), xq.data_ptr(), dst.data_ptr(),
+         torch.cuda.current_stream().cuda_stream)
+    got = host(dst)
+    assert (host(src[T * K + 128:]) == -7).all() and (host(dsti[T * K + 128:]) == -7).all()
+    assert (host(bounds[NE + 1:]) == -7).all()
+    assert (host(xq[xq_bytes:]) == 0x5A).all()
+    rb, _, _, _ = orc.compact_ids(ids, NE, xr)
+    assert np.array_equal(host(bounds[:NE + 1]), rb)
+    xq8 = orc.quantize_q8_1(x.reshape(T * xr, ncols))
+    ref = orc.mmvq_experts(orc.Q4_K, [m.reshape(nrows, -1) for m in mats], ncols, nrows, xq8, T * K, 1,
+                           ids.ravel())
+    assert_close(got.reshape(T * K, nrows), ref, "mmq_experts with reference scratch sizes")
+
+
 def test_mmq_dense(ops):
     T, ncols, nrows = 130, 768, 192
     rng = np.random.default_rng(3)
