@@ -208,10 +208,13 @@ def run_prefill(torch, synth, n_layers: int = 4, T: int = 512, replays: int = 10
     ids = [p.trace(w, T)["ids"].cpu().numpy() for p, w in zip(pres, wss)]
     touched = float(np.mean([len(np.unique(i)) for i in ids]))
     max_load = float(np.mean([np.bincount(i.ravel(), minlength=NE).max() for i in ids]))
+    loads = [np.bincount(i.ravel(), minlength=NE) for i in ids]
+    groups = float(np.mean([np.sum((n + 63) // 64) for n in loads]))       # workgroup row groups of 64
+    tiles = float(np.mean([np.sum((n + 15) // 16) for n in loads]))        # 16-row tiles holding routed rows
     ops_per_layer = 2 * T * K_TOP * (2 * F * H + H * F)
     del g
     return {"us_per_layer": round(us, 2), "tokens_per_s": round(T / us * 1e6, 0), "experts_touched": touched,
-            "max_expert_load": max_load,
+            "max_expert_load": max_load, "row_groups": groups, "tile_fill": round(tiles / (4 * groups), 3),
             "weight_gbs": round(touched * expert_bytes(Q4_K, Q4_K) / (us * 1e-6) / 1e9, 1),
             "int8_tops": round(ops_per_layer / (us * 1e-6) / 1e12, 2),
             "mfma_util": round(ops_per_layer / (us * 1e-6) / 5.0e15, 4)}

@@ -1,26 +1,28 @@
 // mmq.hip - prefill / batched expert GEMM (MMQ) over GGUF K-quant weights for MI355X gfx950: expert-id compaction,
-// Q8_1 activation images, and an int8-MFMA grouped GEMM with the SwiGLU + Q8_1 of act fused into the gate/up pass.
+// split Q8_1 activation images, and an f16-MFMA grouped GEMM with the SwiGLU + Q8_1 of act fused into the gate/up pass.
 //
 // Reference semantics: src/ggml/ggml_mmq.cu:74-129 (mmq_q8_1_bytes, mmq, mmq_experts: mm_ids_helper sorts the
 // (token, slot) pairs by expert, the activations are quantised once per source row, the GEMM writes each row back to
 // its (token, slot) position), include/fns/ggml_kernels.h:50-69. This is a new CDNA4 design, not ggml's mmq.cuh:
 //
-//   * v_mfma_i32_16x16x32_i8: A = 16 activation rows (tokens) x 32 columns, B = 32 columns x 16 weight rows, so the
-//     lane that owns output (token i, weight row j) holds one weight row j = lane % 16 for 4 tokens. The lane that
-//     loads row j's bytes for the B operand is the one that applies row j's block scales: no scale exchange.
-//   * One MFMA covers one 32-value sub-block (Q4_K / Q5_K) - the K-quant scale granularity - so its exact int32
-//     result is scaled once: acc += float(I) * (d * sc_s * d8) - dmin * m_s * (d8 * sum q8). For the 16-value scale
-//     groups of Q6_K / Q3_K the B operand is split in two masked halves (one MFMA per group); their zero points
-//     (32, 4) are subtracted from the codes on the way into the int8 operand, so they need no activation sums.
-//   * A workgroup (4 or 8 waves) owns 64 or 128 weight rows (16 per wave) of one expert and up to 64 of that expert's
-//     rows of activations (4 tiles of 16): each weight byte is read from HBM once per 64 routed rows. Activations are staged
-//     per 256-column superblock in LDS (LDS-DMA of the gathered Q8_1 image rows, 288-byte row stride so the 16 rows of
-//     an A fragment read spread over the banks); weights go straight to VGPRs, one superblock ahead.
-//   * Gate/up: both matrices in one pass (two accumulators per output), then act = up * silu(gate) and its Q8_1 blocks
-//     (32 consecutive rows = 32 consecutive act columns) written straight into the act image rows the down pass reads.
+//   * The K-quant scales change every 32 (Q4_K, Q5_K) or 16 (Q6_K, Q3_K) columns and the Q8_1 scale d8 every 32, so an
+//     int8 MFMA per sub-block needs a convert + scale + add per output element per sub-block: VALU-bound. Here the
+//     scales are folded into the operands instead, exactly: A = q8 * d8 as two f16 halves (hi + lo, see the image
+//     layout below), B = integer code * integer sub-block scale as f16 (|B| <= 2048: exact; Q6_K's 8-bit scales are
+//     split in two operands). v_mfma_f32_16x16x32_f16 then accumulates a whole 256-column superblock, and only the
+//     superblock's float scales d (and dmin times a 16x16x16 f16 MFMA of the min term) touch the accumulators.
+//     Every product is exact; the sums are fp32.
+//   * A = 16 activation rows (tokens) x 32 columns, B = 32 columns x 16 weight rows: the lane that owns output
+//     (token i, weight row j) holds weight row j = lane % 16 for 4 tokens and decodes row j's codes and scales itself.
+//   * A workgroup (4 waves) owns two 16-row weight streams per wave - gate and up of the same 64 rows (GLU), or 128
+//     rows - and up to 64 of the expert's routed activation rows (4 tiles of 16): each weight byte is read from HBM
+//     once per 64 routed rows. Activations are staged per half superblock in LDS through registers, double-buffered
+//     (72 KB: two workgroups per CU); weights go straight to VGPRs, one superblock ahead.
+//   * Gate/up: both matrices in one pass, then act = up * silu(gate) and its Q8_1 blocks (32 consecutive rows = 32
+//     consecutive act columns) written straight into the split image rows the down pass reads.
 //
-// Integer products are exact; per sub-block results are accumulated in fp32 in sub-block order. Outputs match the
-// float64 oracle (oracle/fns_oracle.c) on the same Q8_1 activations within the fp32 tolerance of the tests.
+// Outputs match the float64 oracle (oracle/fns_oracle.c) on the same Q8_1 activations within the fp32 tolerance of
+// the tests.
 #include "fns_block.hpp"
 #include "fns_common.hpp"
 #include "fns_host.hpp"
@@ -35,21 +37,18 @@ using namespace fns::dev;
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-constexpr int kMmqThreads = 256;   // gate/up launch: 4 waves
-constexpr int kMmqRows = 64;       // gate/up launch: weight rows per workgroup (16 per wave)
-constexpr int kMmqWavesWide = 8;   // plain launch (down / dense) when nrows allows: 8 waves, 128 rows per workgroup
+constexpr int kMmqThreads = 256;   // 4 waves
+constexpr int kMmqWaves = kMmqThreads / 64;
+constexpr int kMmqRows = 64;       // row granularity of the weight matrices
 constexpr int kMmqTok = 64;        // activation rows per workgroup (4 MFMA tiles of 16)
-constexpr int kMmqTiles = kMmqTok / 16;
-constexpr int kMmqStride = 288;    // LDS bytes per staged activation row (256 + 32: spreads the A-fragment reads)
 constexpr int kCompactThreads = 1024;
 
 // ---- scratch layout of the expert path --------------------------------------------------------------------------
-// bounds[n_expert + 1] (sorted-row offset of each expert), then gprefix[n_expert + 1] (prefix of ceil(n_e / 64):
-// the workgroup-group index of each expert's first tile group).
-inline size_t bounds_bytes(int64_t n_expert) { return (size_t) 2 * (n_expert + 1) * 4; }
+// bounds[n_expert + 1] (sorted-row offset of each expert); the GEMM's group prefixes gprefix[2][n_expert + 1]: the
+// 64-row groups of each expert for the 4-tile kernel (n_e / 64 full ones, and the remainder if it is > 32 rows), and
+// the remainder groups of <= 32 rows for the 2-tile kernel.
+inline size_t bounds_bytes(int64_t n_expert) { return (size_t) 3 * (n_expert + 1) * 4; }
+inline size_t gprefix_bytes(int64_t n_expert) { return (size_t) 2 * (n_expert + 1) * 4; }
 
 // ---- compaction (ggml mm_ids_helper semantics, stable) ------------------------------------------------------------
 // ids [n_tok][k] -> pairs p = t k + j sorted by expert, ties in p order: ids_dst[q] = p, ids_src1[q] = the activation
@@ -71,25 +70,28 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
     }
     __syncthreads();
     if (wave == 0) {  // exclusive prefix over <= 256 experts: 4 per lane, then a lane scan
-        int v[4], g[4], s = 0, sg = 0;
+        int v[4], g[4], g2[4], s = 0, sg = 0, sg2 = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int e = 4 * lane + j;
+            const int e = 4 * lane + j, r = (e < ne ? cnt[e] : 0) % kMmqTok;
             v[j] = e < ne ? cnt[e] : 0;
-            g[j] = (v[j] + kMmqTok - 1) / kMmqTok;
+            g[j] = v[j] / kMmqTok + (r > kMmqTok / 2);
+            g2[j] = r > 0 && r <= kMmqTok / 2;
             s += v[j];
             sg += g[j];
+            sg2 += g2[j];
         }
-        int incl = s, inclg = sg;
+        int incl = s, inclg = sg, inclg2 = sg2;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const int t = __shfl_up(incl, o, 64), tg = __shfl_up(inclg, o, 64);
+            const int t = __shfl_up(incl, o, 64), tg = __shfl_up(inclg, o, 64), tg2 = __shfl_up(inclg2, o, 64);
             if (lane >= o) {
                 incl += t;
                 inclg += tg;
+                inclg2 += tg2;
             }
         }
-        int run = incl - s, rung = inclg - sg;
+        int run = incl - s, rung = inclg - sg, rung2 = inclg2 - sg2;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int e = 4 * lane + j;
@@ -97,13 +99,16 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
                 base[e] = run;
                 bounds[e] = run;
                 gprefix[e] = rung;
+                gprefix[ne + 1 + e] = rung2;
             }
             run += v[j];
             rung += g[j];
+            rung2 += g2[j];
         }
         if (lane == 63) {
             bounds[ne] = incl;
             gprefix[ne] = inclg;
+            gprefix[2 * ne + 1] = inclg2;
         }
     }
     __syncthreads();
@@ -140,26 +145,42 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
     }
 }
 
-// ---- Q8_1 activation images ---------------------------------------------------------------------------------------
-// One value per lane, 32-lane blocks; the image layout of fns_block.hpp (int8 q with a 16-byte skew per 256 values,
-// then d, d * sum16(q), d * sum32(q) in fp32). The Q8_1 arithmetic is the reference's (q8_1_lane).
-__device__ __forceinline__ void img_store(uint8_t *img, int npad, int i, const Q8Lane &r) {
+// ---- split activation images --------------------------------------------------------------------------------------
+// The GEMM's A operand is the Q8_1 activation q8 * d8 as an exact pair of halves (hi = f16(q8 d8), lo = f16(q8 d8 - hi):
+// a 7-bit integer times an f16 scale has at most 18 significant bits, two halves hold 22). Row layout, per 256-column
+// superblock kb: 1024 bytes at kb * 1024, two 128-column halves of [hi 128 f16][lo 128 f16]; then at nb * 1024 + 32 kb
+// the min-term sums [S_hi 8 f16][S_lo 8 f16], S_s = d8_s * sum(q8 of sub-block s). Within every 8 columns (and every
+// 4 sums) the stored order is 0 2 1 3 4 6 5 7: the order in which the weight decoders below emit their B operand.
+// Magnitudes are those of the reference's f16 Q8_1 fields (|q8 d8| <= amax, S within the f16 sum's range).
+constexpr int kSbMain = 1024, kSbMin = 32;
+__host__ __device__ constexpr int64_t split_row_bytes(int64_t ncols) { return ncols / 256 * (kSbMain + kSbMin); }
+__device__ __forceinline__ int perm8(int k) { return (k & ~3) | ((k & 1) << 1) | ((k >> 1) & 1); }
+
+__device__ __forceinline__ void split_store(uint8_t *row, int ncols, int i, const Q8Lane &r) {
     const float dh = half_to_float(float_to_half(r.d));
-    float *d = (float *) (img + img_q_bytes(npad));
-    img[img_q_index(i)] = (uint8_t) (int8_t) r.q;
-    if (i % 32 == 0) d[i / 32] = dh;
-    if (i % 16 == 0) d[npad / 32 + i / 16] = dh * (float) r.qsum16;
-    if (i % 32 == 0) d[npad / 32 + npad / 16 + i / 32] = dh * (float) r.qsum32;
+    const float v = (float) r.q * dh;  // exact
+    const _Float16 hi = (_Float16) v;
+    const _Float16 lo = (_Float16) (v - (float) hi);
+    _Float16 *p = (_Float16 *) (row + (size_t) (i >> 8) * kSbMain + ((i >> 7) & 1) * 512);
+    const int pos = perm8(i & 127);
+    p[pos] = hi;
+    p[128 + pos] = lo;
+    if ((i & 31) == 0) {
+        const float s = dh * (float) r.qsum32;  // exact in fp32
+        const _Float16 shi = (_Float16) s, slo = (_Float16) (s - (float) shi);
+        _Float16 *m = (_Float16 *) (row + (size_t) (ncols >> 8) * kSbMain + (size_t) (i >> 8) * kSbMin);
+        const int si = perm8((i >> 5) & 7);
+        m[si] = shi;
+        m[8 + si] = slo;
+    }
 }
 
-// x [rows][ncols] f32 -> image rows; grid (ceil(npad / 256), rows), 256 threads.
-__global__ __launch_bounds__(256) void k_quant_image(const float *__restrict__ x, int64_t ncols, uint8_t *__restrict__ out,
+// x [rows][ncols] f32 -> split image rows (reference Q8_1 arithmetic, q8_1_lane); grid (ncols / 256, rows), 256 threads.
+__global__ __launch_bounds__(256) void k_quant_image(const float *__restrict__ x, int ncols, uint8_t *__restrict__ out,
                                                      int64_t img_row_bytes) {
-    const int npad = (int) ((ncols + 511) / 512 * 512);
     const int row = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
-    const float v = i < ncols ? x[(size_t) row * ncols + i] : 0.0f;
-    const Q8Lane r = q8_1_lane(v);
-    if (i < npad) img_store(out + (size_t) row * img_row_bytes, npad, i, r);
+    const Q8Lane r = q8_1_lane(x[(size_t) row * ncols + i]);
+    split_store(out + (size_t) row * img_row_bytes, ncols, i, r);
 }
 
 // ---- grouped GEMM -------------------------------------------------------------------------------------------------
@@ -169,15 +190,16 @@ struct MmqArgs {
     int64_t off_a, off_b;      // byte offsets of the (gate) matrix and of the up matrix (GLU)
     int ncols, nrows;          // K (columns of W) and N (rows of W)
     int n_expert;
-    const uint8_t *xpack;      // activation image rows
+    const uint8_t *xpack;      // split activation image rows
     int64_t x_img;             // bytes per activation image row
     const int32_t *bounds;     // [n_expert + 1] (null: dense)
-    const int32_t *gprefix;    // [n_expert + 1]
+    const int32_t *gprefix;    // [n_expert + 1] group prefix of this launch's list
+    int tail;                  // 1: the groups are the <= 32-row remainders (2-tile kernel)
     const int32_t *src;        // sorted position -> activation image row (null: identity)
     const int32_t *dst_rows;   // sorted position -> output row (null: identity)
     int n_rows;                // dense: number of activation rows
     float *dst;                // [out row][nrows] f32 (non-GLU)
-    uint8_t *out_pack;         // GLU: act image rows (by output row)
+    uint8_t *out_pack;         // GLU: act split image rows (by output row)
     int64_t out_img;
     float *act_out;            // GLU: optional f32 act [out row][nrows]
 };
@@ -189,182 +211,212 @@ template <> struct WFrag<T_Q5_K> { uint4 h; uint2 q[4]; uint2 qh; };
 template <> struct WFrag<T_Q6_K> { uint2 ql[4]; uint2 qh[2]; uint4 sc; uint32_t d; };
 template <> struct WFrag<T_Q3_K> { uint2 qs[2]; uint2 hm; uint4 tail; };
 
-__device__ __forceinline__ uint2 gload8a(const uint8_t *p) {  // 8 bytes at an 8-byte-aligned global address
-    const uint64_t v = *(const __attribute__((address_space(1))) uint64_t *) p;
-    return make_uint2((uint32_t) v, (uint32_t) (v >> 32));
+// Buffer loads: a uniform base in a resource (SGPRs), a 32-bit per-lane offset and a uniform offset - no 64-bit
+// address arithmetic per load. (Unaligned dword access is enabled on the platform, as for the plain global loads.)
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc rsrc_of(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7FFFFFFF, 0x00020000);
 }
-__device__ __forceinline__ uint2 gload8u(const uint8_t *p) {  // 8 bytes at a 2-byte-aligned global address
-    uint2 v;
-    __builtin_memcpy(&v, (const __attribute__((address_space(1))) uint8_t *) p, 8);
-    return v;
+__device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t vo, uint32_t so) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bload8(Rsrc r, uint32_t vo, uint32_t so) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+    return make_uint2(v[0], v[1]);
 }
 
-template <int T> __device__ __forceinline__ void wfrag_load(const uint8_t *blk, int kg, WFrag<T> &f);
-template <> __device__ __forceinline__ void wfrag_load<T_Q4_K>(const uint8_t *blk, int kg, WFrag<T_Q4_K> &f) {
-    f.h = gload<uint4>(blk);
+// fragment of the block at (vo + so) from r for lane group kg
+template <int T> __device__ __forceinline__ void wfrag_load(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T> &f);
+template <> __device__ __forceinline__ void wfrag_load<T_Q4_K>(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T_Q4_K> &f) {
+    f.h = bload16(r, vo, so);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) f.q[g] = gload8a(blk + 16 + 32 * g + 8 * kg);
+    for (int g = 0; g < 4; ++g) f.q[g] = bload8(r, vo + 8 * kg, so + 16 + 32 * g);
 }
-template <> __device__ __forceinline__ void wfrag_load<T_Q5_K>(const uint8_t *blk, int kg, WFrag<T_Q5_K> &f) {
-    f.h = gload<uint4>(blk);
-    f.qh = gload8a(blk + 16 + 8 * kg);
+template <> __device__ __forceinline__ void wfrag_load<T_Q5_K>(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T_Q5_K> &f) {
+    f.h = bload16(r, vo, so);
+    f.qh = bload8(r, vo + 8 * kg, so + 16);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) f.q[g] = gload8a(blk + 48 + 32 * g + 8 * kg);
+    for (int g = 0; g < 4; ++g) f.q[g] = bload8(r, vo + 8 * kg, so + 48 + 32 * g);
 }
-template <> __device__ __forceinline__ void wfrag_load<T_Q6_K>(const uint8_t *blk, int kg, WFrag<T_Q6_K> &f) {
+template <> __device__ __forceinline__ void wfrag_load<T_Q6_K>(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T_Q6_K> &f) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
-        f.ql[2 * n] = gload8u(blk + 64 * n + 8 * kg);
-        f.ql[2 * n + 1] = gload8u(blk + 64 * n + 32 + 8 * kg);
-        f.qh[n] = gload8u(blk + 128 + 32 * n + 8 * kg);
+        f.ql[2 * n] = bload8(r, vo + 8 * kg, so + 64 * n);
+        f.ql[2 * n + 1] = bload8(r, vo + 8 * kg, so + 64 * n + 32);
+        f.qh[n] = bload8(r, vo + 8 * kg, so + 128 + 32 * n);
     }
-    f.sc = gload16u(blk + 192);
-    f.d = gload<uint16_t>(blk + 208);
+    f.sc = bload16(r, vo, so + 192);
+    f.d = __builtin_amdgcn_raw_buffer_load_b16(r, vo, so + 208, 0);
 }
-template <> __device__ __forceinline__ void wfrag_load<T_Q3_K>(const uint8_t *blk, int kg, WFrag<T_Q3_K> &f) {
-    f.hm = gload8u(blk + 8 * kg);
-    f.qs[0] = gload8u(blk + 32 + 8 * kg);
-    f.qs[1] = gload8u(blk + 64 + 8 * kg);
-    f.tail = gload16u(blk + 94);  // scales[12] at +2, d at +14
-}
-
-__device__ __forceinline__ long pack_long(uint32_t lo, uint32_t hi) {
-    return (long) (((uint64_t) hi << 32) | lo);
+template <> __device__ __forceinline__ void wfrag_load<T_Q3_K>(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T_Q3_K> &f) {
+    f.hm = bload8(r, vo + 8 * kg, so);
+    f.qs[0] = bload8(r, vo + 8 * kg, so + 32);
+    f.qs[1] = bload8(r, vo + 8 * kg, so + 64);
+    f.tail = bload16(r, vo, so + 94);  // scales[12] at +2, d at +14
 }
 
-// Per sub-block s (32 values) of the block: the int8 B operand(s) and their float scales.
-//   NG = 1 (Q4_K, Q5_K): b[0] all 32 columns; acc += I * (ws[0] * d8) - wm * (d8 * sum q8)
-//   NG = 2 (Q6_K, Q3_K): b[0] columns 0-15 (other lanes' bytes zero), b[1] columns 16-31; acc += I_g * (ws[g] * d8)
-template <int T> struct SubB {
-    long b[2];
-    float ws[2], wm;
-};
-template <int T> constexpr int groups_of() { return (T == T_Q6_K || T == T_Q3_K) ? 2 : 1; }
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-template <int T> __device__ __forceinline__ SubB<T> sub_b(const WFrag<T> &f, int s, int kg);
-
-// Sub-block index s may be a runtime value: fragments and scale bytes are picked with selects and shifts (no
-// dynamically indexed register arrays).
-__device__ __forceinline__ uint2 sel4(uint2 a, uint2 b, uint2 c, uint2 d, int i) { return i == 0 ? a : i == 1 ? b : i == 2 ? c : d; }
-__device__ __forceinline__ uint32_t byte_dyn(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
-
-// 6-bit scale and min of sub-block s of a Q4_K / Q5_K block (ggml get_scale_min_k4); h.y, h.z, h.w = scales[0..11].
-__device__ __forceinline__ void k4_sc_m(const uint4 &h, int s, int &sc, int &m) {
-    const int i = s & 3;
-    if (s < 4) {
-        sc = (int) (byte_dyn(h.y, i) & 63u);
-        m = (int) (byte_dyn(h.z, i) & 63u);
-    } else {
-        const uint32_t b8 = byte_dyn(h.w, i);
-        sc = (int) ((b8 & 0xFu) | ((byte_dyn(h.y, i) >> 6) << 4));
-        m = (int) ((b8 >> 4) | ((byte_dyn(h.z, i) >> 6) << 4));
-    }
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 splat(_Float16 v) { return h2{v, v}; }
+// bytes b0..b3 (< 1024 each) of w -> halves (1024 + b0, 1024 + b2) and (1024 + b1, 1024 + b3): 0x6400 is 1024.0
+__device__ __forceinline__ h2 biased02(uint32_t w) { return as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04020400u)); }
+__device__ __forceinline__ h2 biased13(uint32_t w) { return as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04030401u)); }
+__device__ __forceinline__ h2 fma2(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
+__device__ __forceinline__ v8h cat4(h2 a, h2 b, h2 c, h2 d) {
+    return __builtin_bit_cast(v8h, make_uint4(as_u(a), as_u(b), as_u(c), as_u(d)));
+}
+// codes bytes (x = columns 0-3, y = columns 4-7 of the lane) times a scale: exact products (|code * scale| <= 2048)
+__device__ __forceinline__ v8h scaled8(uint32_t x, uint32_t y, h2 sc, h2 bias) {  // (1024 + c) sc + bias, bias = -1024 sc
+    return cat4(fma2(biased02(x), sc, bias), fma2(biased13(x), sc, bias), fma2(biased02(y), sc, bias),
+                fma2(biased13(y), sc, bias));
+}
+__device__ __forceinline__ v8h centred8(uint32_t x, uint32_t y, h2 off, h2 sc) {  // ((1024 + c) - off) * sc
+    return cat4((biased02(x) - off) * sc, (biased13(x) - off) * sc, (biased02(y) - off) * sc,
+                (biased13(y) - off) * sc);
 }
 
-template <> __device__ __forceinline__ SubB<T_Q4_K> sub_b<T_Q4_K>(const WFrag<T_Q4_K> &f, int s, int kg) {
-    SubB<T_Q4_K> r;
-    const uint2 q = sel4(f.q[0], f.q[1], f.q[2], f.q[3], s >> 1);
+// B operand(s) of sub-block s (compile-time) for lane group kg: B[k][row] = integer code x integer scale as f16
+// (Q6_K: two operands, scale split as 16 (sc >> 4) + (sc & 15), each product exact). The block's float scale d (and
+// dmin) are applied per superblock. on = (d != 0): a block with d = 0 contributes d * (...) = 0 whatever its codes.
+template <int T> struct BOp { v8h b[T == T_Q6_K ? 2 : 1]; };
+template <int T> __device__ __forceinline__ BOp<T> decode(const WFrag<T> &f, int s, int kg, bool on);
+
+// (sc_s, sc_s) as f16 and its bias -1024 sc_s for sub-block s (compile time) of a Q4_K / Q5_K block; on = 0: zeros.
+// The 6-bit scales are unpacked four at a time (ggml get_scale_min_k4), byte s placed twice next to 0x64 (1024.0).
+__device__ __forceinline__ void k4_scale2(const uint4 &h, int s, bool on, h2 &s2, h2 &bias) {
+    const uint32_t w = s < 4 ? (h.y & 0x3F3F3F3Fu) : ((h.w & kLo4) | ((h.y >> 2) & 0x30303030u));
+    const uint32_t i = (uint32_t) (s & 3);
+    s2 = as_h2(__builtin_amdgcn_perm(0x64646464u, on ? w : 0u, 0x04000400u | (i << 16) | i)) - splat((_Float16) 1024.0f);
+    bias = s2 * splat((_Float16) -1024.0f);
+}
+template <> __device__ __forceinline__ BOp<T_Q4_K> decode<T_Q4_K>(const WFrag<T_Q4_K> &f, int s, int kg, bool on) {
+    const uint2 q = f.q[s >> 1];
     const int sh = 4 * (s & 1);
-    r.b[0] = pack_long((q.x >> sh) & kLo4, (q.y >> sh) & kLo4);
-    int sc, m;
-    k4_sc_m(f.h, s, sc, m);
-    r.ws[0] = half_to_float(f.h.x & 0xffffu) * (float) sc;
-    r.wm = half_to_float(f.h.x >> 16) * (float) m;
+    h2 s2, bias;
+    k4_scale2(f.h, s, on, s2, bias);
+    BOp<T_Q4_K> r;
+    r.b[0] = scaled8((q.x >> sh) & kLo4, (q.y >> sh) & kLo4, s2, bias);
     return r;
 }
-template <> __device__ __forceinline__ SubB<T_Q5_K> sub_b<T_Q5_K>(const WFrag<T_Q5_K> &f, int s, int kg) {
-    SubB<T_Q5_K> r;
-    const uint2 q = sel4(f.q[0], f.q[1], f.q[2], f.q[3], s >> 1);
+template <> __device__ __forceinline__ BOp<T_Q5_K> decode<T_Q5_K>(const WFrag<T_Q5_K> &f, int s, int kg, bool on) {
+    const uint2 q = f.q[s >> 1];
     const int sh = 4 * (s & 1);
-    r.b[0] = pack_long(((q.x >> sh) & kLo4) | (((f.qh.x >> s) & 0x01010101u) << 4),
-                       ((q.y >> sh) & kLo4) | (((f.qh.y >> s) & 0x01010101u) << 4));
-    int sc, m;
-    k4_sc_m(f.h, s, sc, m);
-    r.ws[0] = half_to_float(f.h.x & 0xffffu) * (float) sc;
-    r.wm = half_to_float(f.h.x >> 16) * (float) m;
+    h2 s2, bias;
+    k4_scale2(f.h, s, on, s2, bias);
+    BOp<T_Q5_K> r;
+    r.b[0] = scaled8(((q.x >> sh) & kLo4) | (((f.qh.x >> s) & 0x01010101u) << 4),
+                     ((q.y >> sh) & kLo4) | (((f.qh.y >> s) & 0x01010101u) << 4), s2, bias);
     return r;
 }
 // Q6_K sub-block s: n = s / 4, qq = s % 4: ql[64 n + 32 (qq & 1) + l] nibble qq >> 1, qh[32 n + l] bits 2 qq,
-// value - 32; scale groups 8 n + 2 qq + (l >= 16).
-template <> __device__ __forceinline__ SubB<T_Q6_K> sub_b<T_Q6_K>(const WFrag<T_Q6_K> &f, int s, int kg) {
-    SubB<T_Q6_K> r;
+// value - 32; int8 scale of group 8 n + 2 qq + (l >= 16).
+template <> __device__ __forceinline__ BOp<T_Q6_K> decode<T_Q6_K>(const WFrag<T_Q6_K> &f, int s, int kg, bool on) {
     const int n = s >> 2, qq = s & 3;
-    const uint2 ql = sel4(f.ql[0], f.ql[1], f.ql[2], f.ql[3], 2 * n + (qq & 1)), qh = n == 0 ? f.qh[0] : f.qh[1];
+    const uint2 ql = f.ql[2 * n + (qq & 1)], qh = f.qh[n];
     const int shl = 4 * (qq >> 1), shh = 2 * qq;
-    const uint32_t lo = bytes_sub<32>((int) (((ql.x >> shl) & kLo4) | (((qh.x >> shh) & 0x03030303u) << 4)));
-    const uint32_t hi = bytes_sub<32>((int) (((ql.y >> shl) & kLo4) | (((qh.y >> shh) & 0x03030303u) << 4)));
-    const long v = pack_long(lo, hi);
-    r.b[0] = kg < 2 ? v : 0;
-    r.b[1] = kg < 2 ? 0 : v;
-    const float d = half_to_float(f.d);
+    const uint32_t x = ((ql.x >> shl) & kLo4) | (((qh.x >> shh) & 0x03030303u) << 4);
+    const uint32_t y = ((ql.y >> shl) & kLo4) | (((qh.y >> shh) & 0x03030303u) << 4);
     const int g0 = 8 * n + 2 * qq;  // even: both groups in one word
     const uint32_t w0 = word(f.sc, g0 >> 2);
-    r.ws[0] = d * (float) (int8_t) byte_dyn(w0, g0 & 3);
-    r.ws[1] = d * (float) (int8_t) byte_dyn(w0, (g0 & 3) + 1);
-    r.wm = 0.0f;
+    const int sc = on ? (int) (int8_t) ((w0 >> (8 * ((g0 & 3) + (kg >> 1)))) & 0xffu) : 0;
+    const h2 off = splat((_Float16) 1056.0f);
+    BOp<T_Q6_K> r;
+    r.b[0] = centred8(x, y, off, splat((_Float16) (16 * (sc >> 4))));
+    r.b[1] = centred8(x, y, off, splat((_Float16) (sc & 15)));
     return r;
 }
 // Q3_K sub-block s: n = s / 4, j = s % 4: qs[32 n + l] bits 2 j, hmask[l] bit 4 n + j (clear: -4); scale groups
 // 8 n + 2 j + (l >= 16), 6-bit value - 32 (low nibbles in scales[0..7], high bit pairs in scales[8..11]).
-template <> __device__ __forceinline__ SubB<T_Q3_K> sub_b<T_Q3_K>(const WFrag<T_Q3_K> &f, int s, int kg) {
-    SubB<T_Q3_K> r;
+template <> __device__ __forceinline__ BOp<T_Q3_K> decode<T_Q3_K>(const WFrag<T_Q3_K> &f, int s, int kg, bool on) {
     const int n = s >> 2, j = s & 3;
-    const uint2 q = n == 0 ? f.qs[0] : f.qs[1];
+    const uint2 q = f.qs[n];
     const int hs = 4 * n + j;
-    const uint32_t lo = bytes_sub<4>((int) (((q.x >> (2 * j)) & 0x03030303u) | (((f.hm.x >> hs) & 0x01010101u) << 2)));
-    const uint32_t hi = bytes_sub<4>((int) (((q.y >> (2 * j)) & 0x03030303u) | (((f.hm.y >> hs) & 0x01010101u) << 2)));
-    const long v = pack_long(lo, hi);
-    r.b[0] = kg < 2 ? v : 0;
-    r.b[1] = kg < 2 ? 0 : v;
-    const float d = half_to_float(f.tail.w >> 16);
+    const uint32_t x = ((q.x >> (2 * j)) & 0x03030303u) | (((f.hm.x >> hs) & 0x01010101u) << 2);
+    const uint32_t y = ((q.y >> (2 * j)) & 0x03030303u) | (((f.hm.y >> hs) & 0x01010101u) << 2);
     // tail = block bytes 94..109: scales[i] is tail byte 2 + i
     const uint32_t hi_w = (f.tail.z >> 16) | (f.tail.w << 16);  // scales[8..11]
+    int scv[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int g = 8 * n + 2 * j + h;
         const int lb = (g & 7) + 2;  // tail byte of scales[g & 7]
         const uint32_t lw = lb < 4 ? f.tail.x : lb < 8 ? f.tail.y : f.tail.z;
-        const uint32_t b = byte_dyn(lw, lb & 3);
+        const uint32_t b = (lw >> (8 * (lb & 3))) & 0xffu;
         const uint32_t lo4 = g < 8 ? (b & 0xFu) : (b >> 4);
-        const uint32_t hi2 = (byte_dyn(hi_w, g & 3) >> (2 * (g >> 2))) & 3u;
-        r.ws[h] = d * (float) ((int) (lo4 | (hi2 << 4)) - 32);
+        const uint32_t hi2 = (((hi_w >> (8 * (g & 3))) & 0xffu) >> (2 * (g >> 2))) & 3u;
+        scv[h] = (int) (lo4 | (hi2 << 4)) - 32;
     }
-    r.wm = 0.0f;
+    const int sc = on ? (kg < 2 ? scv[0] : scv[1]) : 0;
+    BOp<T_Q3_K> r;
+    r.b[0] = centred8(x, y, splat((_Float16) 1028.0f), splat((_Float16) sc));
     return r;
 }
 
-// -dmin * m_s of sub-blocks kg and kg + 4 of this lane's row (Q4_K / Q5_K): the B operand of the fp32 MFMAs that add
-// the min term of a whole block at once.
-template <int T> __device__ __forceinline__ void neg_min_pair(const WFrag<T> &f, int kg, float &m0, float &m1) {
-    if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        int sc, m;
-        const float dmin = half_to_float(f.h.x >> 16);
-        k4_sc_m(f.h, kg, sc, m);
-        m0 = -(dmin * (float) m);
-        k4_sc_m(f.h, kg + 4, sc, m);
-        m1 = -(dmin * (float) m);
-    } else {
-        m0 = m1 = 0.0f;
-    }
+// Per-superblock float scales of this lane's row: d, and dmin for Q4_K / Q5_K.
+template <int T> __device__ __forceinline__ float blk_d(const WFrag<T> &f) {
+    if constexpr (T == T_Q4_K || T == T_Q5_K) return half_to_float(f.h.x & 0xffffu);
+    else if constexpr (T == T_Q6_K) return half_to_float(f.d);
+    else return half_to_float(f.tail.w >> 16);
+}
+// Q4_K / Q5_K min term operand: B[k][row] = m_s for the sums [S_hi 8 | S_lo 8] of the A operand, lane group kg holding
+// k = 4 kg .. 4 kg + 3, i.e. sub-blocks 4 (kg & 1) + (0 2 1 3).
+template <int T> __device__ __forceinline__ v4h min_b(const WFrag<T> &f, int kg) {
+    const uint32_t m_lo = f.h.z & 0x3F3F3F3Fu;                                         // m[0..3]
+    const uint32_t m_hi = ((f.h.w >> 4) & kLo4) | ((f.h.z >> 2) & 0x30303030u);       // m[4..7]
+    const uint32_t mw = (kg & 1) ? m_hi : m_lo;
+    const h2 off = splat((_Float16) 1024.0f);
+    return __builtin_bit_cast(v4h, make_uint2(as_u(biased02(mw) - off), as_u(biased13(mw) - off)));
 }
 
-// LDS of one workgroup: the activation superblock chunk [kMmqTok][kMmqStride] int8 and its per-sub-block d8 and
-// d8 * sum(q8) transposed to [8][kMmqTok]; reused as the act tile [kMmqTok][rows] f32 by the GLU epilogue.
-struct alignas(16) MmqLds {
-    uint8_t q[2][kMmqTok * kMmqStride];  // double-buffered: chunk kb + 1 lands while chunk kb is computed
-    float d8[2][8][kMmqTok];
-    float s8[2][8][kMmqTok];
-    int src[kMmqTok];
-    int dst[kMmqTok];
+// LDS of one workgroup (static, distinct objects, so the compiler can tell the chunk being filled by LDS-DMA from the
+// one being read and puts no wait between them): the half-superblock activation chunks [kMmqTok][512] (hi, lo)
+// double-buffered, with the 16-byte pieces of row r stored at piece index p ^ (r % 16) so that the 16 rows of an
+// A-fragment read hit distinct banks; the superblock min-term sums [kMmqTok][32]. 68.5 KB: two workgroups per CU.
+constexpr int kRowA = 512, kRowS = 32;
+struct MmqShared {
+    uint8_t *a0, *a1, *s;
+    int *src, *dst;
 };
 
-template <int T, bool GLU, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(GLU ? 3 : 1, GLU ? 4 : 8))) void k_mmq(const MmqArgs a) {
-    constexpr int NT = NW * 64, ROWS = NW * 16;  // threads, weight rows per workgroup
-    static_assert(sizeof(float) * kMmqTok * ROWS <= sizeof(MmqLds::q), "act tile fits the chunk buffers");
-    extern __shared__ __align__(16) uint8_t smem_raw[];
-    MmqLds &L = *(MmqLds *) smem_raw;
-    constexpr int BB = Traits<T>::bytes, NG = groups_of<T>();
+// 1 / (1 + e^-g); 0 for g -> -inf (the exponential saturates to +inf), 1 for g -> +inf
+__device__ __forceinline__ float silu_rcp(float g) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
+
+__device__ __forceinline__ v4f mfma32(v8h a, v8h b, v4f c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+
+// Workgroup barrier for LDS filled by LDS-DMA: the DMA data is complete once this wave's vmcnt wait before it retires
+// (waits placed by the caller: __syncthreads' fence would also wait for the weight loads still in flight). This
+// wave's own LDS reads must have returned (lgkmcnt 0) before the next DMA into the buffer may start, and the asm's
+// memory clobber keeps the compiler from moving LDS accesses across it (the s_barrier builtin is not a memory op).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void *LdsPtr;
+// 16 bytes per lane from r at (vo + so) into LDS at dst + 16 lane (dst wave-uniform)
+__device__ __forceinline__ void dma16(Rsrc r, void *dst, uint32_t vo, uint32_t so) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr) dst, 16, vo, so, 0, 0);
+}
+// vector loads issued by wfrag_load for one stream (they complete in order with the DMA issued before them)
+template <int T> constexpr int wfrag_loads() { return T == T_Q4_K ? 5 : T == T_Q5_K ? 6 : T == T_Q6_K ? 8 : 4; }
+
+// One workgroup = 4 waves x two 16-row weight streams x up to 16 NT routed activation rows of one expert (NT = 4: the
+// 64-row groups and remainders > 32 rows; NT = 2: remainders <= 32 rows). GLU: stream 0 is the gate row, stream 1 the
+// same up row (64 rows per workgroup); otherwise the streams are rows r and r + 64 (128).
+template <int T, bool GLU, int NT>
+__global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 4))) void k_mmq(const MmqArgs a) {
+    constexpr int ROWS = 16 * NT;  // activation rows of the workgroup
+    __shared__ __align__(16) uint8_t sh_a0[ROWS * kRowA];
+    __shared__ __align__(16) uint8_t sh_a1[ROWS * kRowA];
+    __shared__ __align__(16) uint8_t sh_s[ROWS * kRowS];
+    __shared__ int sh_src[ROWS], sh_dst[ROWS];
+    constexpr int BB = Traits<T>::bytes, NB = T == T_Q6_K ? 2 : 1;
+    constexpr bool MIN = T == T_Q4_K || T == T_Q5_K;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int kg = lane / 16, jl = lane % 16;
 
@@ -380,241 +432,319 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(GLU ? 3
             else hi = mid;
         }
         e = lo;
-        seg = a.bounds[e] + (g - a.gprefix[e]) * kMmqTok;
-        cnt = min(kMmqTok, a.bounds[e + 1] - seg);
+        if (a.tail) {  // the expert's last rows: n_e % 64 of them
+            cnt = (a.bounds[e + 1] - a.bounds[e]) % kMmqTok;
+            seg = a.bounds[e + 1] - cnt;
+        } else {
+            seg = a.bounds[e] + (g - a.gprefix[e]) * kMmqTok;
+            cnt = min(kMmqTok, a.bounds[e + 1] - seg);
+        }
     } else {
         seg = blockIdx.x * kMmqTok;
         cnt = min(kMmqTok, a.n_rows - seg);
     }
     if (cnt <= 0) return;
-    const int ntile = (cnt + 15) / 16;
-    for (int i = tid; i < kMmqTok; i += NT) {
+    for (int i = tid; i < ROWS; i += kMmqThreads) {
         const int q = seg + min(i, cnt - 1);
-        L.src[i] = a.src ? a.src[q] : q;
-        L.dst[i] = a.dst_rows ? a.dst_rows[q] : q;
+        sh_src[i] = a.src ? a.src[q] : q;
+        sh_dst[i] = a.dst_rows ? a.dst_rows[q] : q;
     }
 
     const uint8_t *wbase = a.table ? (const uint8_t *) gload<const char *>((const uint8_t *) (a.table + e)) : a.w_dense;
-    const int row = blockIdx.y * ROWS + wave * 16 + jl;  // this lane's weight row
     const int nb = a.ncols / 256;
     const int64_t row_bytes = (int64_t) nb * BB;
-    const uint8_t *wa = wbase + a.off_a + (int64_t) row * row_bytes;
-    const uint8_t *wb = GLU ? wbase + a.off_b + (int64_t) row * row_bytes : nullptr;
-    const int npad = (a.ncols + 511) / 512 * 512;
-    const int qbytes = img_q_bytes(npad);
+    const int row0 = GLU ? blockIdx.y * 64 + wave * 16 + jl : blockIdx.y * 128 + wave * 16 + jl;
+    const int row1 = GLU ? row0 : min(row0 + 64, a.nrows - 1);  // past the end (nrows % 128 == 64): computed, not stored
+    const Rsrc r0 = rsrc_of(wbase + a.off_a), r1 = rsrc_of(wbase + (GLU ? a.off_b : a.off_a)), rx = rsrc_of(a.xpack);
+    const uint32_t v0 = (uint32_t) (row0 * row_bytes), v1 = (uint32_t) (row1 * row_bytes);
+    __syncthreads();  // sh_src / sh_dst
 
-    v4f acc[kMmqTiles], accu[kMmqTiles];
+    // LDS-DMA of chunk (kb, h) - columns 256 kb + 128 h .. + 127, hi and lo: 512 bytes per row - by instruction u of
+    // wave w: rows 8 u + 2 w, + 1 (one per 32 lanes; lane piece i of row r reads image piece i ^ (r % 16))
+    constexpr int NU = ROWS / 8;
+    uint32_t qo[NU];
 #pragma unroll
-    for (int t = 0; t < kMmqTiles; ++t) acc[t] = accu[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-    WFrag<T> fa, fb, na, nb2;
-    wfrag_load<T>(wa, kg, fa);
-    if constexpr (GLU) wfrag_load<T>(wb, kg, fb);
-    __syncthreads();  // L.src / L.dst
-
-    // staging of superblock chunk kb into buffer kb & 1 through registers (an LDS-DMA would make every LDS read of the
-    // compute loop wait for the prefetch): 18 pieces of 16 bytes per row - the 256 q bytes + 32 bytes of padding read
-    // from what follows them in the same image row - loaded by load_q, written by store_q after the compute; d8 and
-    // d8 * sum(q8) of the chunk's 8 sub-blocks likewise (load_scales / store_scales, stored transposed)
-    const int nrow = ntile * 16, npiece = nrow * (kMmqStride / 16);
-    constexpr int kPieces = (kMmqTok * (kMmqStride / 16) + NT - 1) / NT;
-    uint4 qv0, qv1, qv2, qv3, qv4;  // kPieces = 5 pieces per thread (named: keeps them out of scratch)
-    static_assert(kPieces <= 5, "staging registers");
-    // byte offset (from a.xpack) of each of this thread's staging pieces in chunk 0; chunk kb adds kb * kImgQRow
-    uint32_t qo0 = 0, qo1 = 0, qo2 = 0, qo3 = 0, qo4 = 0;
-    {
-        uint32_t *qo[5] = {&qo0, &qo1, &qo2, &qo3, &qo4};
+    for (int u = 0; u < NU; ++u) {
+        const int r = 8 * u + 2 * wave + lane / 32;
+        qo[u] = (uint32_t) ((size_t) sh_src[r] * a.x_img + 16 * ((lane % 32) ^ (r % 16)));
+    }
+    // min-term sums of superblock kb: rows 32 w' + lane / 2 (2 pieces per row), w' = wave % (ROWS / 32)
+    const int srow = 32 * (wave % (ROWS / 32));
+    const uint32_t so = (uint32_t) ((size_t) sh_src[srow + lane / 2] * a.x_img + (size_t) nb * kSbMain + 16 * (lane & 1));
+    // (unconditional: a fixed number of loads in flight keeps the compiler's wait counts exact; rows past cnt read
+    // the last routed row again)
+    auto dma_chunk = [&](uint8_t *buf, int kb, int h) __attribute__((always_inline)) {
+        const uint32_t soff = (uint32_t) (kb * kSbMain + h * 512);
 #pragma unroll
-        for (int u = 0; u < kPieces; ++u) {
-            const int p = tid + u * NT;
-            if (p < npiece) {
-                const int i = p / (kMmqStride / 16), o = 16 * (p % (kMmqStride / 16));
-                *qo[u] = (uint32_t) ((size_t) L.src[i] * a.x_img + o);
+        for (int u = 0; u < NU; ++u) dma16(rx, buf + (8 * u + 2 * wave) * kRowA, qo[u], soff);
+    };
+    auto dma_sums = [&](int kb) __attribute__((always_inline)) {  // the waves past ROWS / 32 repeat the first ones
+        if constexpr (MIN) dma16(rx, sh_s + srow * kRowS, so, (uint32_t) (kb * kSbMin));
+    };
+
+    WFrag<T> f0, f1, n0, n1;
+    dma_chunk(sh_a0, 0, 0);
+    dma_sums(0);
+    wfrag_load<T>(r0, v0, 0, kg, f0);
+    wfrag_load<T>(r1, v1, 0, kg, f1);
+    dma_wait();
+    lds_barrier();
+
+    // acc[t][m] is kept in units of the current superblock's d (per lane: its row's d, 1 if d = 0), so the MFMAs
+    // accumulate into it directly; between superblocks it is rescaled and the min term added (fp32 rounding).
+    // All four tiles are computed whatever cnt (rows past it hold stale LDS data and are never stored).
+    v4f acc[NT][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float ds0 = blk_d<T>(f0), ds1 = blk_d<T>(f1);
+    bool on0 = ds0 != 0.0f, on1 = ds1 != 0.0f;
+    ds0 = on0 ? ds0 : 1.0f;
+    ds1 = on1 ? ds1 : 1.0f;
+
+    // four sub-blocks of one half from LDS chunk buf: acc[t][m] += A (hi, lo) x B (integer-scaled codes)
+    // Software-pipelined: while the MFMAs of sub-block s issue, the A fragments of s + 1 are read from LDS and its B
+    // operands decoded (VALU), interleaved one MFMA / a few VALU so the two pipes overlap within the wave.
+    auto load_a = [&](const uint8_t *buf, int s4, v8h (&av)[2][NT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint8_t *ap = buf + (t * 16 + jl) * kRowA;
+            av[0][t] = *(const v8h *) (ap + 16 * ((4 * s4 + kg) ^ jl));
+            av[1][t] = *(const v8h *) (ap + 16 * ((16 + 4 * s4 + kg) ^ jl));
+        }
+    };
+    auto half_pass = [&](const uint8_t *buf, auto hc, const WFrag<T> &f0, const WFrag<T> &f1) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value;
+        v8h av[2][NT], an[2][NT];
+        BOp<T> b0 = decode<T>(f0, 4 * h, kg, on0), b1 = decode<T>(f1, 4 * h, kg, on1), c0, c1;
+        load_a(buf, 0, av);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (s4 < 3) {
+                load_a(buf, s4 + 1, an);
+                c0 = decode<T>(f0, 4 * h + s4 + 1, kg, on0);
+                c1 = decode<T>(f1, 4 * h + s4 + 1, kg, on1);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int g = 0; g < NB; ++g) {
+                    acc[t][0] = mfma32(av[0][t], b0.b[g], acc[t][0]);
+                    acc[t][1] = mfma32(av[0][t], b1.b[g], acc[t][1]);
+                    acc[t][0] = mfma32(av[1][t], b0.b[g], acc[t][0]);
+                    acc[t][1] = mfma32(av[1][t], b1.b[g], acc[t][1]);
+                }
+            if (s4 < 3) {
+                // order: the 2 NT LDS reads first, then MFMA / 3 VALU pairs
+#pragma unroll
+                for (int i = 0; i < 2 * NT; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+                for (int i = 0; i < 4 * NT * NB; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    av[0][t] = an[0][t];
+                    av[1][t] = an[1][t];
+                }
+                b0 = c0;
+                b1 = c1;
             }
         }
-    }
-#define FNS_LOAD_Q(kb)                                                                                              \
-    do {                                                                                                            \
-        uint4 *dstv[5] = {&qv0, &qv1, &qv2, &qv3, &qv4};                                                            \
-        const uint32_t offv[5] = {qo0, qo1, qo2, qo3, qo4};                                                         \
-        _Pragma("unroll") for (int u = 0; u < kPieces; ++u) {                                                       \
-            if (tid + u * NT < npiece)                                                                              \
-                *dstv[u] = *(const uint4 *) (a.xpack + offv[u] + (kb) * kImgQRow);                                  \
-        }                                                                                                           \
-    } while (0)
-#define FNS_STORE_Q(kb)                                                                                             \
-    do {                                                                                                            \
-        const uint4 srcv[5] = {qv0, qv1, qv2, qv3, qv4};                                                            \
-        _Pragma("unroll") for (int u = 0; u < kPieces; ++u) {                                                       \
-            const int p = tid + u * NT;                                                                             \
-            if (p < npiece) *(uint4 *) (L.q[(kb) & 1] + 16 * p) = srcv[u];                                          \
-        }                                                                                                           \
-    } while (0)
-    float sv[8];
-    const float *sbase = nullptr;  // this thread's d8 (even) or d8 * sum(q8) (odd thread) row of its token
-    if (tid < 2 * kMmqTok && (tid >> 1) < cnt)
-        sbase = (const float *) (a.xpack + (size_t) L.src[tid >> 1] * a.x_img + qbytes) +
-                ((tid & 1) ? npad / 32 + npad / 16 : 0);
-    auto load_scales = [&](int kb) {
-        if (tid < 2 * kMmqTok) {
-            if (sbase) {
-                const float *f = sbase + 8 * kb;
-                const float4 v0 = *(const float4 *) f, v1 = *(const float4 *) (f + 4);
-                sv[0] = v0.x, sv[1] = v0.y, sv[2] = v0.z, sv[3] = v0.w;
-                sv[4] = v1.x, sv[5] = v1.y, sv[6] = v1.z, sv[7] = v1.w;
+    };
+
+    // one superblock with fragments f0, f1 (current) and n0, n1 (next, loaded here)
+    auto superblock = [&](int kb, const WFrag<T> &f0, const WFrag<T> &f1, WFrag<T> &n0, WFrag<T> &n1)
+                          __attribute__((always_inline)) {
+        const bool more = kb + 1 < nb;
+        const int kn = more ? kb + 1 : kb;  // the last superblock reloads itself: same load count every iteration
+        dma_chunk(sh_a1, kb, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        // next superblock's weights: a whole superblock of compute to land
+        wfrag_load<T>(r0, v0, kn * BB, kg, n0);
+        wfrag_load<T>(r1, v1, kn * BB, kg, n1);
+        __builtin_amdgcn_sched_barrier(0);
+        half_pass(sh_a0, std::integral_constant<int, 0>{}, f0, f1);
+        __builtin_amdgcn_sched_barrier(0);
+        // chunk (kb, 1) landed (only the weight loads issued after it may still be in flight)
+        constexpr int kPend = 2 * wfrag_loads<T>();  // s_waitcnt vmcnt(kPend): vmcnt bits 3:0 and 15:14
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (kPend & 0xF) | ((kPend >> 4) << 14));
+        lds_barrier();  // chunk (kb, 1) visible; chunk buffer 0 free
+
+        dma_chunk(sh_a0, kn, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        half_pass(sh_a1, std::integral_constant<int, 1>{}, f0, f1);
+        __builtin_amdgcn_sched_barrier(0);
+        // superblock done: acc <- (acc ds - dmin (m . S)) / ds_next, ds_next = 1 after the last superblock
+        float nd0 = 1.0f, nd1 = 1.0f;
+        bool non0 = true, non1 = true;
+        dma_wait();  // the next weights (and chunk (kb + 1, 0))
+        if (more) {
+            nd0 = blk_d<T>(n0);
+            nd1 = blk_d<T>(n1);
+            non0 = nd0 != 0.0f;
+            non1 = nd1 != 0.0f;
+            nd0 = non0 ? nd0 : 1.0f;
+            nd1 = non1 ? nd1 : 1.0f;
+        }
+        const float inv0 = __builtin_amdgcn_rcpf(nd0), inv1 = __builtin_amdgcn_rcpf(nd1);
+        const float k0 = ds0 * inv0, k1 = ds1 * inv1;
+        float km0 = 0.0f, km1 = 0.0f;
+        v4h bm0, bm1;
+        if constexpr (MIN) {
+            km0 = -half_to_float(f0.h.x >> 16) * inv0;
+            km1 = -half_to_float(f1.h.x >> 16) * inv1;
+            bm0 = min_b<T>(f0, kg);
+            bm1 = min_b<T>(f1, kg);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if constexpr (MIN) {
+                const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const v4h am = *(const v4h *) (sh_s + (t * 16 + jl) * kRowS + 8 * kg);
+                const v4f m0 = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm0, z, 0, 0, 0);
+                const v4f m1 = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm1, z, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc[t][0][r] = fmaf_(acc[t][0][r], k0, km0 * m0[r]);
+                    acc[t][1][r] = fmaf_(acc[t][1][r], k1, km1 * m1[r]);
+                }
             } else {
 #pragma unroll
-                for (int s = 0; s < 8; ++s) sv[s] = 0.0f;
-            }
-        }
-    };
-    auto store_scales = [&](int kb) {
-        if (tid < 2 * kMmqTok) {
-            const int i = tid >> 1, which = tid & 1;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) (which ? L.s8[kb & 1] : L.d8[kb & 1])[s][i] = sv[s];
-        }
-    };
-    FNS_LOAD_Q(0);
-    load_scales(0);
-    FNS_STORE_Q(0);
-    store_scales(0);
-    // every load of the prologue (fa / fb included) complete before the loop: the compiler's wait analysis merges the
-    // loop-entry state into every iteration, and a pending fa there would put a full wait in front of each sub-block
-    dma_wait();
-    __syncthreads();
-
-    for (int kb = 0; kb < nb; ++kb) {
-        const int cur = kb & 1;
-        if (kb + 1 < nb) {  // next chunk and next block's weights in flight while this one is computed
-            FNS_LOAD_Q(kb + 1);
-            load_scales(kb + 1);
-            wfrag_load<T>(wa + (int64_t) (kb + 1) * BB, kg, na);
-            if constexpr (GLU) wfrag_load<T>(wb + (int64_t) (kb + 1) * BB, kg, nb2);
-        }
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            if (s % 2 == 0) __builtin_amdgcn_sched_barrier(0);  // pairs of sub-blocks: bounded live ranges
-            const SubB<T> ba = sub_b<T>(fa, s, kg);
-            SubB<T> bu;
-            if constexpr (GLU) bu = sub_b<T>(fb, s, kg);
-#pragma unroll
-            for (int t = 0; t < kMmqTiles; ++t) {
-                if (t < ntile) {
-                    const long av = *(const long *) (L.q[cur] + (t * 16 + jl) * kMmqStride + 32 * s + 8 * kg);
-                    const float4 d8 = *(const float4 *) &L.d8[cur][s][t * 16 + 4 * kg];
-                    const float dd[4] = {d8.x, d8.y, d8.z, d8.w};
-#pragma unroll
-                    for (int g = 0; g < NG; ++g) {
-                        const v4i z = {0, 0, 0, 0};
-                        const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, ba.b[g], z, 0, 0, 0);
-                        v4i cu = z;
-                        if constexpr (GLU) cu = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bu.b[g], z, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            acc[t][r] = fmaf_((float) ci[r], ba.ws[g] * dd[r], acc[t][r]);
-                            if constexpr (GLU) accu[t][r] = fmaf_((float) cu[r], bu.ws[g] * dd[r], accu[t][r]);
-                        }
-                    }
+                for (int r = 0; r < 4; ++r) {
+                    acc[t][0][r] *= k0;
+                    acc[t][1][r] *= k1;
                 }
             }
         }
-        if constexpr (NG == 1) {
-            // min term of the whole block: acc[token][row] -= sum_s dmin m_s (d8 sum q8)_s as two fp32 MFMAs
-            // (A = d8 sum q8 of sub-blocks kg, kg + 4 per token, B = -dmin m of the same sub-blocks per row)
-            float ma0, ma1, mb0 = 0.0f, mb1 = 0.0f;
-            neg_min_pair<T>(fa, kg, ma0, ma1);
-            if constexpr (GLU) neg_min_pair<T>(fb, kg, mb0, mb1);
-#pragma unroll
-            for (int t = 0; t < kMmqTiles; ++t) {
-                if (t < ntile) {
-                    const float x0 = L.s8[cur][kg][t * 16 + jl], x1 = L.s8[cur][kg + 4][t * 16 + jl];
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0, ma0, acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1, ma1, acc[t], 0, 0, 0);
-                    if constexpr (GLU) {
-                        accu[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0, mb0, accu[t], 0, 0, 0);
-                        accu[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1, mb1, accu[t], 0, 0, 0);
-                    }
-                }
-            }
-        }
-        if (kb + 1 < nb) {
-            FNS_STORE_Q(kb + 1);
-            store_scales(kb + 1);
-            fa = na;
-            if constexpr (GLU) fb = nb2;
-        }
-        __syncthreads();  // chunk kb + 1 visible; buffer kb & 1 free for chunk kb + 2
+        ds0 = nd0;
+        ds1 = nd1;
+        on0 = non0;
+        on1 = non1;
+        lds_barrier();  // chunk (kb + 1, 0) visible; chunk buffer 1 and the sums free
+        dma_sums(kn);  // read at the end of superblock kb + 1, after its first barrier
+    };
+    // the fragment sets swap roles every superblock
+    for (int kb = 0; kb < nb; kb += 2) {
+        superblock(kb, f0, f1, n0, n1);
+        if (kb + 1 < nb) superblock(kb + 1, n0, n1, f0, f1);
     }
 
-#undef FNS_LOAD_Q
-#undef FNS_STORE_Q
+    dma_wait();  // the last (unused) sums load
     if constexpr (!GLU) {
 #pragma unroll
-        for (int t = 0; t < kMmqTiles; ++t)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = t * 16 + 4 * kg + r;
-                if (t < ntile && i < cnt) a.dst[(size_t) L.dst[i] * a.nrows + row] = acc[t][r];
-            }
-    } else {
-        // act = up * silu(gate) (reference src/ggml/ggml_mmvq.cu:240-247 epilogue with zero biases), staged as
-        // [token][ROWS] f32, then one Q8_1 block per (token, 32 rows) into the act image rows.
-        constexpr int NB = ROWS / 32;  // Q8_1 blocks per token
-        float *act = (float *) &L.q[0][0];
-#pragma unroll
-        for (int t = 0; t < kMmqTiles; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = t * 16 + 4 * kg + r;
-                if (t < ntile) {
-                    float v = accu[t][r] + 0.0f;
-                    v *= silu(acc[t][r] + 0.0f);
-                    act[i * ROWS + wave * 16 + jl] = v;
+                if (i < cnt) {
+                    float *o = a.dst + (size_t) sh_dst[i] * a.nrows;
+                    o[row0] = acc[t][0][r];
+                    if (row0 + 64 < a.nrows) o[row0 + 64] = acc[t][1][r];
                 }
             }
+    } else {
+        // act = up * silu(gate) (reference src/ggml/ggml_mmvq.cu:240-247 epilogue with zero biases; silu(g) =
+        // g / (1 + e^-g) from the hardware exp2 and reciprocal, about 2 ulp), staged as
+        // [token][64 rows] f32 (row stride 68 floats: 16-byte aligned rows, the 64 lanes' writes on distinct banks),
+        // then the Q8_1 blocks (token, 32 rows) into the act split image rows: 4 lanes per block, 8 values per lane
+        constexpr int kAct = 68;
+        static_assert(ROWS * kAct * 4 <= (int) sizeof(sh_a0), "act tile fits a chunk buffer");
+        float *act = (float *) sh_a0;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = t * 16 + 4 * kg + r;
+                const float g = acc[t][0][r] + 0.0f;
+                act[i * kAct + wave * 16 + jl] = (acc[t][1][r] + 0.0f) * (g * silu_rcp(g));
+            }
         __syncthreads();
-        const int fpad = (a.nrows + 511) / 512 * 512;
-        for (int p0 = wave * 2; p0 < NB * cnt; p0 += 2 * NW) {  // wave-uniform trip count
-            const int p = p0 + lane / 32;
-            const bool live = p < NB * cnt;
-            const int i = live ? p / NB : 0, blk = p % NB;
-            const int col = blockIdx.y * ROWS + 32 * blk + lane % 32;
-            const float v = live ? act[i * ROWS + 32 * blk + lane % 32] : 0.0f;
-            const Q8Lane q = q8_1_lane(v);
+        for (int p0 = wave * 16; p0 < 2 * cnt; p0 += 16 * kMmqWaves) {  // wave-uniform trip count
+            const int p = p0 + lane / 4, q = lane % 4;
+            const bool live = p < 2 * cnt;
+            const int i = live ? p / 2 : 0, blk = p % 2;
+            const float *src = act + i * kAct + 32 * blk + 8 * q;
+            const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+            const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            // Q8_1 with the reference's arithmetic (d = amax / 127, q = roundf(v / d)); max and the integer sum are
+            // exact in any order
+            float amax = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+            amax = lanes_max<4>(amax);
+            const float d = amax / 127.0f;
+            const float dh = half_to_float(float_to_half(d));
+            int qsum = 0;
+            _Float16 hi[8], lo[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int qk = amax == 0.0f ? 0 : (int) (int8_t) roundf(v[k] / d);
+                qsum += qk;
+                const float x = (float) qk * dh;  // exact
+                const _Float16 h = (_Float16) x;
+                hi[perm8(k)] = h;
+                lo[perm8(k)] = (_Float16) (x - (float) h);
+            }
+            qsum = lanes_sum_i<4>(qsum);
             if (live) {
-                img_store(a.out_pack + (size_t) L.dst[i] * a.out_img, fpad, col, q);
-                if (a.act_out) a.act_out[(size_t) L.dst[i] * a.nrows + col] = v;
+                const int col = blockIdx.y * 64 + 32 * blk + 8 * q;
+                uint8_t *row = a.out_pack + (size_t) sh_dst[i] * a.out_img;
+                uint8_t *o = row + (size_t) (col >> 8) * kSbMain + ((col >> 7) & 1) * 512 + ((col & 127) >> 3) * 16;
+                *(uint4 *) o = __builtin_bit_cast(uint4, hi);
+                *(uint4 *) (o + 256) = __builtin_bit_cast(uint4, lo);
+                if (q == 0) {
+                    const float sv = dh * (float) qsum;  // exact in fp32
+                    const _Float16 shi = (_Float16) sv, slo = (_Float16) (sv - (float) shi);
+                    _Float16 *m = (_Float16 *) (row + (size_t) (a.nrows >> 8) * kSbMain + (size_t) (col >> 8) * kSbMin);
+                    const int si = perm8((col >> 5) & 7);
+                    m[si] = shi;
+                    m[8 + si] = slo;
+                }
+                if (a.act_out) {
+                    float *ao = a.act_out + (size_t) sh_dst[i] * a.nrows + col;
+                    *(float4 *) ao = x0;
+                    *(float4 *) (ao + 4) = x1;
+                }
             }
         }
     }
 }
 
-template <bool GLU, int NW> const void *mmq_kernel(int type) {
+template <bool GLU, int NT> const void *mmq_kernel(int type) {
     switch (type) {
-        case T_Q3_K: return (const void *) k_mmq<T_Q3_K, GLU, NW>;
-        case T_Q4_K: return (const void *) k_mmq<T_Q4_K, GLU, NW>;
-        case T_Q5_K: return (const void *) k_mmq<T_Q5_K, GLU, NW>;
-        case T_Q6_K: return (const void *) k_mmq<T_Q6_K, GLU, NW>;
+        case T_Q3_K: return (const void *) k_mmq<T_Q3_K, GLU, NT>;
+        case T_Q4_K: return (const void *) k_mmq<T_Q4_K, GLU, NT>;
+        case T_Q5_K: return (const void *) k_mmq<T_Q5_K, GLU, NT>;
+        case T_Q6_K: return (const void *) k_mmq<T_Q6_K, GLU, NT>;
     }
     return nullptr;
 }
 
-int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
-    // the plain launch takes 128 rows per workgroup when nrows allows: twice the weight rows per staged activation
-    // (the gate/up launch stays at 4 waves: at 8 its register budget leaves one workgroup per CU - measured slower)
-    const bool wide = !glu && a.nrows % (16 * kMmqWavesWide) == 0;
-    const int nw = wide ? kMmqWavesWide : 4;
-    const void *fn = glu ? mmq_kernel<true, 4>(type)
-                         : (wide ? mmq_kernel<false, kMmqWavesWide>(type) : mmq_kernel<false, 4>(type));
-    if (!fn) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
+int launch_one(const void *fn, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
     if (groups <= 0) return host::OK;
     MmqArgs arg = a;
     void *args[] = {&arg};
-    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) groups, (unsigned) (a.nrows / (16 * nw))),
-                                         dim3(64 * nw), args, sizeof(MmqLds), st);
+    const int rows = glu ? 64 : 128;
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) groups, (unsigned) ((a.nrows + rows - 1) / rows)),
+                                         dim3(kMmqThreads), args, 0, st);
     if (e != hipSuccess) return host::set_error(host::ERR_LAUNCH, "mmq: %s", hipGetErrorString(e));
     return host::check_launch("mmq");
+}
+
+// groups: upper bound of the 4-tile list (its kernel returns past the device-side count); expert path: then the
+// 2-tile kernel over the <= 32-row remainders (at most one per expert), with the second prefix list
+int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
+    const void *f4 = glu ? mmq_kernel<true, 4>(type) : mmq_kernel<false, 4>(type);
+    const void *f2 = glu ? mmq_kernel<true, 2>(type) : mmq_kernel<false, 2>(type);
+    if (!f4 || !f2) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
+    FNS_TRY(launch_one(f4, glu, a, groups, st));
+    if (!a.bounds) return host::OK;
+    MmqArgs t = a;
+    t.gprefix = a.gprefix + a.n_expert + 1;
+    t.tail = 1;
+    return launch_one(f2, glu, t, a.n_expert, st);
 }
 
 int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
@@ -623,21 +753,19 @@ int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
         return host::set_error(host::ERR_SHAPE, "mmq: ncols must be a positive multiple of 256, nrows of 64");
     return host::OK;
 }
-
 }  // namespace
 
 namespace impl {
 
-size_t mmq_image_bytes(int64_t ncols) { return (size_t) img_bytes((int) host::pad512(ncols)); }
+size_t mmq_image_bytes(int64_t ncols) { return (size_t) split_row_bytes(ncols); }
 size_t mmq_q8_1_bytes(int64_t ncols, int64_t nrows) { return (size_t) nrows * mmq_image_bytes(ncols) + 4096; }
 size_t mmq_bounds_bytes(int64_t n_expert) { return bounds_bytes(n_expert); }
 
 int mmq_quant_image(const float *x, int64_t ncols, int64_t rows, void *xpack, hipStream_t st) {
-    if (!x || !xpack || ncols <= 0 || rows < 0 || rows > 65535)
+    if (!x || !xpack || ncols <= 0 || ncols % 256 || ncols > 65536 || rows < 0 || rows > 65535)
         return host::set_error(host::ERR_SHAPE, "mmq quantize: bad arguments");
     if (rows == 0) return host::OK;
-    const int64_t npad = host::pad512(ncols);
-    hipLaunchKernelGGL(k_quant_image, dim3((unsigned) (npad / 256), (unsigned) rows), dim3(256), 0, st, x, ncols,
+    hipLaunchKernelGGL(k_quant_image, dim3((unsigned) (ncols / 256), (unsigned) rows), dim3(256), 0, st, x, (int) ncols,
                        (uint8_t *) xpack, (int64_t) mmq_image_bytes(ncols));
     return host::check_launch("mmq quantize");
 }
@@ -745,7 +873,7 @@ int moe_prefill_workspace(const FnsMoeLayer *L, int64_t n_tok, size_t *offsets, 
         if (offsets && i < 6) offsets[i] = off;
         off += (sz[i] + 255) / 256 * 256;
     }
-    if (total) *total = off + 4096;  // slack: the GEMM reads 32 bytes past a row's q values inside its image row
+    if (total) *total = off + 4096;
     return host::OK;
 }
 

@@ -131,6 +131,19 @@ def test_mmq_dense(ops):
     assert_close(got, ref, "mmq dense Q4_K")
 
 
+@pytest.mark.parametrize("qtype", [orc.Q4_K, orc.Q6_K])
+def test_mmq_repeatable(ops, qtype):
+    """Repeated launches give bit-identical outputs (a missing wait between the LDS-DMA staging, the workgroup barriers
+    and the LDS reads shows up as run-to-run differences); odd superblock count, ragged groups, two row blocks."""
+    T, ncols, nrows = 130, 768, 192
+    rng = np.random.default_rng(5)
+    w = dev(make_expert_mats(qtype, 1, nrows, ncols, 78)[0])
+    x = dev(gaussian(rng, (T, ncols)))
+    first = host(ops.mmq(qtype, w, ncols, nrows, x))
+    for _ in range(8):
+        assert np.array_equal(host(ops.mmq(qtype, w, ncols, nrows, x)), first)
+
+
 def _oracle_layer_tokens(layer, slots_np, x, toks, ids, w, gu, dn, H, F):
     """float64 chain per token: act = swiglu(gate . q8(x), up . q8(x)); out = sum_j w_j down . q8(act_j)."""
     xq = orc.quantize_q8_1(x[toks])
