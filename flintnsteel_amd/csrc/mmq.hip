@@ -668,19 +668,21 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
             const float *src = act + i * kAct + 32 * blk + 8 * q;
             const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
             const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            // Q8_1 with the reference's arithmetic (d = amax / 127, q = roundf(v / d)); max and the integer sum are
-            // exact in any order
+            // Q8_1 (d = amax / 127, q = roundf(v / d)); max and the integer sum are exact in any order
             float amax = 0.0f;
 #pragma unroll
             for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
             amax = lanes_max<4>(amax);
             const float d = amax / 127.0f;
             const float dh = half_to_float(float_to_half(d));
+            // v / d as v * (1 / d): one division per block (act itself is an fp32 GEMM result, not bit-comparable
+            // with the reference's, so the quotient's last-ulp rounding carries no parity)
+            const float id = amax == 0.0f ? 0.0f : 1.0f / d;
             int qsum = 0;
             _Float16 hi[8], lo[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const int qk = amax == 0.0f ? 0 : (int) (int8_t) roundf(v[k] / d);
+                const int qk = (int) (int8_t) roundf(v[k] * id);
                 qsum += qk;
                 const float x = (float) qk * dh;  // exact
                 const _Float16 h = (_Float16) x;
