@@ -156,31 +156,55 @@ constexpr int kSbMain = 1024, kSbMin = 32;
 __host__ __device__ constexpr int64_t split_row_bytes(int64_t ncols) { return ncols / 256 * (kSbMain + kSbMin); }
 __device__ __forceinline__ int perm8(int k) { return (k & ~3) | ((k & 1) << 1) | ((k >> 1) & 1); }
 
-__device__ __forceinline__ void split_store(uint8_t *row, int ncols, int i, const Q8Lane &r) {
-    const float dh = half_to_float(float_to_half(r.d));
-    const float v = (float) r.q * dh;  // exact
-    const _Float16 hi = (_Float16) v;
-    const _Float16 lo = (_Float16) (v - (float) hi);
-    _Float16 *p = (_Float16 *) (row + (size_t) (i >> 8) * kSbMain + ((i >> 7) & 1) * 512);
-    const int pos = perm8(i & 127);
-    p[pos] = hi;
-    p[128 + pos] = lo;
-    if ((i & 31) == 0) {
-        const float s = dh * (float) r.qsum32;  // exact in fp32
-        const _Float16 shi = (_Float16) s, slo = (_Float16) (s - (float) shi);
-        _Float16 *m = (_Float16 *) (row + (size_t) (ncols >> 8) * kSbMain + (size_t) (i >> 8) * kSbMin);
-        const int si = perm8((i >> 5) & 7);
+// Q8_1 of 8 consecutive values per lane, 4 lanes per 32-value block (lanes 4j .. 4j + 3 of a quad, all active), into
+// the split image row `row` at column col (a multiple of 8): d = amax / 127, q = roundf(v / d) - with an IEEE
+// division per value (EXACT: the reference's arithmetic, bit for bit) or v * (1 / d). The max and the integer sum are
+// exact in any order. Returns nothing; lane q = 0 of the block also stores its min-term sums.
+template <bool EXACT>
+__device__ __forceinline__ void q8_split8(const float (&v)[8], uint8_t *row, int ncols, int col, bool store) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    amax = lanes_max<4>(amax);
+    const float d = amax / 127.0f;
+    const float dh = half_to_float(float_to_half(d));
+    const float id = amax == 0.0f ? 0.0f : 1.0f / d;
+    int qsum = 0;
+    _Float16 hi[8], lo[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int qk = amax == 0.0f ? 0 : (int) (int8_t) roundf(EXACT ? v[k] / d : v[k] * id);
+        qsum += qk;
+        const float x = (float) qk * dh;  // exact
+        const _Float16 h = (_Float16) x;
+        hi[perm8(k)] = h;
+        lo[perm8(k)] = (_Float16) (x - (float) h);
+    }
+    qsum = lanes_sum_i<4>(qsum);
+    if (!store) return;
+    uint8_t *o = row + (size_t) (col >> 8) * kSbMain + ((col >> 7) & 1) * 512 + ((col & 127) >> 3) * 16;
+    *(uint4 *) o = __builtin_bit_cast(uint4, hi);
+    *(uint4 *) (o + 256) = __builtin_bit_cast(uint4, lo);
+    if ((col & 31) == 0) {
+        const float sv = dh * (float) qsum;  // exact in fp32
+        const _Float16 shi = (_Float16) sv, slo = (_Float16) (sv - (float) shi);
+        _Float16 *m = (_Float16 *) (row + (size_t) (ncols >> 8) * kSbMain + (size_t) (col >> 8) * kSbMin);
+        const int si = perm8((col >> 5) & 7);
         m[si] = shi;
         m[8 + si] = slo;
     }
 }
 
-// x [rows][ncols] f32 -> split image rows (reference Q8_1 arithmetic, q8_1_lane); grid (ncols / 256, rows), 256 threads.
+// x [rows][ncols] f32 -> split image rows with the reference's Q8_1 arithmetic; grid (ceil(ncols / 2048), rows), 256
+// threads of 8 columns each (ncols % 256 == 0, so a block's 4 lanes are all in or all out).
 __global__ __launch_bounds__(256) void k_quant_image(const float *__restrict__ x, int ncols, uint8_t *__restrict__ out,
                                                      int64_t img_row_bytes) {
-    const int row = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
-    const Q8Lane r = q8_1_lane(x[(size_t) row * ncols + i]);
-    split_store(out + (size_t) row * img_row_bytes, ncols, i, r);
+    const int row = blockIdx.y, col = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (col >= ncols) return;
+    const float *src = x + (size_t) row * ncols + col;
+    const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    q8_split8<true>(v, out + (size_t) row * img_row_bytes, ncols, col, true);
 }
 
 // ---- grouped GEMM -------------------------------------------------------------------------------------------------
@@ -668,42 +692,11 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
             const float *src = act + i * kAct + 32 * blk + 8 * q;
             const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
             const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            // Q8_1 (d = amax / 127, q = roundf(v / d)); max and the integer sum are exact in any order
-            float amax = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
-            amax = lanes_max<4>(amax);
-            const float d = amax / 127.0f;
-            const float dh = half_to_float(float_to_half(d));
-            // v / d as v * (1 / d): one division per block (act itself is an fp32 GEMM result, not bit-comparable
-            // with the reference's, so the quotient's last-ulp rounding carries no parity)
-            const float id = amax == 0.0f ? 0.0f : 1.0f / d;
-            int qsum = 0;
-            _Float16 hi[8], lo[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int qk = (int) (int8_t) roundf(v[k] * id);
-                qsum += qk;
-                const float x = (float) qk * dh;  // exact
-                const _Float16 h = (_Float16) x;
-                hi[perm8(k)] = h;
-                lo[perm8(k)] = (_Float16) (x - (float) h);
-            }
-            qsum = lanes_sum_i<4>(qsum);
+            // v / d as v * (1 / d): act itself is an fp32 GEMM result, not bit-comparable with the reference's, so
+            // the quotient's last-ulp rounding carries no parity
+            const int col = blockIdx.y * 64 + 32 * blk + 8 * q;
+            q8_split8<false>(v, a.out_pack + (size_t) sh_dst[i] * a.out_img, a.nrows, col, live);
             if (live) {
-                const int col = blockIdx.y * 64 + 32 * blk + 8 * q;
-                uint8_t *row = a.out_pack + (size_t) sh_dst[i] * a.out_img;
-                uint8_t *o = row + (size_t) (col >> 8) * kSbMain + ((col >> 7) & 1) * 512 + ((col & 127) >> 3) * 16;
-                *(uint4 *) o = __builtin_bit_cast(uint4, hi);
-                *(uint4 *) (o + 256) = __builtin_bit_cast(uint4, lo);
-                if (q == 0) {
-                    const float sv = dh * (float) qsum;  // exact in fp32
-                    const _Float16 shi = (_Float16) sv, slo = (_Float16) (sv - (float) shi);
-                    _Float16 *m = (_Float16 *) (row + (size_t) (a.nrows >> 8) * kSbMain + (size_t) (col >> 8) * kSbMin);
-                    const int si = perm8((col >> 5) & 7);
-                    m[si] = shi;
-                    m[8 + si] = slo;
-                }
                 if (a.act_out) {
                     float *ao = a.act_out + (size_t) sh_dst[i] * a.nrows + col;
                     *(float4 *) ao = x0;
@@ -767,7 +760,7 @@ int mmq_quant_image(const float *x, int64_t ncols, int64_t rows, void *xpack, hi
     if (!x || !xpack || ncols <= 0 || ncols % 256 || ncols > 65536 || rows < 0 || rows > 65535)
         return host::set_error(host::ERR_SHAPE, "mmq quantize: bad arguments");
     if (rows == 0) return host::OK;
-    hipLaunchKernelGGL(k_quant_image, dim3((unsigned) (ncols / 256), (unsigned) rows), dim3(256), 0, st, x, (int) ncols,
+    hipLaunchKernelGGL(k_quant_image, dim3((unsigned) ((ncols + 2047) / 2048), (unsigned) rows), dim3(256), 0, st, x, (int) ncols,
                        (uint8_t *) xpack, (int64_t) mmq_image_bytes(ncols));
     return host::check_launch("mmq quantize");
 }

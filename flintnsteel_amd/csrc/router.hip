@@ -88,19 +88,21 @@ __device__ __forceinline__ float round_bf16(float v) {
     return __builtin_bit_cast(float, b);
 }
 template <bool BF16>
-__global__ __launch_bounds__(256) void k_gemm_router(const void *__restrict__ w, const float *__restrict__ bias,
+__global__ __launch_bounds__(512) void k_gemm_router(const void *__restrict__ w, const float *__restrict__ bias,
                                                      const float *__restrict__ x, float *__restrict__ y, int ncols,
                                                      int nrows, int n_tok) {
-    // 16 tokens x 16 experts per workgroup; the 4 waves split the columns (wave w: chunks of 64 columns w, w + 4, ...)
-    // and their partial tiles are added in wave order through LDS.
-    __shared__ v4f part[4][64];
+    // 16 tokens x 16 experts per workgroup; the 8 waves split the columns (wave w: chunks of 64 columns w, w + 8, ...,
+    // the next chunk's loads in flight while one is multiplied) and their partial tiles are added in wave order
+    // through LDS.
+    constexpr int NW = 8;
+    __shared__ v4f part[NW][64];
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, il = lane % 16, kk = lane / 16;
     const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
     const int ta = min(t0 + il, n_tok - 1), ea = min(e0 + il, nrows - 1);  // clamped rows (results discarded)
     const float *xr = x + (size_t) ta * ncols;
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k0 = wave * 64; k0 < ncols; k0 += 4 * 64) {
-        float4 a[4], b[4];
+    float4 a[4], b[4];
+    auto load = [&](int k0) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int k = k0 + 16 * u + 4 * kk;
@@ -108,23 +110,31 @@ __global__ __launch_bounds__(256) void k_gemm_router(const void *__restrict__ w,
             if constexpr (BF16) b[u] = ld4_bf16_guard((const uint16_t *) w + (size_t) ea * ncols, k, ncols);
             else b[u] = ld4_guard((const float *) w + (size_t) ea * ncols, k, ncols);
         }
+    };
+    int k0 = wave * 64;
+    if (k0 < ncols) load(k0);
+    for (; k0 < ncols; k0 += NW * 64) {
+        float av[4][4], bv[4][4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            float av[4] = {a[u].x, a[u].y, a[u].z, a[u].w}, bv[4] = {b[u].x, b[u].y, b[u].z, b[u].w};
+            av[u][0] = a[u].x, av[u][1] = a[u].y, av[u][2] = a[u].z, av[u][3] = a[u].w;
+            bv[u][0] = b[u].x, bv[u][1] = b[u].y, bv[u][2] = b[u].z, bv[u][3] = b[u].w;
+        }
+        if (k0 + NW * 64 < ncols) load(k0 + NW * 64);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const float xa = BF16 ? round_bf16(av[m]) : av[m];
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, bv[m], acc, 0, 0, 0);
+                const float xa = BF16 ? round_bf16(av[u][m]) : av[u][m];
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, bv[u][m], acc, 0, 0, 0);
             }
-        }
     }
     part[wave][lane] = acc;
     __syncthreads();
     if (wave == 0) {
         v4f s = part[0][lane];
-        s += part[1][lane];
-        s += part[2][lane];
-        s += part[3][lane];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) s += part[w2][lane];
         const int e = e0 + il;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -198,8 +208,8 @@ int gemm_router_bias(int dtype, const void *w, const float *bias, const float *x
         return host::set_error(host::ERR_SHAPE, "gemm_router: bad arguments");
     if (n_tok == 0) return host::OK;
     const dim3 g((unsigned) ((n_tok + 15) / 16), (unsigned) ((nrows + 15) / 16));
-    if (dtype == T_BF16) hipLaunchKernelGGL(k_gemm_router<true>, g, dim3(256), 0, st, w, bias, x, y, ncols, nrows, n_tok);
-    else if (dtype == 0) hipLaunchKernelGGL(k_gemm_router<false>, g, dim3(256), 0, st, w, bias, x, y, ncols, nrows, n_tok);
+    if (dtype == T_BF16) hipLaunchKernelGGL(k_gemm_router<true>, g, dim3(512), 0, st, w, bias, x, y, ncols, nrows, n_tok);
+    else if (dtype == 0) hipLaunchKernelGGL(k_gemm_router<false>, g, dim3(512), 0, st, w, bias, x, y, ncols, nrows, n_tok);
     else return host::set_error(host::ERR_TYPE, "gemm_router: dtype %d not supported", dtype);
     return host::check_launch("gemm_router");
 }
