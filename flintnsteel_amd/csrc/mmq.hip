@@ -549,15 +549,16 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
                 c0 = decode<T>(f0, 4 * h + s4 + 1, kg, on0);
                 c1 = decode<T>(f1, 4 * h + s4 + 1, kg, on1);
             }
+            // hi for every (tile, stream), then lo: dependent MFMAs 2 NT issues apart
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+            for (int g = 0; g < NB; ++g)
 #pragma unroll
-                for (int g = 0; g < NB; ++g) {
-                    acc[t][0] = mfma32(av[0][t], b0.b[g], acc[t][0]);
-                    acc[t][1] = mfma32(av[0][t], b1.b[g], acc[t][1]);
-                    acc[t][0] = mfma32(av[1][t], b0.b[g], acc[t][0]);
-                    acc[t][1] = mfma32(av[1][t], b1.b[g], acc[t][1]);
-                }
+                for (int x = 0; x < 2; ++x)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        acc[t][0] = mfma32(av[x][t], b0.b[g], acc[t][0]);
+                        acc[t][1] = mfma32(av[x][t], b1.b[g], acc[t][1]);
+                    }
             if (s4 < 3) {
                 // order: the 2 NT LDS reads first, then MFMA / 3 VALU pairs
 #pragma unroll
