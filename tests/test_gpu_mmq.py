@@ -120,6 +120,27 @@ def test_mmq_experts_reference_scratch_sizes(ops):
     assert_close(got.reshape(T * K, nrows), ref, "mmq_experts with reference scratch sizes")
 
 
+@pytest.mark.parametrize("qtype", TYPES)
+def test_mmq_experts_group_shapes(ops, qtype):
+    """Expert loads chosen to hit every group shape of the two launches: empty experts, remainders of 1, 16, 17, 32
+    rows (2-tile list) and 33, 63 rows (4-tile list), whole 64-row groups, 64 + remainder, 128 + 1."""
+    loads = [0, 1, 16, 17, 32, 33, 63, 64, 65, 96, 129, 0]
+    NE, ncols, nrows = len(loads), 512, 128
+    pairs = np.concatenate([np.full(n, e, np.int32) for e, n in enumerate(loads)])
+    rng = np.random.default_rng(11)
+    pairs = pairs[rng.permutation(len(pairs))]
+    K = 1
+    T = len(pairs)
+    ids = pairs.reshape(T, K)
+    mats = make_expert_mats(qtype, NE, nrows, ncols, 700 + qtype)
+    x = gaussian(rng, (T, ncols))
+    md = dev(mats)  # the table points into it: keep it alive
+    got = host(ops.mmq_experts(qtype, table_of(md), 0, ncols, nrows, NE, dev(x), 1, dev(ids)))
+    xq = orc.quantize_q8_1(x)
+    ref = orc.mmvq_experts(qtype, [m.reshape(nrows, -1) for m in mats], ncols, nrows, xq, T, K, ids.ravel())
+    assert_close(got.reshape(T * K, nrows), ref, f"mmq_experts group shapes {orc.TYPE_NAMES[qtype]}")
+
+
 def test_mmq_dense(ops):
     T, ncols, nrows = 130, 768, 192
     rng = np.random.default_rng(3)
