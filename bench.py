@@ -20,7 +20,7 @@ The JSON line also carries:
   cpu_baseline - the oracle's OpenMP CPU restatement of the same layer (int8 x K-quant dot products, not ggml), timed
                  on this host's cores on a bounded sample.
   extra        - configs 1 (Q3_K/Q5_K mix), 2 (4-token speculative verify), 3 (48-layer Q4_K/Q6_K stack) and 4
-                 (512-token prefill through the int8-MFMA grouped GEMM, Dirichlet(0.3)-skewed router bias; MFMA
+                 (512-token prefill through the f16-MFMA split-operand grouped GEMM, Dirichlet(0.3)-skewed router bias; MFMA
                  utilisation = 38.65 G int8 ops per layer / time / 5.0 POP/s dense int8 peak).
 """
 from __future__ import annotations

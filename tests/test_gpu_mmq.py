@@ -1,4 +1,4 @@
-"""Parity of the prefill / batched expert path (MMQ: compaction, int8-MFMA grouped GEMM, prefill layer) with the CPU
+"""Parity of the prefill / batched expert path (MMQ: compaction, f16-MFMA split-operand grouped GEMM, prefill layer) with the CPU
 oracle, called through the C ABI of libfns_hip.so.
 
 Reference tests this follows: tests/mmq_parity.cu (T = 77 tokens, not a tile multiple, synthetic distinct-per-token
