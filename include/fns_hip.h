@@ -136,8 +136,9 @@ int fns_hip_moe_layer_stage(const FnsMoeLayer *layer, int stage, const float *x,
                             int n_tok, void *workspace, size_t workspace_bytes, void *stream);
 
 /* --- prefill / batched expert GEMM (MMQ) ---
- * Q8_1 activation rows for the MMQ path are kept as "images" (int8 values, then per-32 scale and scaled sums in
- * f32): fns_hip_mmq_q8_1_bytes(ncols, nrows) bytes hold nrows of them. */
+ * Q8_1 activation rows for the MMQ path are kept as "split images" (q8 * d8 as two f16 halves per value, then the
+ * per-32 scaled sums as f16 halves: 4.125 bytes per value): fns_hip_mmq_q8_1_bytes(ncols, nrows) bytes hold nrows
+ * of them plus 4096 bytes of slack (mmq_experts keeps its group lists there). */
 /* include/fns/ggml_kernels.h:53-54 mmq_q8_1_bytes */
 size_t fns_hip_mmq_q8_1_bytes(int64_t ncols, int64_t nrows);
 /* bytes of the expert_bounds buffer of fns_hip_mmq_compact for n_expert experts (bounds + tile-group prefix) */

@@ -61,3 +61,22 @@ def test_empty_inputs_are_noops():
     assert L.fns_hip_mmvq_experts(12, _buf(), 0, 2048, 16, _buf(), 1, _buf(), 0, _buf(), None) == 0
     assert L.fns_hip_quantize_q8_1(_buf(), _buf(), 2048, 0, None) == 0
     assert L.fns_hip_route_topk(_buf(), _buf(), _buf(), 128, 8, 0, 0, 1, None) == 0
+
+
+def test_mmq_sizes():
+    L = _lib.lib()
+    # split image: 1056 bytes per 256 columns (q8 * d8 as hi + lo halves, then the 8 sub-block sums as hi + lo)
+    assert L.fns_hip_mmq_q8_1_bytes(2048, 1) == 8 * 1056 + 4096
+    assert L.fns_hip_mmq_q8_1_bytes(768, 10) == 10 * 3 * 1056 + 4096
+    # standalone compaction: bounds [n_expert + 1] and the two group-prefix lists
+    assert L.fns_hip_mmq_bounds_bytes(128) == 3 * 129 * 4
+
+
+def test_mmq_preconditions():
+    L = _lib.lib()
+    assert L.fns_hip_mmq(8, _buf(), 2048, 64, _buf(), 4, _buf(), _buf(), None) == -1     # Q8_0: not a K-quant
+    assert L.fns_hip_mmq(12, _buf(), 1000, 64, _buf(), 4, _buf(), _buf(), None) == -2    # ncols % 256
+    assert L.fns_hip_mmq(12, _buf(), 2048, 100, _buf(), 4, _buf(), _buf(), None) == -2   # nrows % 64
+    assert L.fns_hip_mmq(12, _buf(), 2048, 64, _buf(), 0, _buf(), _buf(), None) == 0     # no tokens: no-op
+    assert L.fns_hip_mmq_compact(_buf(), 4, 8, 300, 1, _buf(), _buf(), _buf(), None) == -2  # > 256 experts
+    assert L.fns_hip_mmq_compact(_buf(), 4, 8, 128, 3, _buf(), _buf(), _buf(), None) == -2  # rows per token 1 or k
