@@ -213,4 +213,41 @@ template <> __device__ __forceinline__ float quarter_dot<T_Q3_K, Any2>(const uin
     return q3k_quarter(blk, x, bb, qt);
 }
 
+// The same dot for NC activation columns (n < ncol live; NC == 1 ignores ncol): acc[n] += quarter_dot(blk, x[n]).
+// Q4_K reads and unpacks the weight quarter once for all columns; each column's arithmetic is exactly that of
+// quarter_dot (a verify column equals the batch-1 result bit for bit). Other types call quarter_dot per column.
+template <int T, class L, int NC>
+__device__ __forceinline__ void quarter_dot_nc(const uint8_t *blk, const ActImg (&x)[NC], int ncol, int bb, int qt,
+                                               float (&acc)[NC]) {
+    if constexpr (T == T_Q4_K) {
+        const uint4 h = L::ld(blk);
+        const uint4 q0 = L::ld(blk + 16 + 32 * qt), q1 = L::ld(blk + 32 + 32 * qt);
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        int lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            lo[i] = (int) (q[i] & kLo4);
+            hi[i] = (int) ((q[i] >> 4) & kLo4);
+        }
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            if (NC == 1 || n < ncol) {
+                int a[16];
+                act_quarter(x[n], bb, qt, a);
+                int dl = 0, dh = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    dl = dot4(lo[i], a[i], dl);
+                    dh = dot4(hi[i], a[8 + i], dh);
+                }
+                acc[n] += k4_finish(h, x[n], bb, qt, dl, dh);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < NC; ++n)
+            if (NC == 1 || n < ncol) acc[n] += quarter_dot<T, L>(blk, x[n], bb, qt);
+    }
+}
+
 }  // namespace fns::dev

@@ -653,17 +653,12 @@ __global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
     for (int qi = lane; qi < 4 * nblk; qi += 32) {
         const int bb = qi >> 2, qt = qi & 3;
         const int off = rl * row_bytes + bb * BB;
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            if (NC == 1 || n < ncol) {
-                if (staged) {
-                    acc[n] += quarter_dot<TQ, Aligned16>(s_w + off, img[n], bb, qt);
-                    accg[n] += quarter_dot<TQ, Aligned16>(s_w + region + off, img[n], bb, qt);
-                } else {
-                    acc[n] += quarter_dot<TQ, Any2>(wa + off, img[n], bb, qt);
-                    accg[n] += quarter_dot<TQ, Any2>(wb + off, img[n], bb, qt);
-                }
-            }
+        if (staged) {
+            quarter_dot_nc<TQ, Aligned16, NC>(s_w + off, img, ncol, bb, qt, acc);
+            quarter_dot_nc<TQ, Aligned16, NC>(s_w + region + off, img, ncol, bb, qt, accg);
+        } else {
+            quarter_dot_nc<TQ, Any2, NC>(wa + off, img, ncol, bb, qt, acc);
+            quarter_dot_nc<TQ, Any2, NC>(wb + off, img, ncol, bb, qt, accg);
         }
     }
     gate_up_epilogue<32, NC>(a, rs, s_act, kGuRows, rl, row, lane, acc, accg);
