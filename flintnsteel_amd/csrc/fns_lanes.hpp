@@ -71,6 +71,21 @@ template <int W> __device__ __forceinline__ float lanes_max(float v) {
     return v;
 }
 
+// Max of a 64-bit unsigned value over the whole wave (every lane receives it).
+template <int O> __device__ __forceinline__ uint64_t max_xor_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t) xor_lane_i<O>((int) (uint32_t) v), hi = (uint32_t) xor_lane_i<O>((int) (uint32_t) (v >> 32));
+    const uint64_t o = ((uint64_t) hi << 32) | lo;
+    return o > v ? o : v;
+}
+__device__ __forceinline__ uint64_t lanes_max_u64(uint64_t v) {
+    v = max_xor_u64<32>(v);
+    v = max_xor_u64<16>(v);
+    v = max_xor_u64<8>(v);
+    v = max_xor_u64<4>(v);
+    v = max_xor_u64<2>(v);
+    return max_xor_u64<1>(v);
+}
+
 // Q8_1 of one value per lane, 32-lane blocks (lanes 0-31, 32-63): the reference's op order (d = amax / 127,
 // q = roundf(x / d), ds = (d, sum) with xor butterflies 16 .. 1). Returns q; d, sum and the 16-lane integer sum of q
 // (for the K-quant min term) and the block's max |v| are valid in every lane of the block.

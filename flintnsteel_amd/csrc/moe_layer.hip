@@ -273,13 +273,11 @@ __device__ __forceinline__ int route_channel(const LayerArgs &a, RouteLds &rs) {
 
 // Routing of n_tok > 1 tokens, run once by the last router workgroup to finish (kK1Threads = 1024 threads): wave t
 // computes token t's probabilities with route_topk_block's fp32 operations (same bits as the batch-1 routing) as
-// 64-bit keys (bits(p) << 32) | ~e; every (token, expert) pair is then ranked by tpp threads counting the keys above
-// its own (the rank r < k is the slot); the weights follow route_weight (slot-order sum). The distinct experts are
-// listed in ascending order with their (token, slot) columns - the channel table the gate/up workgroups read (ggml
-// mm_ids_helper-style compaction: each distinct expert's weights are read once per call) - and ids, weights and down
-// pointers are published.
+// 64-bit keys (bits(p) << 32) | ~e and takes its top k by k rounds of wave argmax (the same order as the batch-1
+// rank); the weights follow route_weight (slot-order sum). The distinct experts are listed in ascending order with
+// their (token, slot) columns - the channel table the gate/up workgroups read (ggml mm_ids_helper-style compaction:
+// each distinct expert's weights are read once per call) - and ids, weights and down pointers are published.
 __device__ void route_all(const LayerArgs &a) {
-    __shared__ uint64_t s_key[kMaxTok][256];
     __shared__ int s_sel[kMaxTok][16];
     __shared__ float s_pv[kMaxTok][16];
     __shared__ int8_t s_col[256][kMaxTok];  // slot + 1 of expert e in token t's selection, 0 if not selected
@@ -312,45 +310,27 @@ __device__ void route_all(const LayerArgs &a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) p[j] = lane + 64 * j < NE ? 1.0f / (1.0f + fns_expf(-v[j])) : 0.0f;
         }
+        // top-k of the token by k rounds of wave argmax over its 64-bit keys (bits(p) << 32 | ~e: unique; larger =
+        // higher probability, then lower index - the order of the reference's ties-to-lower-index top-k)
+        uint64_t key[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int e = lane + 64 * j;
-            s_key[wave][e] = e < NE ? ((uint64_t) __builtin_bit_cast(uint32_t, p[j]) << 32) | (uint32_t) ~e : 0ull;
+            key[j] = e < NE ? ((uint64_t) __builtin_bit_cast(uint32_t, p[j]) << 32) | (uint32_t) ~e : 0ull;
         }
-    }
-    __syncthreads();
-    FNS_MARK(0, blockIdx.x, 5);
-    // ranks: tpp threads per (token, expert) pair, pair = tid / tpp, keys part + tpp i
-    const int npairs = T * NE;
-    int tpp = 1;
-    while (tpp < 8 && 2 * tpp * npairs <= kK1Threads) tpp *= 2;
-    for (int q0 = 0; q0 < npairs * tpp; q0 += kK1Threads) {  // wave-uniform trip count
-        const int q = q0 + tid, pair = q / tpp, part = q % tpp;
-        const bool live = pair < npairs;
-        const int t = live ? pair / NE : 0, e = live ? pair % NE : 0;
-        const uint64_t own = s_key[t][e];
-        // part takes keys [part * span, part * span + span) of the token's 256 (span: NE / tpp rounded up to 32; zero
-        // keys past NE never count); each batch of 16 reads is issued before its first compare
-        const int span = ((NE + tpp - 1) / tpp + 31) / 32 * 32;
-        const ulonglong2 *kp = (const ulonglong2 *) &s_key[t][part * span];
-        int rank = 0;
-        for (int c0 = 0; c0 < span / 2; c0 += 16) {
-            ulonglong2 kk[16];
+        for (int r = 0; r < K; ++r) {
+            uint64_t m = key[0];
 #pragma unroll
-            for (int c = 0; c < 16; ++c) kk[c] = kp[c0 + c];
+            for (int j = 1; j < 4; ++j) m = key[j] > m ? key[j] : m;
+            m = lanes_max_u64(m);
+            const int e = (int) ~(uint32_t) m;
 #pragma unroll
-            for (int c = 0; c < 16; ++c) rank += (kk[c].x > own ? 1 : 0) + (kk[c].y > own ? 1 : 0);
-        }
-        if (!live) rank = 0;
-        switch (tpp) {
-            case 8: rank = lanes_sum_i<8>(rank); break;
-            case 4: rank = lanes_sum_i<4>(rank); break;
-            case 2: rank = lanes_sum_i<2>(rank); break;
-            default: break;
-        }
-        if (live && part == 0 && rank < K) {
-            s_sel[t][rank] = e;
-            s_pv[t][rank] = __builtin_bit_cast(float, (uint32_t) (own >> 32));
+            for (int j = 0; j < 4; ++j)
+                if (lane + 64 * j == e) key[j] = 0ull;  // the owner drops the winner
+            if (lane == 0) {
+                s_sel[wave][r] = e;
+                s_pv[wave][r] = __builtin_bit_cast(float, (uint32_t) (m >> 32));
+            }
         }
     }
     __syncthreads();
