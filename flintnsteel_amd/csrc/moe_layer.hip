@@ -1032,17 +1032,23 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     uintptr_t mis = producer ? ((uintptr_t) wa | (uintptr_t) wb) : 0;
     for (int j = 0; j < K; ++j) mis |= (uintptr_t) (s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd);
     const bool staged = (mis & 15u) == 0;
-    if (staged) {
-        if (producer) {
-            dma_wave(s_gu, wa, 2 * wave * rbg, (2 * wave + 2) * rbg);
-            dma_wave(s_gu + gu_region, wb, 2 * wave * rbg, (2 * wave + 2) * rbg);
-        }
-        // down: wave w takes pieces [w * dn_piece, (w + 1) * dn_piece) of the flattened [K][dn_region] image
+    // down: wave w takes pieces [w * dn_piece, (w + 1) * dn_piece) of the flattened [K][dn_region] image
+    auto dma_down = [&]() {
         const int dn_total = K * dn_region, dn_piece = ((dn_total + kQWaves * 16 - 1) / (kQWaves * 16)) * 16;
         const int p_lo = wave * dn_piece, p_hi = min(dn_total, p_lo + dn_piece);
         for (int j = p_lo / dn_region; j < K && j * dn_region < p_hi; ++j) {
             const int lo = max(p_lo - j * dn_region, 0), hi = min(p_hi - j * dn_region, dn_region);
             dma_wave(s_dn + j * dn_region, s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd, lo, hi);
+        }
+    };
+    // Producers fetch their gate/up rows first and their down rows only once those are consumed: the gate/up bytes,
+    // which the critical path waits for, then get the HBM to themselves, and the down bytes land during the exchange.
+    if (staged) {
+        if (producer) {
+            dma_wave(s_gu, wa, 2 * wave * rbg, (2 * wave + 2) * rbg);
+            dma_wave(s_gu + gu_region, wb, 2 * wave * rbg, (2 * wave + 2) * rbg);
+        } else {
+            dma_down();
         }
     }
     dma_wait();
@@ -1069,16 +1075,17 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         const float gs = lanes_sum<32>(accg);
         v += 0.0f;  // fused-GLU epilogue with zero biases (reference src/ggml/ggml_mmvq.cu:240-247)
         v *= silu(gs + 0.0f);
-        if (lane == 0) {
-            s_act[rl] = v;
-            store_dev(a.act + (size_t) c * F + row, v);
-        }
+        if (lane == 0) s_act[rl] = v;
         __syncthreads();
         FNS_MARK(1, blockIdx.x, 6);
+        // Wave 0 alone stores the act values, so its own wait covers them and the other waves need not wait for
+        // their down rows before the arrival is counted.
+        if (wave != 0 && staged) dma_down();
         if (wave == 0) {  // the 32 rows form one Q8_1 block (lanes 0-31; lanes 32-63 quantise zeros, store nothing)
             const int i = u * kGuRows + lane64 % 32;
             const Q8Lane r = q8_1_lane(lane64 < 32 ? s_act[lane64] : 0.0f);
             if (lane64 < 32) {
+                store_dev(a.act + (size_t) c * F + i, s_act[lane64]);
                 uint8_t *img_g = a.apack + (size_t) c * fbytes;
                 const float dh = half_to_float(float_to_half(r.d));
                 float *dg = (float *) (img_g + img_q_bytes(fpad));
@@ -1097,9 +1104,8 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
             }
         }
         FNS_MARK(1, blockIdx.x, 7);
-        dma_wait();  // this wave's device-coherent stores have completed
     }
-    __syncthreads();
+    if (producer && wave == 0) dma_wait();  // the act stores have completed
     FNS_MARK(1, blockIdx.x, 3);
     // 4. arrival (producers) and wait (everyone; bounded: a timeout poisons this workgroup's outputs with NaN)
     const int nprod = K * upc;
@@ -1117,6 +1123,10 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
                     __hip_atomic_store(sy + (kSyncGroups + 1 + f) * kSyncStride, 1, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
         }
+    }
+    if (producer && wave == 0 && staged) dma_down();
+    if (tid == 0) {
+        const int *sy = a.sync;
         const int *flag = sy + (kSyncGroups + 1 + blockIdx.x % kSyncGroups) * kSyncStride;
         int spins = 0;
         while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
