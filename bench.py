@@ -210,14 +210,16 @@ def run_prefill(torch, synth, n_layers: int = 4, T: int = 512, replays: int = 10
     max_load = float(np.mean([np.bincount(i.ravel(), minlength=NE).max() for i in ids]))
     loads = [np.bincount(i.ravel(), minlength=NE) for i in ids]
     groups = float(np.mean([np.sum((n + 63) // 64) for n in loads]))       # workgroup row groups of 64
-    tiles = float(np.mean([np.sum((n + 15) // 16) for n in loads]))        # 16-row tiles holding routed rows
+    tiles = float(np.mean([np.sum((n + 31) // 32) for n in loads]))        # 32-row MFMA tiles computed
     ops_per_layer = 2 * T * K_TOP * (2 * F * H + H * F)
     del g
     return {"us_per_layer": round(us, 2), "tokens_per_s": round(T / us * 1e6, 0), "experts_touched": touched,
-            "max_expert_load": max_load, "row_groups": groups, "tile_fill": round(tiles / (4 * groups), 3),
+            "max_expert_load": max_load, "row_groups": groups, "tile_fill": round(T * K_TOP / (32 * tiles), 3),
             "weight_gbs": round(touched * expert_bytes(Q4_K, Q4_K) / (us * 1e-6) / 1e9, 1),
             "int8_tops": round(ops_per_layer / (us * 1e-6) / 1e12, 2),
-            "mfma_util": round(ops_per_layer / (us * 1e-6) / 5.0e15, 4)}
+            "mfma_util": round(ops_per_layer / (us * 1e-6) / 5.0e15, 4),
+            # the split-operand GEMM issues every product twice (hi and lo halves) on the 2.5 PFLOP/s f16 pipe
+            "f16_pipe_util": round(2 * ops_per_layer / (us * 1e-6) / 2.5e15, 4)}
 
 
 def main() -> int:

@@ -9,15 +9,16 @@
 //     int8 MFMA per sub-block needs a convert + scale + add per output element per sub-block: VALU-bound. Here the
 //     scales are folded into the operands instead, exactly: A = q8 * d8 as two f16 halves (hi + lo, see the image
 //     layout below), B = integer code * integer sub-block scale as f16 (|B| <= 2048: exact; Q6_K's 8-bit scales are
-//     split in two operands). v_mfma_f32_16x16x32_f16 then accumulates a whole 256-column superblock, and only the
-//     superblock's float scales d (and dmin times a 16x16x16 f16 MFMA of the min term) touch the accumulators.
+//     split in two operands). v_mfma_f32_32x32x16_f16 then accumulates a whole 256-column superblock, and only the
+//     superblock's float scales d (and dmin times one more MFMA of the min term) touch the accumulators.
 //     Every product is exact; the sums are fp32.
-//   * A = 16 activation rows (tokens) x 32 columns, B = 32 columns x 16 weight rows: the lane that owns output
-//     (token i, weight row j) holds weight row j = lane % 16 for 4 tokens and decodes row j's codes and scales itself.
-//   * A workgroup (4 waves) owns two 16-row weight streams per wave - gate and up of the same 64 rows (GLU), or 128
-//     rows - and up to 64 of the expert's routed activation rows (4 tiles of 16): each weight byte is read from HBM
-//     once per 64 routed rows. Activations are staged per half superblock in LDS through registers, double-buffered
-//     (72 KB: two workgroups per CU); weights go straight to VGPRs, one superblock ahead.
+//   * A = 32 activation rows (tokens) x 16 columns, B = 16 columns x 32 weight rows: the lane that owns output
+//     (token i, weight row j) holds weight row j = lane % 32 for 16 tokens and decodes row j's codes and scales
+//     itself. The 32x32 shape moves half the operand bytes (LDS reads, decode VALU) per product of the 16x16 one.
+//   * A workgroup (4 waves) owns two 32-row weight streams per wave - gate and up of the same 128 rows (GLU), or 256
+//     rows - and up to 64 of the expert's routed activation rows (2 tiles of 32): each weight byte is read from HBM
+//     once per 64 routed rows. Activations are staged per half superblock in LDS by LDS-DMA, double-buffered (66 KB:
+//     two workgroups per CU); weights go straight to VGPRs, half a superblock ahead.
 //   * Gate/up: both matrices in one pass, then act = up * silu(gate) and its Q8_1 blocks (32 consecutive rows = 32
 //     consecutive act columns) written straight into the split image rows the down pass reads.
 //
@@ -217,8 +218,8 @@ struct MmqArgs {
     const uint8_t *xpack;      // split activation image rows
     int64_t x_img;             // bytes per activation image row
     const int32_t *bounds;     // [n_expert + 1] (null: dense)
-    const int32_t *gprefix;    // [n_expert + 1] group prefix of this launch's list
-    int tail;                  // 1: the groups are the <= 32-row remainders (2-tile kernel)
+    const int32_t *gprefix;    // [2][n_expert + 1] group prefixes: 64-row groups, then the <= 32-row remainders
+    int n_main;                // launch: workgroup rows (blockIdx.y) of the 64-row list
     const int32_t *src;        // sorted position -> activation image row (null: identity)
     const int32_t *dst_rows;   // sorted position -> output row (null: identity)
     int n_rows;                // dense: number of activation rows
@@ -228,12 +229,13 @@ struct MmqArgs {
     float *act_out;            // GLU: optional f32 act [out row][nrows]
 };
 
-// Weight fragments of one 256-value block for one lane (row j, column group kg = lane / 16 of every sub-block).
+// Weight fragments of one 256-value block for one lane: the header (scales, d) and the codes of column groups
+// kg = 2 h and 2 h + 1 (h = lane / 32) of every sub-block - 16 contiguous bytes per code array, one load each.
 template <int T> struct WFrag;
-template <> struct WFrag<T_Q4_K> { uint4 h; uint2 q[4]; };
-template <> struct WFrag<T_Q5_K> { uint4 h; uint2 q[4]; uint2 qh; };
-template <> struct WFrag<T_Q6_K> { uint2 ql[4]; uint2 qh[2]; uint4 sc; uint32_t d; };
-template <> struct WFrag<T_Q3_K> { uint2 qs[2]; uint2 hm; uint4 tail; };
+template <> struct WFrag<T_Q4_K> { uint4 h; uint4 q[4]; };
+template <> struct WFrag<T_Q5_K> { uint4 h; uint4 q[4]; uint4 qh; };
+template <> struct WFrag<T_Q6_K> { uint4 ql[4]; uint4 qh[2]; uint4 sc; uint32_t d; };
+template <> struct WFrag<T_Q3_K> { uint4 qs[2]; uint4 hm; uint4 tail; };
 
 // Buffer loads: a uniform base in a resource (SGPRs), a 32-bit per-lane offset and a uniform offset - no 64-bit
 // address arithmetic per load. (Unaligned dword access is enabled on the platform, as for the plain global loads.)
@@ -245,42 +247,44 @@ __device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t vo, uint32_t so) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ uint2 bload8(Rsrc r, uint32_t vo, uint32_t so) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
-    return make_uint2(v[0], v[1]);
-}
 
-// fragment of the block at (vo + so) from r for lane group kg
-template <int T> __device__ __forceinline__ void wfrag_load(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T> &f);
-template <> __device__ __forceinline__ void wfrag_load<T_Q4_K>(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T_Q4_K> &f) {
-    f.h = bload16(r, vo, so);
+// Part P (compile time) of the fragment of the block at (vo + so) from r; vc = vo + 16 h selects the lane's code
+// bytes. Part 0: the header and the codes of sub-blocks 0-3; part 1: the codes of sub-blocks 4-7.
+template <int T, int P>
+__device__ __forceinline__ void wfrag_load(Rsrc r, uint32_t vo, uint32_t vc, uint32_t so, WFrag<T> &f) {
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        constexpr int qoff = T == T_Q4_K ? 16 : 48;
+        if constexpr (P == 0) {
+            f.h = bload16(r, vo, so);
+            if constexpr (T == T_Q5_K) f.qh = bload16(r, vc, so + 16);
+        }
 #pragma unroll
-    for (int g = 0; g < 4; ++g) f.q[g] = bload8(r, vo + 8 * kg, so + 16 + 32 * g);
-}
-template <> __device__ __forceinline__ void wfrag_load<T_Q5_K>(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T_Q5_K> &f) {
-    f.h = bload16(r, vo, so);
-    f.qh = bload8(r, vo + 8 * kg, so + 16);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) f.q[g] = bload8(r, vo + 8 * kg, so + 48 + 32 * g);
-}
-template <> __device__ __forceinline__ void wfrag_load<T_Q6_K>(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T_Q6_K> &f) {
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-        f.ql[2 * n] = bload8(r, vo + 8 * kg, so + 64 * n);
-        f.ql[2 * n + 1] = bload8(r, vo + 8 * kg, so + 64 * n + 32);
-        f.qh[n] = bload8(r, vo + 8 * kg, so + 128 + 32 * n);
+        for (int g = 2 * P; g < 2 * P + 2; ++g) f.q[g] = bload16(r, vc, so + qoff + 32 * g);
+    } else if constexpr (T == T_Q6_K) {
+        f.ql[2 * P] = bload16(r, vc, so + 64 * P);
+        f.ql[2 * P + 1] = bload16(r, vc, so + 64 * P + 32);
+        f.qh[P] = bload16(r, vc, so + 128 + 32 * P);
+        if constexpr (P == 0) {
+            f.sc = bload16(r, vo, so + 192);
+            f.d = __builtin_amdgcn_raw_buffer_load_b16(r, vo, so + 208, 0);
+        }
+    } else {
+        if constexpr (P == 0) {
+            f.hm = bload16(r, vc, so);
+            f.tail = bload16(r, vo, so + 94);  // scales[12] at +2, d at +14
+        }
+        f.qs[P] = bload16(r, vc, so + 32 + 32 * P);
     }
-    f.sc = bload16(r, vo, so + 192);
-    f.d = __builtin_amdgcn_raw_buffer_load_b16(r, vo, so + 208, 0);
 }
-template <> __device__ __forceinline__ void wfrag_load<T_Q3_K>(Rsrc r, uint32_t vo, uint32_t so, int kg, WFrag<T_Q3_K> &f) {
-    f.hm = bload8(r, vo + 8 * kg, so);
-    f.qs[0] = bload8(r, vo + 8 * kg, so + 32);
-    f.qs[1] = bload8(r, vo + 8 * kg, so + 64);
-    f.tail = bload16(r, vo, so + 94);  // scales[12] at +2, d at +14
+// vector loads issued by part P of wfrag_load for one stream
+template <int T, int P> constexpr int wfrag_loads() {
+    return T == T_Q4_K ? (P ? 2 : 3) : T == T_Q5_K ? (P ? 2 : 4) : T == T_Q6_K ? (P ? 3 : 5) : (P ? 1 : 3);
 }
+// the 8 code bytes of column group 2 h + p (p compile time) from a 16-byte code array
+__device__ __forceinline__ uint2 half8(const uint4 &v, int p) { return p ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y); }
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -305,11 +309,12 @@ __device__ __forceinline__ v8h centred8(uint32_t x, uint32_t y, h2 off, h2 sc) {
                 (biased13(y) - off) * sc);
 }
 
-// B operand(s) of sub-block s (compile-time) for lane group kg: B[k][row] = integer code x integer scale as f16
-// (Q6_K: two operands, scale split as 16 (sc >> 4) + (sc & 15), each product exact). The block's float scale d (and
-// dmin) are applied per superblock. on = (d != 0): a block with d = 0 contributes d * (...) = 0 whatever its codes.
+// B operand(s) of sub-block s, column group kg = 2 h + p (s, p compile time) for this lane: B[k][row] = integer code x
+// integer scale as f16 (Q6_K: two operands, scale split as 16 (sc >> 4) + (sc & 15), each product exact). The block's
+// float scale d (and dmin) are applied per superblock. on = (d != 0): a block with d = 0 contributes d * (...) = 0
+// whatever its codes.
 template <int T> struct BOp { v8h b[T == T_Q6_K ? 2 : 1]; };
-template <int T> __device__ __forceinline__ BOp<T> decode(const WFrag<T> &f, int s, int kg, bool on);
+template <int T> __device__ __forceinline__ BOp<T> decode(const WFrag<T> &f, int s, int p, int h, bool on);
 
 // (sc_s, sc_s) as f16 and its bias -1024 sc_s for sub-block s (compile time) of a Q4_K / Q5_K block; on = 0: zeros.
 // The 6-bit scales are unpacked four at a time (ggml get_scale_min_k4), byte s placed twice next to 0x64 (1024.0).
@@ -319,8 +324,8 @@ __device__ __forceinline__ void k4_scale2(const uint4 &h, int s, bool on, h2 &s2
     s2 = as_h2(__builtin_amdgcn_perm(0x64646464u, on ? w : 0u, 0x04000400u | (i << 16) | i)) - splat((_Float16) 1024.0f);
     bias = s2 * splat((_Float16) -1024.0f);
 }
-template <> __device__ __forceinline__ BOp<T_Q4_K> decode<T_Q4_K>(const WFrag<T_Q4_K> &f, int s, int kg, bool on) {
-    const uint2 q = f.q[s >> 1];
+template <> __device__ __forceinline__ BOp<T_Q4_K> decode<T_Q4_K>(const WFrag<T_Q4_K> &f, int s, int p, int, bool on) {
+    const uint2 q = half8(f.q[s >> 1], p);
     const int sh = 4 * (s & 1);
     h2 s2, bias;
     k4_scale2(f.h, s, on, s2, bias);
@@ -328,27 +333,27 @@ template <> __device__ __forceinline__ BOp<T_Q4_K> decode<T_Q4_K>(const WFrag<T_
     r.b[0] = scaled8((q.x >> sh) & kLo4, (q.y >> sh) & kLo4, s2, bias);
     return r;
 }
-template <> __device__ __forceinline__ BOp<T_Q5_K> decode<T_Q5_K>(const WFrag<T_Q5_K> &f, int s, int kg, bool on) {
-    const uint2 q = f.q[s >> 1];
+template <> __device__ __forceinline__ BOp<T_Q5_K> decode<T_Q5_K>(const WFrag<T_Q5_K> &f, int s, int p, int, bool on) {
+    const uint2 q = half8(f.q[s >> 1], p), qh = half8(f.qh, p);
     const int sh = 4 * (s & 1);
     h2 s2, bias;
     k4_scale2(f.h, s, on, s2, bias);
     BOp<T_Q5_K> r;
-    r.b[0] = scaled8(((q.x >> sh) & kLo4) | (((f.qh.x >> s) & 0x01010101u) << 4),
-                     ((q.y >> sh) & kLo4) | (((f.qh.y >> s) & 0x01010101u) << 4), s2, bias);
+    r.b[0] = scaled8(((q.x >> sh) & kLo4) | (((qh.x >> s) & 0x01010101u) << 4),
+                     ((q.y >> sh) & kLo4) | (((qh.y >> s) & 0x01010101u) << 4), s2, bias);
     return r;
 }
 // Q6_K sub-block s: n = s / 4, qq = s % 4: ql[64 n + 32 (qq & 1) + l] nibble qq >> 1, qh[32 n + l] bits 2 qq,
-// value - 32; int8 scale of group 8 n + 2 qq + (l >= 16).
-template <> __device__ __forceinline__ BOp<T_Q6_K> decode<T_Q6_K>(const WFrag<T_Q6_K> &f, int s, int kg, bool on) {
+// value - 32; int8 scale of group 8 n + 2 qq + (l >= 16), i.e. + h for column groups 2 h, 2 h + 1.
+template <> __device__ __forceinline__ BOp<T_Q6_K> decode<T_Q6_K>(const WFrag<T_Q6_K> &f, int s, int p, int h, bool on) {
     const int n = s >> 2, qq = s & 3;
-    const uint2 ql = f.ql[2 * n + (qq & 1)], qh = f.qh[n];
+    const uint2 ql = half8(f.ql[2 * n + (qq & 1)], p), qh = half8(f.qh[n], p);
     const int shl = 4 * (qq >> 1), shh = 2 * qq;
     const uint32_t x = ((ql.x >> shl) & kLo4) | (((qh.x >> shh) & 0x03030303u) << 4);
     const uint32_t y = ((ql.y >> shl) & kLo4) | (((qh.y >> shh) & 0x03030303u) << 4);
     const int g0 = 8 * n + 2 * qq;  // even: both groups in one word
     const uint32_t w0 = word(f.sc, g0 >> 2);
-    const int sc = on ? (int) (int8_t) ((w0 >> (8 * ((g0 & 3) + (kg >> 1)))) & 0xffu) : 0;
+    const int sc = on ? (int) (int8_t) ((w0 >> (8 * ((g0 & 3) + h))) & 0xffu) : 0;
     const h2 off = splat((_Float16) 1056.0f);
     BOp<T_Q6_K> r;
     r.b[0] = centred8(x, y, off, splat((_Float16) (16 * (sc >> 4))));
@@ -357,26 +362,26 @@ template <> __device__ __forceinline__ BOp<T_Q6_K> decode<T_Q6_K>(const WFrag<T_
 }
 // Q3_K sub-block s: n = s / 4, j = s % 4: qs[32 n + l] bits 2 j, hmask[l] bit 4 n + j (clear: -4); scale groups
 // 8 n + 2 j + (l >= 16), 6-bit value - 32 (low nibbles in scales[0..7], high bit pairs in scales[8..11]).
-template <> __device__ __forceinline__ BOp<T_Q3_K> decode<T_Q3_K>(const WFrag<T_Q3_K> &f, int s, int kg, bool on) {
+template <> __device__ __forceinline__ BOp<T_Q3_K> decode<T_Q3_K>(const WFrag<T_Q3_K> &f, int s, int p, int h, bool on) {
     const int n = s >> 2, j = s & 3;
-    const uint2 q = f.qs[n];
+    const uint2 q = half8(f.qs[n], p), hm = half8(f.hm, p);
     const int hs = 4 * n + j;
-    const uint32_t x = ((q.x >> (2 * j)) & 0x03030303u) | (((f.hm.x >> hs) & 0x01010101u) << 2);
-    const uint32_t y = ((q.y >> (2 * j)) & 0x03030303u) | (((f.hm.y >> hs) & 0x01010101u) << 2);
+    const uint32_t x = ((q.x >> (2 * j)) & 0x03030303u) | (((hm.x >> hs) & 0x01010101u) << 2);
+    const uint32_t y = ((q.y >> (2 * j)) & 0x03030303u) | (((hm.y >> hs) & 0x01010101u) << 2);
     // tail = block bytes 94..109: scales[i] is tail byte 2 + i
     const uint32_t hi_w = (f.tail.z >> 16) | (f.tail.w << 16);  // scales[8..11]
     int scv[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int g = 8 * n + 2 * j + h;
+    for (int u = 0; u < 2; ++u) {
+        const int g = 8 * n + 2 * j + u;
         const int lb = (g & 7) + 2;  // tail byte of scales[g & 7]
         const uint32_t lw = lb < 4 ? f.tail.x : lb < 8 ? f.tail.y : f.tail.z;
         const uint32_t b = (lw >> (8 * (lb & 3))) & 0xffu;
         const uint32_t lo4 = g < 8 ? (b & 0xFu) : (b >> 4);
         const uint32_t hi2 = (((hi_w >> (8 * (g & 3))) & 0xffu) >> (2 * (g >> 2))) & 3u;
-        scv[h] = (int) (lo4 | (hi2 << 4)) - 32;
+        scv[u] = (int) (lo4 | (hi2 << 4)) - 32;
     }
-    const int sc = on ? (kg < 2 ? scv[0] : scv[1]) : 0;
+    const int sc = on ? (h == 0 ? scv[0] : scv[1]) : 0;
     BOp<T_Q3_K> r;
     r.b[0] = centred8(x, y, splat((_Float16) 1028.0f), splat((_Float16) sc));
     return r;
@@ -388,32 +393,30 @@ template <int T> __device__ __forceinline__ float blk_d(const WFrag<T> &f) {
     else if constexpr (T == T_Q6_K) return half_to_float(f.d);
     else return half_to_float(f.tail.w >> 16);
 }
-// Q4_K / Q5_K min term operand: B[k][row] = m_s for the sums [S_hi 8 | S_lo 8] of the A operand, lane group kg holding
-// k = 4 kg .. 4 kg + 3, i.e. sub-blocks 4 (kg & 1) + (0 2 1 3).
-template <int T> __device__ __forceinline__ v4h min_b(const WFrag<T> &f, int kg) {
+// Q4_K / Q5_K min term operand: B[k][row] = m_s against the A operand [S_hi 8 | S_lo 8] (lane half h holds k = 8 h ..
+// 8 h + 7), both halves the 8 mins in the stored sum order 0 2 1 3 4 6 5 7.
+template <int T> __device__ __forceinline__ v8h min_b(const WFrag<T> &f) {
     const uint32_t m_lo = f.h.z & 0x3F3F3F3Fu;                                         // m[0..3]
     const uint32_t m_hi = ((f.h.w >> 4) & kLo4) | ((f.h.z >> 2) & 0x30303030u);       // m[4..7]
-    const uint32_t mw = (kg & 1) ? m_hi : m_lo;
     const h2 off = splat((_Float16) 1024.0f);
-    return __builtin_bit_cast(v4h, make_uint2(as_u(biased02(mw) - off), as_u(biased13(mw) - off)));
+    return cat4(biased02(m_lo) - off, biased13(m_lo) - off, biased02(m_hi) - off, biased13(m_hi) - off);
 }
 
 // LDS of one workgroup (static, distinct objects, so the compiler can tell the chunk being filled by LDS-DMA from the
-// one being read and puts no wait between them): the half-superblock activation chunks [kMmqTok][512] (hi, lo)
+// one being read and puts no wait between them): the half-superblock activation chunks [rows][512] (hi, lo)
 // double-buffered, with the 16-byte pieces of row r stored at piece index p ^ (r % 16) so that the 16 rows of an
-// A-fragment read hit distinct banks; the superblock min-term sums [kMmqTok][32]. 68.5 KB: two workgroups per CU.
+// A-fragment read quarter hit distinct banks; the superblock min-term sums [rows][32]. 66 KB for 64 rows: two
+// workgroups per CU.
 constexpr int kRowA = 512, kRowS = 32;
-struct MmqShared {
-    uint8_t *a0, *a1, *s;
-    int *src, *dst;
-};
 
 // 1 / (1 + e^-g); 0 for g -> -inf (the exponential saturates to +inf), 1 for g -> +inf
 __device__ __forceinline__ float silu_rcp(float g) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
 }
 
-__device__ __forceinline__ v4f mfma32(v8h a, v8h b, v4f c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ v16f mfma32(v8h a, v8h b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
 
 // Workgroup barrier for LDS filled by LDS-DMA: the DMA data is complete once this wave's vmcnt wait before it retires
 // (waits placed by the caller: __syncthreads' fence would also wait for the weight loads still in flight). This
@@ -426,45 +429,60 @@ typedef __attribute__((address_space(3))) void *LdsPtr;
 __device__ __forceinline__ void dma16(Rsrc r, void *dst, uint32_t vo, uint32_t so) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr) dst, 16, vo, so, 0, 0);
 }
-// vector loads issued by wfrag_load for one stream (they complete in order with the DMA issued before them)
-template <int T> constexpr int wfrag_loads() { return T == T_Q4_K ? 5 : T == T_Q5_K ? 6 : T == T_Q6_K ? 8 : 4; }
 
-// One workgroup = 4 waves x two 16-row weight streams x up to 16 NT routed activation rows of one expert (NT = 4: the
-// 64-row groups and remainders > 32 rows; NT = 2: remainders <= 32 rows). GLU: stream 0 is the gate row, stream 1 the
-// same up row (64 rows per workgroup); otherwise the streams are rows r and r + 64 (128).
+// One workgroup = 4 waves x two 32-row weight streams x up to 32 NT routed activation rows of one expert (NT = 2: the
+// 64-row groups and remainders > 32 rows; NT = 1: remainders <= 32 rows). GLU: stream 0 is the gate row, stream 1 the
+// same up row (128 rows per workgroup); otherwise the streams are rows r and r + 128 (256).
+// v_mfma_f32_32x32x16_f16: A = 32 activation rows x 16 columns, B = 16 columns x 32 weight rows; the lane that owns
+// weight row j = lane % 32 decodes row j's codes and scales itself (column groups 2 h, 2 h + 1 of each sub-block,
+// h = lane / 32), and holds the outputs of row j for 16 of the 32 tokens.
+// LDS of one workgroup, sized for the 64-row groups (the 32-row groups use the first half of each array).
+struct MmqLds {
+    uint8_t (&a0)[kMmqTok * kRowA];
+    uint8_t (&a1)[kMmqTok * kRowA];
+    uint8_t (&s)[kMmqTok * kRowS];
+    int (&src)[kMmqTok];
+    int (&dst)[kMmqTok];
+};
+
+// Group g of the launch's list (NT = 2: the 64-row groups and remainders > 32 rows; NT = 1: the expert's <= 32-row
+// remainder), weight row block wb.
 template <int T, bool GLU, int NT>
-__global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 4))) void k_mmq(const MmqArgs a) {
-    constexpr int ROWS = 16 * NT;  // activation rows of the workgroup
-    __shared__ __align__(16) uint8_t sh_a0[ROWS * kRowA];
-    __shared__ __align__(16) uint8_t sh_a1[ROWS * kRowA];
-    __shared__ __align__(16) uint8_t sh_s[ROWS * kRowS];
-    __shared__ int sh_src[ROWS], sh_dst[ROWS];
+__device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const MmqLds &L) {
+    constexpr int ROWS = 32 * NT;  // activation rows of the workgroup
+    constexpr int WROWS = GLU ? 128 : 256;  // weight rows of the workgroup
+    auto &sh_a0 = L.a0;
+    auto &sh_a1 = L.a1;
+    auto &sh_s = L.s;
+    auto &sh_src = L.src;
+    auto &sh_dst = L.dst;
     constexpr int BB = Traits<T>::bytes, NB = T == T_Q6_K ? 2 : 1;
     constexpr bool MIN = T == T_Q4_K || T == T_Q5_K;
-    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-    const int kg = lane / 16, jl = lane % 16;
+    // (the wave index as a scalar: the LDS-DMA destinations derived from it are wave-uniform M0 values)
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
+    const int hh = lane / 32, jl = lane % 32;
 
     // which expert / rows of activations
     int e = 0, seg = 0, cnt = 0;
     if (a.bounds) {
-        const int g = blockIdx.x;
-        if (g >= a.gprefix[a.n_expert]) return;
-        int lo = 0, hi = a.n_expert;  // largest e with gprefix[e] <= g
+        const int32_t *gp = NT == 2 ? a.gprefix : a.gprefix + a.n_expert + 1;
+        if (g >= gp[a.n_expert]) return;
+        int lo = 0, hi = a.n_expert;  // largest e with gp[e] <= g
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
-            if (a.gprefix[mid] <= g) lo = mid;
+            if (gp[mid] <= g) lo = mid;
             else hi = mid;
         }
         e = lo;
-        if (a.tail) {  // the expert's last rows: n_e % 64 of them
+        if constexpr (NT == 1) {  // the expert's last rows: n_e % 64 of them
             cnt = (a.bounds[e + 1] - a.bounds[e]) % kMmqTok;
             seg = a.bounds[e + 1] - cnt;
         } else {
-            seg = a.bounds[e] + (g - a.gprefix[e]) * kMmqTok;
+            seg = a.bounds[e] + (g - gp[e]) * kMmqTok;
             cnt = min(kMmqTok, a.bounds[e + 1] - seg);
         }
     } else {
-        seg = blockIdx.x * kMmqTok;
+        seg = g * kMmqTok;
         cnt = min(kMmqTok, a.n_rows - seg);
     }
     if (cnt <= 0) return;
@@ -474,13 +492,21 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
         sh_dst[i] = a.dst_rows ? a.dst_rows[q] : q;
     }
 
+    // (the expert's base as a scalar, so the weight buffer resources stay in SGPRs)
     const uint8_t *wbase = a.table ? (const uint8_t *) gload<const char *>((const uint8_t *) (a.table + e)) : a.w_dense;
+    {
+        const uint64_t wb64 = (uint64_t) wbase;
+        wbase = (const uint8_t *) (((uint64_t) __builtin_amdgcn_readfirstlane((uint32_t) (wb64 >> 32)) << 32) |
+                                   (uint32_t) __builtin_amdgcn_readfirstlane((uint32_t) wb64));
+    }
     const int nb = a.ncols / 256;
     const int64_t row_bytes = (int64_t) nb * BB;
-    const int row0 = GLU ? blockIdx.y * 64 + wave * 16 + jl : blockIdx.y * 128 + wave * 16 + jl;
-    const int row1 = GLU ? row0 : min(row0 + 64, a.nrows - 1);  // past the end (nrows % 128 == 64): computed, not stored
+    // weight rows past nrows (nrows % WROWS != 0) are computed from the last row and not stored
+    const int row0 = wb * WROWS + wave * 32 + jl;
+    const int ra = min(row0, a.nrows - 1), rb = GLU ? ra : min(row0 + 128, a.nrows - 1);
     const Rsrc r0 = rsrc_of(wbase + a.off_a), r1 = rsrc_of(wbase + (GLU ? a.off_b : a.off_a)), rx = rsrc_of(a.xpack);
-    const uint32_t v0 = (uint32_t) (row0 * row_bytes), v1 = (uint32_t) (row1 * row_bytes);
+    const uint32_t v0 = (uint32_t) (ra * row_bytes), v1 = (uint32_t) (rb * row_bytes);
+    const uint32_t c0 = v0 + 16 * hh, c1 = v1 + 16 * hh;
     __syncthreads();  // sh_src / sh_dst
 
     // LDS-DMA of chunk (kb, h) - columns 256 kb + 128 h .. + 127, hi and lo: 512 bytes per row - by instruction u of
@@ -509,95 +535,144 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     WFrag<T> f0, f1, n0, n1;
     dma_chunk(sh_a0, 0, 0);
     dma_sums(0);
-    wfrag_load<T>(r0, v0, 0, kg, f0);
-    wfrag_load<T>(r1, v1, 0, kg, f1);
+    wfrag_load<T, 0>(r0, v0, c0, 0, f0);
+    wfrag_load<T, 0>(r1, v1, c1, 0, f1);
     dma_wait();
     lds_barrier();
 
     // acc[t][m] is kept in units of the current superblock's d (per lane: its row's d, 1 if d = 0), so the MFMAs
     // accumulate into it directly; between superblocks it is rescaled and the min term added (fp32 rounding).
-    // All four tiles are computed whatever cnt (rows past it hold stale LDS data and are never stored).
-    v4f acc[NT][2];
+    // All tiles are computed whatever cnt (rows past it hold stale LDS data and are never stored).
+    v16f acc[NT][2];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][0][r] = acc[t][1][r] = 0.0f;
     float ds0 = blk_d<T>(f0), ds1 = blk_d<T>(f1);
     bool on0 = ds0 != 0.0f, on1 = ds1 != 0.0f;
     ds0 = on0 ? ds0 : 1.0f;
     ds1 = on1 ? ds1 : 1.0f;
 
-    // four sub-blocks of one half from LDS chunk buf: acc[t][m] += A (hi, lo) x B (integer-scaled codes)
-    // Software-pipelined: while the MFMAs of sub-block s issue, the A fragments of s + 1 are read from LDS and its B
-    // operands decoded (VALU), interleaved one MFMA / a few VALU so the two pipes overlap within the wave.
-    auto load_a = [&](const uint8_t *buf, int s4, v8h (&av)[2][NT]) __attribute__((always_inline)) {
+    // eight 16-column steps of one half from LDS chunk buf (step i: sub-block 4 h + i / 2, column group 2 hh + i % 2):
+    // acc[t][m] += A (hi, lo) x B (integer-scaled codes). Software-pipelined: while the MFMAs of step i issue, the A
+    // fragments of step i + 1 are read from LDS and its B operands decoded (VALU), interleaved one MFMA / a few VALU.
+    auto load_a = [&](const uint8_t *buf, int i, v8h (&av)[2][NT]) __attribute__((always_inline)) {
+        const int piece = 4 * (i >> 1) + 2 * hh + (i & 1);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const uint8_t *ap = buf + (t * 16 + jl) * kRowA;
-            av[0][t] = *(const v8h *) (ap + 16 * ((4 * s4 + kg) ^ jl));
-            av[1][t] = *(const v8h *) (ap + 16 * ((16 + 4 * s4 + kg) ^ jl));
+            const uint8_t *ap = buf + (t * 32 + jl) * kRowA;
+            av[0][t] = *(const v8h *) (ap + 16 * (piece ^ (jl & 15)));
+            av[1][t] = *(const v8h *) (ap + 16 * ((16 + piece) ^ (jl & 15)));
         }
+    };
+    auto load_a1 = [&](const uint8_t *buf, int i, int x, v8h (&av)[NT]) __attribute__((always_inline)) {
+        const int piece = 16 * x + 4 * (i >> 1) + 2 * hh + (i & 1);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) av[t] = *(const v8h *) (buf + (t * 32 + jl) * kRowA + 16 * (piece ^ (jl & 15)));
     };
     auto half_pass = [&](const uint8_t *buf, auto hc, const WFrag<T> &f0, const WFrag<T> &f1) __attribute__((always_inline)) {
         constexpr int h = decltype(hc)::value;
-        v8h av[2][NT], an[2][NT];
-        BOp<T> b0 = decode<T>(f0, 4 * h, kg, on0), b1 = decode<T>(f1, 4 * h, kg, on1), c0, c1;
+        v8h av[2][NT];
+        BOp<T> b0 = decode<T>(f0, 4 * h, 0, hh, on0), b1 = decode<T>(f1, 4 * h, 0, hh, on1), d0, d1;
         load_a(buf, 0, av);
+        if constexpr (NB == 1) {
+            // One B operand per stream: the hi fragments of step i + 1 are read into the registers of step i's as soon
+            // as its hi MFMAs have issued, the lo ones after its lo MFMAs (no second set of A registers).
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            __builtin_amdgcn_sched_barrier(0);
-            if (s4 < 3) {
-                load_a(buf, s4 + 1, an);
-                c0 = decode<T>(f0, 4 * h + s4 + 1, kg, on0);
-                c1 = decode<T>(f1, 4 * h + s4 + 1, kg, on1);
-            }
-            // hi for every (tile, stream), then lo: dependent MFMAs 2 NT issues apart
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (i < 7) {
+                    d0 = decode<T>(f0, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on0);
+                    d1 = decode<T>(f1, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on1);
+                }
 #pragma unroll
-            for (int g = 0; g < NB; ++g)
-#pragma unroll
-                for (int x = 0; x < 2; ++x)
+                for (int x = 0; x < 2; ++x) {
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
-                        acc[t][0] = mfma32(av[x][t], b0.b[g], acc[t][0]);
-                        acc[t][1] = mfma32(av[x][t], b1.b[g], acc[t][1]);
+                        acc[t][0] = mfma32(av[x][t], b0.b[0], acc[t][0]);
+                        acc[t][1] = mfma32(av[x][t], b1.b[0], acc[t][1]);
                     }
-            if (s4 < 3) {
-                // order: the 2 NT LDS reads first, then MFMA / 3 VALU pairs
-#pragma unroll
-                for (int i = 0; i < 2 * NT; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-                for (int i = 0; i < 4 * NT * NB; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                    if (i < 7) load_a1(buf, i + 1, x, av[x]);
                 }
+                if (i < 7) {
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    av[0][t] = an[0][t];
-                    av[1][t] = an[1][t];
+                    for (int x = 0; x < 2; ++x) {
+#pragma unroll
+                        for (int k = 0; k < 2 * NT; ++k) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 6 / NT, 0);
+                        }
+#pragma unroll
+                        for (int k = 0; k < NT; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    }
+                    b0 = d0;
+                    b1 = d1;
                 }
-                b0 = c0;
-                b1 = c1;
+            }
+        } else {
+            v8h an[2][NT];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (i < 7) {
+                    load_a(buf, i + 1, an);
+                    d0 = decode<T>(f0, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on0);
+                    d1 = decode<T>(f1, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on1);
+                }
+                // hi for every (tile, stream), then lo: dependent MFMAs 2 NT issues apart
+#pragma unroll
+                for (int g = 0; g < NB; ++g)
+#pragma unroll
+                    for (int x = 0; x < 2; ++x)
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) {
+                            acc[t][0] = mfma32(av[x][t], b0.b[g], acc[t][0]);
+                            acc[t][1] = mfma32(av[x][t], b1.b[g], acc[t][1]);
+                        }
+                if (i < 7) {
+                    // order: the 2 NT LDS reads first, then MFMA / VALU groups
+#pragma unroll
+                    for (int k = 0; k < 2 * NT; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+                    for (int k = 0; k < 4 * NT * NB; ++k) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 6 / NT, 0);
+                    }
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        av[0][t] = an[0][t];
+                        av[1][t] = an[1][t];
+                    }
+                    b0 = d0;
+                    b1 = d1;
+                }
             }
         }
     };
 
-    // one superblock with fragments f0, f1 (current) and n0, n1 (next, loaded here)
-    auto superblock = [&](int kb, const WFrag<T> &f0, const WFrag<T> &f1, WFrag<T> &n0, WFrag<T> &n1)
+    // one superblock with fragments f0, f1 (current; their first part loaded) and n0, n1 (next, first part loaded here)
+    auto superblock = [&](int kb, WFrag<T> &f0, WFrag<T> &f1, WFrag<T> &n0, WFrag<T> &n1)
                           __attribute__((always_inline)) {
         const bool more = kb + 1 < nb;
         const int kn = more ? kb + 1 : kb;  // the last superblock reloads itself: same load count every iteration
         dma_chunk(sh_a1, kb, 1);
         __builtin_amdgcn_sched_barrier(0);
-        // next superblock's weights: a whole superblock of compute to land
-        wfrag_load<T>(r0, v0, kn * BB, kg, n0);
-        wfrag_load<T>(r1, v1, kn * BB, kg, n1);
+        // Weights one half superblock ahead: this block's second-half codes now, the next block's header and
+        // first-half codes during the second half. Each part has half a superblock of compute to land, and only
+        // about one and a half fragments per stream are live at a time.
+        wfrag_load<T, 1>(r0, v0, c0, kb * BB, f0);
+        wfrag_load<T, 1>(r1, v1, c1, kb * BB, f1);
         __builtin_amdgcn_sched_barrier(0);
         half_pass(sh_a0, std::integral_constant<int, 0>{}, f0, f1);
         __builtin_amdgcn_sched_barrier(0);
         // chunk (kb, 1) landed (only the weight loads issued after it may still be in flight)
-        constexpr int kPend = 2 * wfrag_loads<T>();  // s_waitcnt vmcnt(kPend): vmcnt bits 3:0 and 15:14
+        constexpr int kPend = 2 * wfrag_loads<T, 1>();  // s_waitcnt vmcnt(kPend): vmcnt bits 3:0 and 15:14
         __builtin_amdgcn_s_waitcnt(0x0F70 | (kPend & 0xF) | ((kPend >> 4) << 14));
         lds_barrier();  // chunk (kb, 1) visible; chunk buffer 0 free
 
         dma_chunk(sh_a0, kn, 0);
+        wfrag_load<T, 0>(r0, v0, c0, kn * BB, n0);
+        wfrag_load<T, 0>(r1, v1, c1, kn * BB, n1);
         __builtin_amdgcn_sched_barrier(0);
         half_pass(sh_a1, std::integral_constant<int, 1>{}, f0, f1);
         __builtin_amdgcn_sched_barrier(0);
@@ -616,28 +691,32 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
         const float inv0 = __builtin_amdgcn_rcpf(nd0), inv1 = __builtin_amdgcn_rcpf(nd1);
         const float k0 = ds0 * inv0, k1 = ds1 * inv1;
         float km0 = 0.0f, km1 = 0.0f;
-        v4h bm0, bm1;
+        v8h bm0, bm1;
         if constexpr (MIN) {
             km0 = -half_to_float(f0.h.x >> 16) * inv0;
             km1 = -half_to_float(f1.h.x >> 16) * inv1;
-            bm0 = min_b<T>(f0, kg);
-            bm1 = min_b<T>(f1, kg);
+            bm0 = min_b<T>(f0);
+            bm1 = min_b<T>(f1);
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             if constexpr (MIN) {
-                const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-                const v4h am = *(const v4h *) (sh_s + (t * 16 + jl) * kRowS + 8 * kg);
-                const v4f m0 = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm0, z, 0, 0, 0);
-                const v4f m1 = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm1, z, 0, 0, 0);
+                // one min-term product at a time (each is 16 registers)
+                v16f z;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc[t][0][r] = fmaf_(acc[t][0][r], k0, km0 * m0[r]);
-                    acc[t][1][r] = fmaf_(acc[t][1][r], k1, km1 * m1[r]);
+                for (int r = 0; r < 16; ++r) z[r] = 0.0f;
+                const v8h am = *(const v8h *) (sh_s + (t * 32 + jl) * kRowS + 16 * hh);
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const v16f mt = mfma32(am, m ? bm1 : bm0, z);
+                    const float k = m ? k1 : k0, km = m ? km1 : km0;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[t][m][r] = fmaf_(acc[t][m][r], k, km * mt[r]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
+                for (int r = 0; r < 16; ++r) {
                     acc[t][0][r] *= k0;
                     acc[t][1][r] *= k1;
                 }
@@ -657,90 +736,96 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     }
 
     dma_wait();  // the last (unused) sums load
+    // output (token i, weight row row0) of acc[t][m][r]: i = 32 t + 8 (r / 4) + 4 hh + r % 4
     if constexpr (!GLU) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = t * 16 + 4 * kg + r;
+            for (int r = 0; r < 16; ++r) {
+                const int i = t * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
                 if (i < cnt) {
                     float *o = a.dst + (size_t) sh_dst[i] * a.nrows;
-                    o[row0] = acc[t][0][r];
-                    if (row0 + 64 < a.nrows) o[row0 + 64] = acc[t][1][r];
+                    if (row0 < a.nrows) o[row0] = acc[t][0][r];
+                    if (row0 + 128 < a.nrows) o[row0 + 128] = acc[t][1][r];
                 }
             }
     } else {
         // act = up * silu(gate) (reference src/ggml/ggml_mmvq.cu:240-247 epilogue with zero biases; silu(g) =
-        // g / (1 + e^-g) from the hardware exp2 and reciprocal, about 2 ulp), staged as
-        // [token][64 rows] f32 (row stride 68 floats: 16-byte aligned rows, the 64 lanes' writes on distinct banks),
+        // g / (1 + e^-g) from the hardware exp2 and reciprocal, about 2 ulp), staged as [token][64 rows] f32 per wave
+        // pair (waves 0-1 in chunk buffer 0, waves 2-3 in buffer 1; row stride 68 floats: 16-byte aligned rows),
         // then the Q8_1 blocks (token, 32 rows) into the act split image rows: 4 lanes per block, 8 values per lane
         constexpr int kAct = 68;
-        static_assert(ROWS * kAct * 4 <= (int) sizeof(sh_a0), "act tile fits a chunk buffer");
-        float *act = (float *) sh_a0;
+        static_assert(ROWS * kAct * 4 <= ROWS * kRowA, "act tile fits a chunk buffer");
+        float *act = (float *) (wave < 2 ? sh_a0 : sh_a1);
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = t * 16 + 4 * kg + r;
+            for (int r = 0; r < 16; ++r) {
+                const int i = t * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
                 const float g = acc[t][0][r] + 0.0f;
-                act[i * kAct + wave * 16 + jl] = (acc[t][1][r] + 0.0f) * (g * silu_rcp(g));
+                act[i * kAct + (wave & 1) * 32 + jl] = (acc[t][1][r] + 0.0f) * (g * silu_rcp(g));
             }
         __syncthreads();
-        for (int p0 = wave * 16; p0 < 2 * cnt; p0 += 16 * kMmqWaves) {  // wave-uniform trip count
+        for (int p0 = wave * 16; p0 < 4 * cnt; p0 += 16 * kMmqWaves) {  // wave-uniform trip count
             const int p = p0 + lane / 4, q = lane % 4;
-            const bool live = p < 2 * cnt;
-            const int i = live ? p / 2 : 0, blk = p % 2;
-            const float *src = act + i * kAct + 32 * blk + 8 * q;
+            const int i = p < 4 * cnt ? p / 4 : 0, blk = p % 4;
+            const int col = wb * WROWS + 32 * blk + 8 * q;
+            const bool live = p < 4 * cnt && col < a.nrows;  // the same for the 4 lanes of a block
+            const float *src = (const float *) (blk < 2 ? sh_a0 : sh_a1) + i * kAct + 32 * (blk & 1) + 8 * q;
             const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
             const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             // v / d as v * (1 / d): act itself is an fp32 GEMM result, not bit-comparable with the reference's, so
             // the quotient's last-ulp rounding carries no parity
-            const int col = blockIdx.y * 64 + 32 * blk + 8 * q;
             q8_split8<false>(v, a.out_pack + (size_t) sh_dst[i] * a.out_img, a.nrows, col, live);
-            if (live) {
-                if (a.act_out) {
-                    float *ao = a.act_out + (size_t) sh_dst[i] * a.nrows + col;
-                    *(float4 *) ao = x0;
-                    *(float4 *) (ao + 4) = x1;
-                }
+            if (live && a.act_out) {
+                float *ao = a.act_out + (size_t) sh_dst[i] * a.nrows + col;
+                *(float4 *) ao = x0;
+                *(float4 *) (ao + 4) = x1;
             }
         }
     }
 }
 
-template <bool GLU, int NT> const void *mmq_kernel(int type) {
+// One launch runs both lists, the 64-row groups first (blockIdx.y < n_main) and then the experts' <= 32-row
+// remainders, so the smaller workgroups fill the machine while the last large ones finish; blockIdx.x is the weight
+// row block.
+template <int T, bool GLU>
+__global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 4))) void k_mmq(const MmqArgs a) {
+    __shared__ __align__(16) uint8_t sh_a0[kMmqTok * kRowA];
+    __shared__ __align__(16) uint8_t sh_a1[kMmqTok * kRowA];
+    __shared__ __align__(16) uint8_t sh_s[(T == T_Q4_K || T == T_Q5_K) ? kMmqTok * kRowS : 16];
+    __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok];
+    const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst};
+    const int g = blockIdx.y;
+    if (g < a.n_main) mmq_group<T, GLU, 2>(a, g, blockIdx.x, L);
+    else mmq_group<T, GLU, 1>(a, g - a.n_main, blockIdx.x, L);
+}
+
+template <bool GLU> const void *mmq_kernel(int type) {
     switch (type) {
-        case T_Q3_K: return (const void *) k_mmq<T_Q3_K, GLU, NT>;
-        case T_Q4_K: return (const void *) k_mmq<T_Q4_K, GLU, NT>;
-        case T_Q5_K: return (const void *) k_mmq<T_Q5_K, GLU, NT>;
-        case T_Q6_K: return (const void *) k_mmq<T_Q6_K, GLU, NT>;
+        case T_Q3_K: return (const void *) k_mmq<T_Q3_K, GLU>;
+        case T_Q4_K: return (const void *) k_mmq<T_Q4_K, GLU>;
+        case T_Q5_K: return (const void *) k_mmq<T_Q5_K, GLU>;
+        case T_Q6_K: return (const void *) k_mmq<T_Q6_K, GLU>;
     }
     return nullptr;
 }
 
-int launch_one(const void *fn, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
+// groups: upper bound of the 64-row list (its workgroups return past the device-side count); expert path: then the
+// <= 32-row remainders (at most one per expert), with the second prefix list
+int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
+    const void *fn = glu ? mmq_kernel<true>(type) : mmq_kernel<false>(type);
+    if (!fn) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
     if (groups <= 0) return host::OK;
     MmqArgs arg = a;
+    arg.n_main = groups;
+    const int total = groups + (a.bounds ? a.n_expert : 0);
     void *args[] = {&arg};
-    const int rows = glu ? 64 : 128;
-    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) groups, (unsigned) ((a.nrows + rows - 1) / rows)),
+    const int rows = glu ? 128 : 256;  // weight rows per workgroup
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) ((a.nrows + rows - 1) / rows), (unsigned) total),
                                          dim3(kMmqThreads), args, 0, st);
     if (e != hipSuccess) return host::set_error(host::ERR_LAUNCH, "mmq: %s", hipGetErrorString(e));
     return host::check_launch("mmq");
-}
-
-// groups: upper bound of the 4-tile list (its kernel returns past the device-side count); expert path: then the
-// 2-tile kernel over the <= 32-row remainders (at most one per expert), with the second prefix list
-int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
-    const void *f4 = glu ? mmq_kernel<true, 4>(type) : mmq_kernel<false, 4>(type);
-    const void *f2 = glu ? mmq_kernel<true, 2>(type) : mmq_kernel<false, 2>(type);
-    if (!f4 || !f2) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
-    FNS_TRY(launch_one(f4, glu, a, groups, st));
-    if (!a.bounds) return host::OK;
-    MmqArgs t = a;
-    t.gprefix = a.gprefix + a.n_expert + 1;
-    t.tail = 1;
-    return launch_one(f2, glu, t, a.n_expert, st);
 }
 
 int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
