@@ -41,33 +41,44 @@ namespace {
 constexpr int kMmqThreads = 256;   // 4 waves
 constexpr int kMmqWaves = kMmqThreads / 64;
 constexpr int kMmqRows = 64;       // row granularity of the weight matrices
-constexpr int kMmqTok = 64;        // activation rows per workgroup (4 MFMA tiles of 16)
+constexpr int kMmqTok = 64;        // activation rows per workgroup (2 MFMA tiles of 32)
 constexpr int kCompactThreads = 1024;
 
 // ---- scratch layout of the expert path --------------------------------------------------------------------------
 // bounds[n_expert + 1] (sorted-row offset of each expert); the GEMM's group prefixes gprefix[2][n_expert + 1]: the
-// 64-row groups of each expert for the 4-tile kernel (n_e / 64 full ones, and the remainder if it is > 32 rows), and
-// the remainder groups of <= 32 rows for the 2-tile kernel.
+// 64-row groups of each expert (n_e / 64 full ones, and the remainder if it is > 32 rows; two 32-row MFMA tiles), and
+// the remainder groups of <= 32 rows (one tile).
 inline size_t bounds_bytes(int64_t n_expert) { return (size_t) 3 * (n_expert + 1) * 4; }
 inline size_t gprefix_bytes(int64_t n_expert) { return (size_t) 2 * (n_expert + 1) * 4; }
 
 // ---- compaction (ggml mm_ids_helper semantics, stable) ------------------------------------------------------------
 // ids [n_tok][k] -> pairs p = t k + j sorted by expert, ties in p order: ids_dst[q] = p, ids_src1[q] = the activation
 // row of p (t when x_rows_per_tok = 1, p when x_rows_per_tok = k), bounds[e] = first sorted position of expert e.
-// One workgroup: histogram and prefix in LDS, then rounds of 1024 pairs ranked within each wave by ballots on the
-// expert id bits (lanes sharing an expert find each other without a loop), wave counts prefixed across the round.
+// One workgroup; wave w owns a contiguous chunk of the pairs: per-wave histograms (LDS atomics), one prefix over
+// (expert, wave) in that order, then each wave walks its chunk again in order, ranking the lanes that share an expert
+// by ballots on the expert id bits, and advances its own running positions - two passes over the ids, three barriers.
 __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *__restrict__ ids, int n, int k, int ne,
                                                                  int x_rows_per_tok, int32_t *__restrict__ ids_src1,
                                                                  int32_t *__restrict__ ids_dst, int32_t *bounds,
                                                                  int32_t *gprefix) {
-    __shared__ int cnt[256], base[256];
-    __shared__ int wcnt[kCompactThreads / kWave][256];
+    constexpr int NW = kCompactThreads / kWave;
+    __shared__ int cnt[256];
+    __shared__ int wpos[NW][256];  // per-wave counts, then each wave's next sorted position per expert
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-    for (int e = tid; e < 256; e += kCompactThreads) cnt[e] = 0;
+    for (int i = tid; i < NW * 256; i += kCompactThreads) (&wpos[0][0])[i] = 0;
     __syncthreads();
-    for (int p = tid; p < n; p += kCompactThreads) {
-        const int e = ids[p];
-        if (e >= 0 && e < ne) atomicAdd(&cnt[e], 1);
+    const int chunk = (n + NW * kWave - 1) / (NW * kWave) * kWave;  // pairs per wave, a multiple of 64
+    const int p0 = wave * chunk, p1 = min(n, p0 + chunk);
+    for (int p = p0 + lane; p < p0 + chunk; p += kWave) {  // wave-uniform trip count
+        const int e = p < p1 ? ids[p] : -1;
+        if (e >= 0 && e < ne) atomicAdd(&wpos[wave][e], 1);
+    }
+    __syncthreads();
+    if (tid < ne) {
+        int c = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) c += wpos[w][tid];
+        cnt[tid] = c;
     }
     __syncthreads();
     if (wave == 0) {  // exclusive prefix over <= 256 experts: 4 per lane, then a lane scan
@@ -97,7 +108,14 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         for (int j = 0; j < 4; ++j) {
             const int e = 4 * lane + j;
             if (e < ne) {
-                base[e] = run;
+                // the expert's sorted positions, split over the waves in wave order
+                int pos = run;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    const int c = wpos[w][e];
+                    wpos[w][e] = pos;
+                    pos += c;
+                }
                 bounds[e] = run;
                 gprefix[e] = rung;
                 gprefix[ne + 1 + e] = rung2;
@@ -113,9 +131,8 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         }
     }
     __syncthreads();
-    for (int r0 = 0; r0 < n; r0 += kCompactThreads) {
-        const int p = r0 + tid;
-        const int e = p < n ? ids[p] : -1;
+    for (int p = p0 + lane; p < p0 + chunk; p += kWave) {
+        const int e = p < p1 ? ids[p] : -1;
         const bool live = e >= 0 && e < ne;
         // lanes with the same expert id: intersect the ballots of each id bit (and of liveness)
         uint64_t same = __ballot(live);
@@ -126,23 +143,13 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         }
         if (!live) same = 0;
         const int rank = __popcll(same & ((1ull << lane) - 1ull));
-        for (int i = tid; i < (kCompactThreads / kWave) * 256; i += kCompactThreads) (&wcnt[0][0])[i] = 0;
-        __syncthreads();
-        if (live && rank == 0) wcnt[wave][e] = __popcll(same);
-        __syncthreads();
         if (live) {
-            int pos = base[e] + rank;
-            for (int w = 0; w < wave; ++w) pos += wcnt[w][e];
+            const int pos = wpos[wave][e] + rank;
             ids_dst[pos] = p;
             ids_src1[pos] = x_rows_per_tok == 1 ? p / k : p;
         }
-        __syncthreads();
-        for (int e2 = tid; e2 < ne; e2 += kCompactThreads) {
-            int s = 0;
-            for (int w = 0; w < kCompactThreads / kWave; ++w) s += wcnt[w][e2];
-            base[e2] += s;
-        }
-        __syncthreads();
+        // (this wave's reads above complete before its write below: one wave, LDS accesses in order)
+        if (live && rank == 0) wpos[wave][e] += __popcll(same);
     }
 }
 
@@ -443,8 +450,15 @@ struct MmqLds {
     uint8_t (&s)[kMmqTok * kRowS];
     int (&src)[kMmqTok];
     int (&dst)[kMmqTok];
+    int (&grp)[4];  // the group's expert, first sorted row and row count
 };
 
+#ifdef FNS_MPROBE
+__device__ unsigned long long g_mprobe[2][8192][14];
+#define MMQ_MARK(i) do { if (threadIdx.x == 0) g_mprobe[GLU][blockIdx.x + gridDim.x * blockIdx.y][i] = wall_clock64(); } while (0)
+#else
+#define MMQ_MARK(i) do { } while (0)
+#endif
 // Group g of the launch's list (NT = 2: the 64-row groups and remainders > 32 rows; NT = 1: the expert's <= 32-row
 // remainder), weight row block wb.
 template <int T, bool GLU, int NT>
@@ -462,30 +476,41 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
     const int hh = lane / 32, jl = lane % 32;
 
-    // which expert / rows of activations
+    // which expert / rows of activations: thread t < n_expert tests whether group g is expert t's (gp[t] <= g <
+    // gp[t + 1]); all the prefix loads are independent, one round trip, and the one match publishes through LDS
     int e = 0, seg = 0, cnt = 0;
     if (a.bounds) {
         const int32_t *gp = NT == 2 ? a.gprefix : a.gprefix + a.n_expert + 1;
         if (g >= gp[a.n_expert]) return;
-        int lo = 0, hi = a.n_expert;  // largest e with gp[e] <= g
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (gp[mid] <= g) lo = mid;
-            else hi = mid;
+        if (tid < a.n_expert) {
+            const int g0 = gp[tid], g1 = gp[tid + 1], b0 = a.bounds[tid], b1 = a.bounds[tid + 1];
+            if (g0 <= g && g < g1) {
+                int c, sg;
+                if constexpr (NT == 1) {  // the expert's last rows: n_e % 64 of them
+                    c = (b1 - b0) % kMmqTok;
+                    sg = b1 - c;
+                } else {
+                    sg = b0 + (g - g0) * kMmqTok;
+                    c = min(kMmqTok, b1 - sg);
+                }
+                L.grp[0] = tid;
+                L.grp[1] = sg;
+                L.grp[2] = c;
+            }
         }
-        e = lo;
-        if constexpr (NT == 1) {  // the expert's last rows: n_e % 64 of them
-            cnt = (a.bounds[e + 1] - a.bounds[e]) % kMmqTok;
-            seg = a.bounds[e + 1] - cnt;
-        } else {
-            seg = a.bounds[e] + (g - gp[e]) * kMmqTok;
-            cnt = min(kMmqTok, a.bounds[e + 1] - seg);
-        }
+        __syncthreads();
+        e = __builtin_amdgcn_readfirstlane(L.grp[0]);
+        seg = __builtin_amdgcn_readfirstlane(L.grp[1]);
+        cnt = __builtin_amdgcn_readfirstlane(L.grp[2]);
     } else {
         seg = g * kMmqTok;
         cnt = min(kMmqTok, a.n_rows - seg);
     }
     if (cnt <= 0) return;
+    MMQ_MARK(0);
+#ifdef FNS_MPROBE
+    if (threadIdx.x == 0) g_mprobe[GLU][blockIdx.x + gridDim.x * blockIdx.y][13] = NT * 1000 + cnt;
+#endif
     for (int i = tid; i < ROWS; i += kMmqThreads) {
         const int q = seg + min(i, cnt - 1);
         sh_src[i] = a.src ? a.src[q] : q;
@@ -539,6 +564,7 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
     wfrag_load<T, 0>(r1, v1, c1, 0, f1);
     dma_wait();
     lds_barrier();
+    MMQ_MARK(1);
 
     // acc[t][m] is kept in units of the current superblock's d (per lane: its row's d, 1 if d = 0), so the MFMAs
     // accumulate into it directly; between superblocks it is rescaled and the min term added (fp32 rounding).
@@ -728,6 +754,7 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
         on1 = non1;
         lds_barrier();  // chunk (kb + 1, 0) visible; chunk buffer 1 and the sums free
         dma_sums(kn);  // read at the end of superblock kb + 1, after its first barrier
+        MMQ_MARK(2 + kb);
     };
     // the fragment sets swap roles every superblock
     for (int kb = 0; kb < nb; kb += 2) {
@@ -784,6 +811,7 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
             }
         }
     }
+    MMQ_MARK(12);
 }
 
 // One launch runs both lists, the 64-row groups first (blockIdx.y < n_main) and then the experts' <= 32-row
@@ -794,8 +822,8 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     __shared__ __align__(16) uint8_t sh_a0[kMmqTok * kRowA];
     __shared__ __align__(16) uint8_t sh_a1[kMmqTok * kRowA];
     __shared__ __align__(16) uint8_t sh_s[(T == T_Q4_K || T == T_Q5_K) ? kMmqTok * kRowS : 16];
-    __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok];
-    const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst};
+    __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok], sh_grp[4];
+    const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp};
     const int g = blockIdx.y;
     if (g < a.n_main) mmq_group<T, GLU, 2>(a, g, blockIdx.x, L);
     else mmq_group<T, GLU, 1>(a, g - a.n_main, blockIdx.x, L);
@@ -828,6 +856,19 @@ int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st)
     return host::check_launch("mmq");
 }
 
+#ifdef FNS_MPROBE
+}  // namespace
+}  // namespace fns
+extern "C" int fns_mprobe_read(void *host) {
+    return (int) hipMemcpyFromSymbol(host, HIP_SYMBOL(fns::g_mprobe), sizeof(fns::g_mprobe));
+}
+extern "C" int fns_mprobe_clear() {
+    static unsigned long long z[2][8192][14];
+    return (int) hipMemcpyToSymbol(HIP_SYMBOL(fns::g_mprobe), z, sizeof(z));
+}
+namespace fns {
+namespace {
+#endif
 int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
     if (!host::is_kquant(type)) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
     if (ncols <= 0 || ncols % 256 || nrows <= 0 || nrows % kMmqRows || ncols > 65536)

@@ -148,11 +148,21 @@ __global__ __launch_bounds__(512) void k_gemm_router(const void *__restrict__ w,
 
 namespace {
 
-__global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ logits, int32_t *__restrict__ ids,
-                                                   float *__restrict__ w, int n_expert, int k, int gating, int norm) {
+// One token per 256-thread workgroup: the rank-based block top-k (same probabilities, same selection and weights as
+// route_topk_wave, bit for bit), without the k dependent argmax rounds of a single wave.
+constexpr int kRouteThreads = 256;
+__global__ __launch_bounds__(kRouteThreads) void k_route_topk(const float *__restrict__ logits, int32_t *__restrict__ ids,
+                                                              float *__restrict__ w, int n_expert, int k, int gating,
+                                                              int norm) {
+    __shared__ uint64_t s_key[256];
+    __shared__ int s_sel[16];
+    __shared__ float s_pv[16];
     const int t = blockIdx.x;
-    route_topk_wave(logits + (size_t) t * n_expert, n_expert, k, gating, norm, ids + (size_t) t * k,
-                    w + (size_t) t * k, nullptr);
+    route_topk_block<kRouteThreads>(logits + (size_t) t * n_expert, n_expert, k, gating, s_key, s_sel, s_pv);
+    if ((int) threadIdx.x < k) {
+        ids[(size_t) t * k + threadIdx.x] = s_sel[threadIdx.x];
+        w[(size_t) t * k + threadIdx.x] = route_weight(s_pv, k, norm, threadIdx.x);
+    }
 }
 
 __global__ void k_moe_combine(const float *__restrict__ dexp, const float *__restrict__ escale,
@@ -224,8 +234,8 @@ int route_topk(const float *logits, int32_t *ids, float *w, int n_expert, int k,
         (gating != 0 && gating != 1))
         return host::set_error(host::ERR_SHAPE, "route_topk: expected 1 <= k <= min(16, n_expert), n_expert <= 256");
     if (n_tok == 0) return host::OK;
-    hipLaunchKernelGGL(k_route_topk, dim3((unsigned) n_tok), dim3(64), 0, st, logits, ids, w, n_expert, k, gating,
-                       norm);
+    hipLaunchKernelGGL(k_route_topk, dim3((unsigned) n_tok), dim3(kRouteThreads), 0, st, logits, ids, w, n_expert, k,
+                       gating, norm);
     return host::check_launch("route_topk");
 }
 
