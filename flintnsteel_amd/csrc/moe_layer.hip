@@ -993,7 +993,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     __shared__ RouteLds rs;
     __shared__ const uint8_t *s_tab[256];
     __shared__ float s_dexp[16][kFusedRows];
-    __shared__ float s_e[16], s_w[16], s_act[kGuRows];
+    __shared__ float s_e[16], s_w[16], s_act[kGuRows], s_res[kFusedRows];
     __shared__ int s_fail;
     constexpr int BG = Traits<TGU>::bytes, BD = Traits<TDN>::bytes;
     const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
@@ -1016,6 +1016,9 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     // 1. waves 1-15: x image and expert table; wave 0: logits. Routing (all selected slots are needed here).
     if (wave != 0 && tid - kWave < a.NE)
         s_tab[tid - kWave] = gload<const uint8_t *>((const uint8_t *) (a.table + (tid - kWave)));
+    // this workgroup's residual rows, read now rather than after the exchange (x_resid may alias out: each
+    // workgroup reads and writes only its own rows)
+    if (wave == kQWaves - 1 && lane64 < kFusedRows) s_res[lane64] = a.x_resid ? a.x_resid[r0 + lane64] : 0.0f;
     if (tid == 0) s_fail = 0;
     dma_waves_from<kQWaves>(s_x, a.xpack, xbytes, 1);
     if (wave != 0) dma_wait();
@@ -1201,7 +1204,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         float moe = (s_dexp[0][tid] * s_e[0]) * s_w[0];
         for (int j = 1; j < K; ++j) moe = moe + (s_dexp[j][tid] * s_e[j]) * s_w[j];
         moe = moe + 0.0f;
-        float o = a.x_resid ? moe + a.x_resid[r] : moe;
+        float o = a.x_resid ? moe + s_res[tid] : moe;
         if (s_fail) o = __builtin_nanf("");
         a.out[r] = o;
     }
