@@ -21,7 +21,8 @@ The JSON line also carries:
                  on this host's cores on a bounded sample.
   extra        - configs 1 (Q3_K/Q5_K mix), 2 (4-token speculative verify), 3 (48-layer Q4_K/Q6_K stack) and 4
                  (512-token prefill through the f16-MFMA split-operand grouped GEMM, Dirichlet(0.3)-skewed router bias; MFMA
-                 utilisation = 38.65 G int8 ops per layer / time / 5.0 POP/s dense int8 peak).
+                 utilisation = 38.65 G int8 ops per layer / time / 5.0 POP/s dense int8 peak), and the reference
+                 model's whole MoE block (RMSNorm, 256 experts top-6 sigmoid, width 512, shared expert) at decode.
 """
 from __future__ import annotations
 
@@ -85,6 +86,33 @@ def capture(torch, layers, xs, outs, wss, steps_per_graph: int):
             for l, layer in enumerate(layers):
                 layer(xs[st, l], out=outs[l], ws=wss[l])
     return g
+
+
+def run_flint(torch, synth, n_layers: int = 8, replays: int = 40) -> dict:
+    """The reference model's MoE block shape (src/model.cpp:159-164: RMSNorm, bf16 router, sigmoid top-6 of 256
+    experts of width 512, F16 guard, shared expert of width 1024; gate/up Q4_K, down Q5_K), decode batch 1 through
+    fns_hip_moe_layer with the residual added; n_layers resident copies replayed in one graph."""
+    layers = [synth.build_flint_layer(H, 512, 256, 6, 1024, Q4_K, Q5_K, SEED, layer=600 + l) for l in range(n_layers)]
+    xs = [synth.activations(1, H, SEED, layer=700 + l) for l in range(n_layers)]
+    outs = [torch.empty(1, H, device="cuda") for _ in layers]
+    wss = [layer.workspace(1) for layer in layers]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for l, layer in enumerate(layers):
+            layer(xs[l], out=outs[l], ws=wss[l], x_resid=xs[l])
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for l, layer in enumerate(layers):
+            layer(xs[l], out=outs[l], ws=wss[l], x_resid=xs[l])
+    us = time_graph(torch, g, replays, 3) * 1e3 / n_layers
+    routed = 6 * (2 * 512 * (H // 256) * 144 + H * 2 * 176)
+    shared = 2 * 1024 * (H // 256) * 144 + H * 4 * 176
+    byts = routed + shared + 256 * H * 2
+    del g
+    return {"us_per_layer": round(us, 3), "hbm_bytes_per_layer": byts, "hbm_gbs": round(byts / (us * 1e-6) / 1e9, 1)}
 
 
 def time_graph(torch, g, replays: int, warmup: int) -> float:
@@ -325,6 +353,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         extra["config4_prefill512"] = run_prefill(torch, synth)
         log(f"config4 (prefill 512): {extra['config4_prefill512']}")
+        torch.cuda.empty_cache()
+        extra["flint_block_decode"] = run_flint(torch, synth)
+        log(f"flint block (decode): {extra['flint_block_decode']}")
     cpu = None
     if not args.no_cpu:
         if args.no_extra:

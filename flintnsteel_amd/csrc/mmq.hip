@@ -969,7 +969,7 @@ int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, i
 // activations quantised once per token, gate and up in one pass with the SwiGLU and the Q8_1 of act fused, and the
 // expert sort shared by both GEMMs.
 namespace {
-constexpr int kPrefillSections = 11;
+constexpr int kPrefillSections = 15;
 void prefill_sizes(const FnsMoeLayer *L, int64_t T, size_t *sz) {
     const int64_t P = T * L->k;
     sz[0] = (size_t) T * L->n_expert * 4;                 // logits
@@ -983,6 +983,11 @@ void prefill_sizes(const FnsMoeLayer *L, int64_t T, size_t *sz) {
     sz[8] = bounds_bytes(L->n_expert);                    // bounds + group prefix
     sz[9] = L->guard ? (size_t) P * L->inter * 4 : 0;     // f32 act (F16 guard only)
     sz[10] = (size_t) P * 4;                              // escale
+    const int64_t fs = L->shexp_inter > 0 ? L->shexp_inter : 0;
+    sz[11] = L->ffn_norm ? (size_t) T * L->hidden * 4 : 0;                         // RMSNorm output h
+    sz[12] = L->ffn_norm ? (size_t) T * host::q8_1_row_bytes(L->hidden) : 0;      // its Q8_1 blocks (unused)
+    sz[13] = fs ? (size_t) T * mmq_image_bytes(fs) : 0;                            // shared-expert act images
+    sz[14] = fs ? (size_t) T * L->hidden * 4 : 0;                                  // shared-expert output
 }
 }  // namespace
 
@@ -999,6 +1004,37 @@ int moe_prefill_workspace(const FnsMoeLayer *L, int64_t n_tok, size_t *offsets, 
     return host::OK;
 }
 
+// The shared expert over the n_tok split-image rows of h: one GLU launch (gate and up, SwiGLU, Q8_1 of act into
+// act_img) and the down launch into sh [n_tok][hidden]; both are the grouped GEMM over one dense matrix.
+int mmq_dense_shared(const FnsMoeLayer *L, const void *ximg, int64_t n_tok, void *act_img, float *sh, hipStream_t st) {
+    const int gt = L->shexp_gu_type ? L->shexp_gu_type : L->gu_type;
+    const int dt = L->shexp_down_type ? L->shexp_down_type : L->down_type;
+    FNS_TRY(check_mmq_shape(gt, L->hidden, L->shexp_inter));
+    FNS_TRY(check_mmq_shape(dt, L->shexp_inter, L->hidden));
+    const int groups = (int) ((n_tok + kMmqTok - 1) / kMmqTok);
+    MmqArgs g{};
+    g.w_dense = (const uint8_t *) L->shexp_gate;
+    g.off_a = 0;
+    g.off_b = (const uint8_t *) L->shexp_up - (const uint8_t *) L->shexp_gate;
+    g.ncols = L->hidden;
+    g.nrows = L->shexp_inter;
+    g.xpack = (const uint8_t *) ximg;
+    g.x_img = (int64_t) mmq_image_bytes(L->hidden);
+    g.n_rows = (int) n_tok;
+    g.out_pack = (uint8_t *) act_img;
+    g.out_img = (int64_t) mmq_image_bytes(L->shexp_inter);
+    FNS_TRY(launch_mmq(gt, true, g, groups, st));
+    MmqArgs d{};
+    d.w_dense = (const uint8_t *) L->shexp_down;
+    d.ncols = L->shexp_inter;
+    d.nrows = L->hidden;
+    d.xpack = (const uint8_t *) act_img;
+    d.x_img = (int64_t) mmq_image_bytes(L->shexp_inter);
+    d.n_rows = (int) n_tok;
+    d.dst = sh;
+    return launch_mmq(dt, false, d, groups, st);
+}
+
 int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int64_t n_tok, void *ws,
                 size_t ws_bytes, hipStream_t st) {
     if (!L || !x || !out || !ws || !L->router_w || !L->table) return host::set_error(host::ERR_SHAPE, "moe_prefill: null argument");
@@ -1009,6 +1045,8 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
         return host::set_error(host::ERR_SHAPE, "moe_prefill: 1 <= k <= min(16, n_expert), n_expert <= 256");
     FNS_TRY(check_mmq_shape(L->gu_type, L->hidden, L->inter));
     FNS_TRY(check_mmq_shape(L->down_type, L->inter, L->hidden));
+    if (L->shexp_inter < 0 || (L->shexp_inter > 0 && (!L->shexp_gate || !L->shexp_up || !L->shexp_down)))
+        return host::set_error(host::ERR_SHAPE, "moe_prefill: shared expert: gate, up and down given");
     size_t sz[kPrefillSections];
     prefill_sizes(L, n_tok, sz);
     uint8_t *sec[kPrefillSections];
@@ -1023,6 +1061,11 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
     const int64_t P = n_tok * L->k;
     const char *const *table = (const char *const *) L->table;
 
+    // RMSNorm first when the layer has one: the router and the experts read h (reference src/engine.cu:331)
+    if (L->ffn_norm) {
+        FNS_TRY(rms_norm_q8_1(x, L->ffn_norm, (float *) sec[11], sec[12], (int) L->hidden, L->norm_eps, (int) n_tok, st));
+        x = (const float *) sec[11];
+    }
     FNS_TRY(gemm_router_bias(L->router_dtype, L->router_w, L->router_bias, x, logits, L->hidden, L->n_expert, (int) n_tok,
                              st));
     FNS_TRY(route_topk(logits, ids, w, L->n_expert, L->k, (int) n_tok, L->gating, L->norm_w, st));
@@ -1039,7 +1082,12 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
     // themselves (activation row = output row = p), so the gate/up sort is reused with ids_dst as the source list
     FNS_TRY(mmq_gemm_experts(L->down_type, table, L->down_off, 0, false, L->inter, L->hidden, L->n_expert, sec[4], P,
                              dstr, dstr, bounds, bounds + L->n_expert + 1, dexp, nullptr, nullptr, st));
-    return moe_combine(dexp, L->guard ? escale : nullptr, w, nullptr, x_resid, out, L->hidden, L->k, (int) n_tok, st);
+    float *sh = nullptr;
+    if (L->shexp_inter > 0) {  // shared expert (reference src/engine.cu:351-355): dense gate/up + SwiGLU, then down
+        sh = (float *) sec[14];
+        FNS_TRY(mmq_dense_shared(L, sec[3], n_tok, sec[13], sh, st));
+    }
+    return moe_combine(dexp, L->guard ? escale : nullptr, w, sh, x_resid, out, L->hidden, L->k, (int) n_tok, st);
 }
 
 }  // namespace impl

@@ -88,6 +88,11 @@ struct LayerArgs {
     int *chan;            // n_tok > 1: [kMaxCh][kChanInts] channel table, then n_distinct, then the router arrival count
     int64_t xq_row_bytes;
     int fused;            // the shape fits the fused kernel (n_tok = 1)
+    const float *sh;      // [T][H] shared-expert output added in the combine, or null
+    // host side only: the caller's x (x above is then the RMSNorm output), the shared expert's buffers
+    const float *x_in;
+    float *act_sh, *tmp_sh, *sh_out;
+    uint8_t *xq_sh;
 };
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t) b << 16); }
@@ -774,13 +779,13 @@ __global__ __launch_bounds__(256) void k_down_combine(const LayerArgs a) {
         if (lane == 0 && ok) s_dexp[ch][row - r0] = acc;
     }
     __syncthreads();
-    // 4. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + 0) (+ x_resid)
+    // 4. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + sh) (+ x_resid), sh: shared expert or 0
     if (tid < T * kDownRows) {
         const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
         if (r < H) {
             float moe = (s_dexp[t * K][rr] * s_e[t * K]) * s_w[t * K];
             for (int j = 1; j < K; ++j) moe = moe + (s_dexp[t * K + j][rr] * s_e[t * K + j]) * s_w[t * K + j];
-            moe = moe + 0.0f;
+            moe = moe + (a.sh ? a.sh[(size_t) t * H + r] : 0.0f);
             a.out[(size_t) t * H + r] = a.x_resid ? moe + a.x_resid[(size_t) t * H + r] : moe;
         }
     }
@@ -870,12 +875,12 @@ __global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
     }
     __syncthreads();
     FNS_MARK(2, blockIdx.x, 3);
-    // 5. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + 0) (+ x_resid)
+    // 5. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + sh) (+ x_resid), sh: shared expert or 0
     if (tid < T * kDownRows) {
         const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
         float moe = (s_dexp[t * K][rr] * s_e[t * K]) * s_w[t * K];
         for (int j = 1; j < K; ++j) moe = moe + (s_dexp[t * K + j][rr] * s_e[t * K + j]) * s_w[t * K + j];
-        moe = moe + 0.0f;
+        moe = moe + (a.sh ? a.sh[(size_t) t * H + r] : 0.0f);
         a.out[(size_t) t * H + r] = a.x_resid ? moe + a.x_resid[(size_t) t * H + r] : moe;
     }
     FNS_MARK(2, blockIdx.x, 4);
@@ -954,12 +959,12 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
     }
     __syncthreads();
     FNS_MARK(2, blockIdx.x, 3);
-    // combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + 0) (+ x_resid)
+    // combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + sh) (+ x_resid), sh: shared expert or 0
     if (tid < T * kDownRows) {
         const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
         float moe = (s_dexp[t * K][rr] * s_e[t * K]) * s_w[t * K];
         for (int j = 1; j < K; ++j) moe = moe + (s_dexp[t * K + j][rr] * s_e[t * K + j]) * s_w[t * K + j];
-        moe = moe + 0.0f;
+        moe = moe + (a.sh ? a.sh[(size_t) t * H + r] : 0.0f);
         a.out[(size_t) t * H + r] = a.x_resid ? moe + a.x_resid[(size_t) t * H + r] : moe;
     }
     FNS_MARK(2, blockIdx.x, 4);
@@ -993,7 +998,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     __shared__ RouteLds rs;
     __shared__ const uint8_t *s_tab[256];
     __shared__ float s_dexp[16][kFusedRows];
-    __shared__ float s_e[16], s_w[16], s_act[kGuRows], s_res[kFusedRows];
+    __shared__ float s_e[16], s_w[16], s_act[kGuRows], s_res[kFusedRows], s_sh[kFusedRows];
     __shared__ int s_fail;
     constexpr int BG = Traits<TGU>::bytes, BD = Traits<TDN>::bytes;
     const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
@@ -1018,7 +1023,10 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         s_tab[tid - kWave] = gload<const uint8_t *>((const uint8_t *) (a.table + (tid - kWave)));
     // this workgroup's residual rows, read now rather than after the exchange (x_resid may alias out: each
     // workgroup reads and writes only its own rows)
-    if (wave == kQWaves - 1 && lane64 < kFusedRows) s_res[lane64] = a.x_resid ? a.x_resid[r0 + lane64] : 0.0f;
+    if (wave == kQWaves - 1 && lane64 < kFusedRows) {
+        s_res[lane64] = a.x_resid ? a.x_resid[r0 + lane64] : 0.0f;
+        s_sh[lane64] = a.sh ? a.sh[r0 + lane64] : 0.0f;  // the shared expert's output (an earlier kernel's)
+    }
     if (tid == 0) s_fail = 0;
     dma_waves_from<kQWaves>(s_x, a.xpack, xbytes, 1);
     if (wave != 0) dma_wait();
@@ -1203,7 +1211,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         const int r = r0 + tid;
         float moe = (s_dexp[0][tid] * s_e[0]) * s_w[0];
         for (int j = 1; j < K; ++j) moe = moe + (s_dexp[j][tid] * s_e[j]) * s_w[j];
-        moe = moe + 0.0f;
+        moe = moe + s_sh[tid];
         float o = a.x_resid ? moe + s_res[tid] : moe;
         if (s_fail) o = __builtin_nanf("");
         a.out[r] = o;
@@ -1438,10 +1446,11 @@ int by_type_down(int t, const LayerArgs &a, hipStream_t st) {
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
-constexpr int kSections = 12;
+constexpr int kSections = 17;
 
 // Byte sizes of the workspace sections: 0 logits, 1 xq, 2 ids, 3 w, 4 act, 5 escale (documented in fns_hip.h),
-// then internal: 6 xpack, 7 apack, 8 blk_amax, 9 dptr, 10 sync, 11 channel table + arrival count (n_tok > 1).
+// then internal: 6 xpack, 7 apack, 8 blk_amax, 9 dptr, 10 sync, 11 channel table + arrival count (n_tok > 1),
+// 12 RMSNorm output h, 13 shared-expert act, 14 its gate (n_tok > 1), 15 Q8_1 of its act, 16 its output sh.
 void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     const size_t hpad = (size_t) host::pad512(L->hidden), fpad = (size_t) host::pad512(L->inter);
     const size_t ch = (size_t) n_tok * L->k;
@@ -1457,6 +1466,12 @@ void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     sizes[9] = ch * 8;
     sizes[10] = (size_t) kSyncLines * kSyncStride * 4;
     sizes[11] = (size_t) (kMaxCh * kChanInts + 2) * 4;
+    const size_t fs = L->shexp_inter > 0 ? (size_t) L->shexp_inter : 0;
+    sizes[12] = L->ffn_norm ? (size_t) n_tok * L->hidden * 4 : 0;
+    sizes[13] = (size_t) n_tok * fs * 4;
+    sizes[14] = n_tok > 1 ? (size_t) n_tok * fs * 4 : 0;
+    sizes[15] = fs ? (size_t) n_tok * host::q8_1_row_bytes((int64_t) fs) : 0;
+    sizes[16] = fs ? (size_t) n_tok * L->hidden * 4 : 0;
 }
 
 }  // namespace
@@ -1492,6 +1507,14 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     if (L->n_expert > 256 || L->k > L->n_expert)
         return host::set_error(host::ERR_SHAPE, "moe_layer: 1 <= k <= min(16, n_expert), n_expert <= 256");
     if (L->gating != 0 && L->gating != 1) return host::set_error(host::ERR_SHAPE, "moe_layer: bad gating");
+    if (L->shexp_inter < 0 || L->shexp_inter % 256 || L->shexp_inter > 16384 ||
+        (L->shexp_inter > 0 && (!L->shexp_gate || !L->shexp_up || !L->shexp_down)))
+        return host::set_error(host::ERR_SHAPE, "moe_layer: shared expert: width a multiple of 256 (<= 16384), "
+                                                "gate, up and down given");
+    if (L->shexp_inter > 0 && ((L->shexp_gu_type && !host::is_kquant(L->shexp_gu_type)) ||
+                               (L->shexp_down_type && !host::is_kquant(L->shexp_down_type))))
+        return host::set_error(host::ERR_TYPE, "moe_layer: shared expert types %d/%d not supported", L->shexp_gu_type,
+                               L->shexp_down_type);
     if (L->router_dtype != 0 && L->router_dtype != T_BF16)
         return host::set_error(host::ERR_TYPE, "moe_layer: router dtype %d not supported", L->router_dtype);
     if (!host::is_kquant(L->gu_type) || !host::is_kquant(L->down_type))
@@ -1540,15 +1563,44 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     a.chan = (int *) sec[11];
     a.xq_row_bytes = host::q8_1_row_bytes(L->hidden);
     a.fused = n_tok == 1 && fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type)) > 0;
+    a.x_in = x;
+    if (L->ffn_norm) a.x = (const float *) sec[12];  // the router and the experts read h = RMSNorm(x)
+    if (L->shexp_inter > 0) {
+        a.act_sh = (float *) sec[13];
+        a.tmp_sh = (float *) sec[14];
+        a.xq_sh = sec[15];
+        a.sh_out = (float *) sec[16];
+        a.sh = a.sh_out;
+    }
     return host::OK;
 }
 
+// The shared expert of the reference's ffn_block (src/engine.cu:685-690, dense_glu then gemv): gate and up over the
+// Q8_1 of h (one fused GLU launch for one column, else two GEMVs and the GLU), Q8_1 of act, down.
+static int launch_shared(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t st) {
+    const int gt = L->shexp_gu_type ? L->shexp_gu_type : L->gu_type;
+    const int dt = L->shexp_down_type ? L->shexp_down_type : L->down_type;
+    const int64_t H = a.H, Fs = L->shexp_inter;
+    if (a.T == 1) {
+        FNS_TRY(mmvq_swiglu(gt, L->shexp_gate, L->shexp_up, H, Fs, a.xq, a.act_sh, st));
+    } else {
+        FNS_TRY(mmvq(gt, L->shexp_gate, H, Fs, a.xq, a.tmp_sh, a.T, st));
+        FNS_TRY(mmvq(gt, L->shexp_up, H, Fs, a.xq, a.act_sh, a.T, st));
+        FNS_TRY(glu_mmvq(a.tmp_sh, a.act_sh, a.act_sh, (int) (a.T * Fs), st));
+    }
+    FNS_TRY(quantize_q8_1(a.act_sh, a.xq_sh, Fs, a.T, st));
+    return mmvq(dt, L->shexp_down, Fs, H, a.xq_sh, a.sh_out, a.T, st);
+}
+
 static int launch_stage(const FnsMoeLayer *L, const LayerArgs &a, int stage, hipStream_t st) {
-    if (stage == 0) {
+    if (stage == 0) {  // [RMSNorm], router + Q8_1 of x, [shared expert]
+        if (L->ffn_norm)
+            FNS_TRY(rms_norm_q8_1(a.x_in, L->ffn_norm, (float *) a.x, a.xq, a.H, L->norm_eps, a.T, st));
         const int chunks = (int) ((host::pad512(L->hidden) + kK1Threads - 1) / kK1Threads);
         const int n_router_wg = (L->n_expert + kK1Rows - 1) / kK1Rows;
         hipLaunchKernelGGL(k_route_quant, dim3((unsigned) (n_router_wg + chunks * a.T)), dim3(kK1Threads), 0, st, a);
-        return host::check_launch("moe route_quant");
+        FNS_TRY(host::check_launch("moe route_quant"));
+        return L->shexp_inter > 0 ? launch_shared(L, a, st) : host::OK;
     }
     // n_tok = 1 shapes that fit take the fused kernel as stage 1; stage 2 then has nothing left to do
     if (stage == 1) return use_fused(L, a) ? launch_fused(L, a, st) : by_type_gate_up(L->gu_type, a, st);

@@ -242,6 +242,9 @@ class MoeLayerDesc(ctypes.Structure):
         ("gu_type", ctypes.c_int), ("down_type", ctypes.c_int),
         ("table", ctypes.c_void_p), ("gate_off", ctypes.c_size_t), ("up_off", ctypes.c_size_t),
         ("down_off", ctypes.c_size_t), ("router_bias", ctypes.c_void_p),
+        ("ffn_norm", ctypes.c_void_p), ("norm_eps", ctypes.c_float), ("shexp_inter", ctypes.c_int),
+        ("shexp_gu_type", ctypes.c_int), ("shexp_down_type", ctypes.c_int),
+        ("shexp_gate", ctypes.c_void_p), ("shexp_up", ctypes.c_void_p), ("shexp_down", ctypes.c_void_p),
     ]
 
 
@@ -253,12 +256,21 @@ class MoeLayer:
 
     def __init__(self, router_w: torch.Tensor, slots: ExpertSlots, gu_type: int, down_type: int, hidden: int,
                  inter: int, k: int, gating: int = GATING_SOFTMAX, norm: bool = True, guard: bool = False,
-                 router_bias: torch.Tensor | None = None):
+                 router_bias: torch.Tensor | None = None, ffn_norm: torch.Tensor | None = None,
+                 norm_eps: float = 1e-6, shexp: dict | None = None):
+        """shexp: the shared expert, {"gate", "up", "down": uint8 block tensors, "inter": width, "gu_type",
+        "down_type"} (the reference's gate_shexp / up_shexp / down_shexp); ffn_norm: f32 [hidden] RMSNorm weights."""
         self.router_w, self.slots, self.router_bias = router_w, slots, router_bias
+        self.ffn_norm, self.shexp = ffn_norm, shexp
+        sh = shexp or {}
         self.desc = MoeLayerDesc(hidden, inter, slots.n_expert, k, gating, int(norm), int(guard),
                                  _dtype_code(router_w), router_w.data_ptr(), gu_type, down_type,
                                  slots.table.data_ptr(), slots.gate_off, slots.up_off, slots.down_off,
-                                 router_bias.data_ptr() if router_bias is not None else None)
+                                 router_bias.data_ptr() if router_bias is not None else None,
+                                 ffn_norm.data_ptr() if ffn_norm is not None else None, norm_eps,
+                                 sh.get("inter", 0), sh.get("gu_type", 0), sh.get("down_type", 0),
+                                 sh["gate"].data_ptr() if sh else None, sh["up"].data_ptr() if sh else None,
+                                 sh["down"].data_ptr() if sh else None)
 
     def workspace_layout(self, n_tok: int):
         offs = (ctypes.c_size_t * 6)()

@@ -9,7 +9,7 @@ import torch
 
 from . import ops
 
-KIND_ROUTER, KIND_GATE, KIND_UP, KIND_DOWN, KIND_X, KIND_BIAS = range(6)
+KIND_ROUTER, KIND_GATE, KIND_UP, KIND_DOWN, KIND_X, KIND_BIAS, KIND_SHEXP, KIND_NORM = range(8)
 
 
 def tensor_seed(seed: int, layer: int, kind: int) -> int:
@@ -44,6 +44,27 @@ def build_layer(hidden: int, inter: int, n_expert: int, k: int, gu_type: int, do
     quantized_matrices(gu_type, n_expert, inter, hidden, tensor_seed(seed, layer, KIND_UP), std, slots.view("up"))
     quantized_matrices(down_type, n_expert, hidden, inter, tensor_seed(seed, layer, KIND_DOWN), std, slots.view("down"))
     return ops.MoeLayer(router, slots, gu_type, down_type, hidden, inter, k, gating=gating, guard=guard)
+
+
+def build_flint_layer(hidden: int, inter: int, n_expert: int, k: int, shexp_inter: int, gu_type: int, down_type: int,
+                      seed: int, layer: int = 0, std: float = 0.02, guard: bool = True) -> ops.MoeLayer:
+    """A layer shaped like the reference model's MoE blocks (src/model.cpp:159-164: sigmoid gating, bf16 router,
+    normalised top-k weights, a shared expert, RMSNorm before the FFN): build_layer's experts plus the shared
+    expert's gate/up [shexp_inter x hidden] and down [hidden x shexp_inter] (same types) and norm weights
+    ~N(1, 0.1)."""
+    base = build_layer(hidden, inter, n_expert, k, gu_type, down_type, seed, layer=layer,
+                       gating=ops.GATING_SIGMOID, guard=guard, router_dtype=torch.bfloat16, std=std)
+    sseed = tensor_seed(seed, layer, KIND_SHEXP)
+    gate = torch.empty(1, ops.row_bytes(gu_type, hidden) * shexp_inter, dtype=torch.uint8, device="cuda")
+    up = torch.empty_like(gate)
+    down = torch.empty(1, ops.row_bytes(down_type, shexp_inter) * hidden, dtype=torch.uint8, device="cuda")
+    quantized_matrices(gu_type, 1, shexp_inter, hidden, sseed, std, gate)
+    quantized_matrices(gu_type, 1, shexp_inter, hidden, sseed + 1, std, up)
+    quantized_matrices(down_type, 1, hidden, shexp_inter, sseed + 2, std, down)
+    norm = ops.fill_normal(torch.empty(hidden, device="cuda"), tensor_seed(seed, layer, KIND_NORM), mean=1.0, std=0.1)
+    shexp = {"gate": gate, "up": up, "down": down, "inter": shexp_inter, "gu_type": gu_type, "down_type": down_type}
+    return ops.MoeLayer(base.router_w, base.slots, gu_type, down_type, hidden, inter, k, gating=ops.GATING_SIGMOID,
+                        guard=guard, ffn_norm=norm, norm_eps=1e-6, shexp=shexp)
 
 
 def activations(n_tok: int, hidden: int, seed: int, layer: int = 0, step: int = 0) -> torch.Tensor:

@@ -120,6 +120,17 @@ typedef struct FnsMoeLayer {
     const void *const *table;
     size_t gate_off, up_off, down_off;
     const float *router_bias; /* NULL or f32 [n_expert], added to the logits before gating (selection and weights) */
+    /* The rest of the reference's Engine::ffn_block (src/engine.cu:655-696; prefill src/engine.cu:331-357); all zero:
+     * absent. With ffn_norm the layer input x is the residual stream: h = RMSNorm(x) * ffn_norm (eps norm_eps, as
+     * rms_norm_q8_1) feeds the router and the experts. With a shared expert (shexp_inter > 0) its output
+     * sh = down_sh . q8_1(up_sh . q8_1(h) * silu(gate_sh . q8_1(h))) joins the combine as the reference's:
+     * out = (sum_j w_j e_j dexp_j + sh) + x_resid. */
+    const float *ffn_norm;     /* NULL or f32 [hidden] */
+    float norm_eps;
+    int shexp_inter;           /* 0 or the shared expert's width (a positive multiple of 256) */
+    int shexp_gu_type, shexp_down_type;  /* K-quant types of the shared expert's gate/up and down (0: gu_type / down_type) */
+    const void *shexp_gate, *shexp_up;   /* [shexp_inter][hidden] blocks */
+    const void *shexp_down;              /* [hidden][shexp_inter] blocks */
 } FnsMoeLayer;
 
 int fns_hip_moe_workspace_layout(const FnsMoeLayer *layer, int n_tok, size_t *offsets, size_t *total_bytes);
