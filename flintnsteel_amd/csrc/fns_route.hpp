@@ -87,7 +87,121 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ lg, in
     }
 }
 
-// Gating + top-k + renormalisation for one token by a whole workgroup of NT threads (n_expert <= 256). Wave 0
+// LDS scratch of route_topk_block, in 64-bit words: keys [0, 256), candidates [256, 384), group maxima [384, 416),
+// the threshold and the candidate counts after them.
+constexpr int kTopkScratch = 432;
+
+// Group-maximum form (n_expert > 128 in route_topk_block): gating + top-k + renormalisation for one token by a whole
+// workgroup of NT threads (n_expert <= 256). Wave 0
+// computes the probabilities exactly as route_topk_wave (same fp32 operations, so the same bits) and stores for each
+// expert the 64-bit key (bits(p) << 32) | ~e: p >= 0, so the keys order as (p descending, index ascending) and the
+// live ones are distinct and non-zero. Then: the maxima of the 32 groups of 8 consecutive experts, and T0 = the k-th
+// largest of them. At least k keys are >= T0 (those k group maxima), so the top k are all >= T0, and a key below T0
+// exceeds none of them: the top k are the keys >= T0 ranked among themselves (at most 8k candidates, eight threads
+// per candidate). The result is the same as k rounds of argmax with ties to the lower index. Must be called by every
+// thread of the workgroup (it contains barriers). Results: sel[0..k) and their probabilities pv[0..k) in LDS, visible
+// to the whole workgroup on return.
+template <int NT>
+__device__ __forceinline__ void route_topk_filter(const float *__restrict__ lg, int n_expert, int k, int gating,
+                                                 uint64_t *scratch, int *sel, float *pv) {
+    static_assert(NT >= 64 && NT % 64 == 0 && NT <= 1024, "whole waves");
+    constexpr int P = 8;         // threads per candidate
+    constexpr int CPP = NT / P;  // candidates per pass
+    uint64_t *s_key = scratch, *s_cand = scratch + 256, *s_gm = scratch + 384, *s_t0 = scratch + 416;
+    int *s_cnt = (int *) (scratch + 417);  // candidates per wave (16 at most)
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    if (tid < kWave) {
+        float p[4];
+        if (gating == 0) {
+            float v[4], m = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = lane + 64 * j;
+                v[j] = e < n_expert ? lg[e] : -__builtin_inff();
+                m = fmaxf(m, v[j]);
+            }
+            m = lanes_max<64>(m);
+            float ev[4], s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ev[j] = lane + 64 * j < n_expert ? fns_expf(v[j] - m) : 0.0f;
+                s = s + ev[j];
+            }
+            s = lanes_sum<64>(s);
+            const float inv = 1.0f / s;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = ev[j] * inv;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = lane + 64 * j;
+                p[j] = e < n_expert ? 1.0f / (1.0f + fns_expf(-lg[e])) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            s_key[e] = e < n_expert ? ((uint64_t) __builtin_bit_cast(uint32_t, p[j]) << 32) | (uint32_t) ~e : 0ull;
+        }
+        if (lane == 0) *s_t0 = 0ull;  // kept when fewer than k groups are live: every live key is a candidate
+    }
+    __syncthreads();
+    if (tid < 32) {
+        uint64_t m = 0ull;
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const ulonglong2 kk = *(const ulonglong2 *) (s_key + 8 * tid + i);
+            m = kk.x > m ? kk.x : m;
+            m = kk.y > m ? kk.y : m;
+        }
+        s_gm[tid] = m;
+    }
+    __syncthreads();
+    if (tid < 32) {  // dead groups (maximum 0) tie with each other and all write 0
+        const uint64_t own = s_gm[tid];
+        int r = 0;
+#pragma unroll
+        for (int g = 0; g < 32; g += 2) {
+            const ulonglong2 kk = *(const ulonglong2 *) (s_gm + g);
+            r += kk.x > own ? 1 : 0;
+            r += kk.y > own ? 1 : 0;
+        }
+        if (r == k - 1) *s_t0 = own;
+    }
+    __syncthreads();
+    const uint64_t t0 = *s_t0;
+    // the candidates in expert order: one expert per thread, chunks of NT experts
+    int C = 0;
+    for (int e0 = 0; e0 < 256; e0 += NT) {
+        const int e = e0 + tid;
+        const uint64_t kt = e < 256 ? s_key[e] : 0ull;
+        const bool cand = kt != 0ull && kt >= t0;
+        const uint64_t b = __ballot(cand);
+        if (lane == 0) s_cnt[wave] = __popcll(b);
+        __syncthreads();
+        int base = C;
+        for (int w = 0; w < wave; ++w) base += s_cnt[w];
+        if (cand) s_cand[base + __popcll(b & ((1ull << lane) - 1ull))] = kt;
+        for (int w = 0; w < NT / kWave; ++w) C += s_cnt[w];
+        __syncthreads();
+    }
+    const int part = tid % P;
+    for (int c0 = 0; c0 < C; c0 += CPP) {
+        const int c = c0 + tid / P;
+        const uint64_t kc = c < C ? s_cand[c] : ~0ull;
+        int rank = 0;
+        for (int i = part; i < C; i += P) rank += s_cand[i] > kc ? 1 : 0;
+        rank = lanes_sum_i<P>(rank);
+        if (c < C && part == 0 && rank < k) {
+            sel[rank] = (int) ~(uint32_t) kc;
+            pv[rank] = __builtin_bit_cast(float, (uint32_t) (kc >> 32));
+        }
+    }
+    __syncthreads();
+}
+
+// All-pairs form (n_expert <= 128 in route_topk_block): gating + top-k + renormalisation for one token by a whole
+// workgroup of NT threads (n_expert <= 256). Wave 0
 // computes the probabilities exactly as route_topk_wave (same fp32 operations, so the same bits) and stores for
 // each expert the 64-bit key (bits(p) << 32) | ~e: p >= 0, so the keys order as (p descending, index ascending) and
 // are all distinct. Then eight threads per expert each count the keys above the expert's own over one eighth of the
@@ -95,7 +209,7 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ lg, in
 // index, without a dependent cross-lane chain. Must be called by every thread of the workgroup (it contains
 // barriers). Results: sel[0..k) and their probabilities pv[0..k) in LDS, visible to the whole workgroup on return.
 template <int NT>
-__device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, int n_expert, int k, int gating,
+__device__ __forceinline__ void route_topk_pairs(const float *__restrict__ lg, int n_expert, int k, int gating,
                                                  uint64_t *s_key, int *sel, float *pv) {
     constexpr int P = 8;         // threads per expert
     constexpr int EPP = NT / P;  // experts per pass
@@ -155,6 +269,15 @@ __device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, i
         }
     }
     __syncthreads();
+}
+
+// Gating + top-k + renormalisation for one token by a whole workgroup (n_expert <= 256): the all-pairs rank up to
+// 128 experts, the group-maximum filter beyond (4x the pairs at 256 experts); both give the same selection.
+template <int NT>
+__device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, int n_expert, int k, int gating,
+                                                 uint64_t *scratch, int *sel, float *pv) {
+    if (n_expert <= 128) route_topk_pairs<NT>(lg, n_expert, k, gating, scratch, sel, pv);
+    else route_topk_filter<NT>(lg, n_expert, k, gating, scratch, sel, pv);
 }
 
 // Combine weight of slot j (0 <= j < k < 16) from the selected probabilities pv[0..k): renormalised by their sum in

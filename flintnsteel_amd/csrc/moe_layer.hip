@@ -89,10 +89,19 @@ struct LayerArgs {
     int64_t xq_row_bytes;
     int fused;            // the shape fits the fused kernel (n_tok = 1)
     const float *sh;      // [T][H] shared-expert output added in the combine, or null
+    const float *norm_w;  // [H] RMSNorm weights, or null: the router kernel normalises x first
+    float norm_eps;
+    // the shared expert inside the fused decode kernel (gate, up [Fs][H] and down [H][Fs] blocks of the routed
+    // types; shd null: not fused)
+    const uint8_t *shg, *shu, *shd;
+    int Fs;
+    // dense mode of the gate/up and down kernels (the shared expert outside the fused kernel): one channel holding
+    // every token, gate and up at dense_gu + gate_off / + up_off, down at dense_down, weight 1, no guard
+    const uint8_t *dense_gu, *dense_down;
     // host side only: the caller's x (x above is then the RMSNorm output), the shared expert's buffers
     const float *x_in;
-    float *act_sh, *tmp_sh, *sh_out;
-    uint8_t *xq_sh;
+    float *act_sh, *tmp_sh, *sh_out, *amax_sh;
+    uint8_t *xq_sh, *apack_sh;
 };
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t) b << 16); }
@@ -120,16 +129,39 @@ __device__ void route_all(const LayerArgs &a);
 // quantise 1024 columns of one token row. Few, wide workgroups start faster than one small workgroup per row.
 constexpr int kK1Threads = 1024, kK1Rows = kK1Threads / 256;
 
+template <bool NORM>
 __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
     __shared__ float red[kK1Rows][4][kMaxTok];
+    __shared__ float s_nred[4], s_scale[kMaxTok], s_nq[kK1Rows][4][kMaxTok];
     const int H = a.H, T = a.T;
     const int n_router_wg = (a.NE + kK1Rows - 1) / kK1Rows;
     FNS_MARK(0, blockIdx.x, 0);
+    if (NORM && (int) blockIdx.x >= n_router_wg) {
+        // RMSNorm scale of each token row, by threads 0-255 in the order of the rms_norm_q8_1 kernel (same bits):
+        // the quantising workgroups then read h = (scale x) w where they would read x. (The router workgroups
+        // accumulate x^2 beside their dot products and scale the logit at the end: same value up to fp32 rounding,
+        // with no extra round trip before their loads.)
+        for (int t = 0; t < T; ++t) {
+            if (threadIdx.x < 256) {
+                const float *xr = a.x + (size_t) t * H;
+                float s = 0.0f;
+                for (int i = threadIdx.x; i < H; i += 256) s += xr[i] * xr[i];
+                s = lanes_sum<64>(s);
+                if (threadIdx.x % 64 == 0) s_nred[threadIdx.x / 64] = s;
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                const float s = (s_nred[0] + s_nred[1]) + (s_nred[2] + s_nred[3]);
+                s_scale[t] = 1.0f / sqrtf(s / H + a.norm_eps);
+            }
+            __syncthreads();
+        }
+    }
     if (blockIdx.x == 0 && threadIdx.x < kSyncLines) a.sync[threadIdx.x * kSyncStride] = 0;  // ordered before the next kernel
     if ((int) blockIdx.x < n_router_wg) {
         const int sub = threadIdx.x / 256, t256 = threadIdx.x % 256;
         const int r = blockIdx.x * kK1Rows + sub;
-        float s[kMaxTok] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float s[kMaxTok] = {0.0f, 0.0f, 0.0f, 0.0f}, ssq[kMaxTok] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (r < a.NE) {
             // four 16-byte pieces of the row per lane per pass, every load of a pass issued before the first use
             for (int i0 = t256; i0 < H / 4; i0 += 4 * 256) {
@@ -158,6 +190,11 @@ __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
                             const int i = i0 + 256 * u;
                             xv[u] = i < H / 4 ? ((const float4 *) (a.x + (size_t) t * H))[i]
                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                            if (NORM && i < H / 4) {  // x^2 for the scale; x w into the dot product
+                                const float4 nw = ((const float4 *) a.norm_w)[i];
+                                ssq[t] += xv[u].x * xv[u].x + xv[u].y * xv[u].y + xv[u].z * xv[u].z + xv[u].w * xv[u].w;
+                                xv[u] = make_float4(xv[u].x * nw.x, xv[u].y * nw.y, xv[u].z * nw.z, xv[u].w * nw.w);
+                            }
                         }
 #pragma unroll
                         for (int u = 0; u < 4; ++u)
@@ -171,11 +208,19 @@ __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
             if (t < T) {
                 const float v = lanes_sum<64>(s[t]);
                 if (t256 % 64 == 0) red[sub][t256 / 64][t] = v;
+                if (NORM) {
+                    const float q = lanes_sum<64>(ssq[t]);
+                    if (t256 % 64 == 0) s_nq[sub][t256 / 64][t] = q;
+                }
             }
         }
         __syncthreads();
         if (t256 < T && r < a.NE) {
-            const float lg = (red[sub][0][t256] + red[sub][1][t256]) + (red[sub][2][t256] + red[sub][3][t256]);
+            float lg = (red[sub][0][t256] + red[sub][1][t256]) + (red[sub][2][t256] + red[sub][3][t256]);
+            if (NORM) {
+                const float q = (s_nq[sub][0][t256] + s_nq[sub][1][t256]) + (s_nq[sub][2][t256] + s_nq[sub][3][t256]);
+                lg *= 1.0f / sqrtf(q / H + a.norm_eps);
+            }
             const float v = a.router_bias ? lg + a.router_bias[r] : lg;
             if (T > 1) __hip_atomic_store(a.logits + (size_t) t256 * a.NE + r, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             else a.logits[(size_t) t256 * a.NE + r] = v;
@@ -202,7 +247,8 @@ __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
     const int chunks = (npad + kK1Threads - 1) / kK1Threads;
     const int chunk = blockIdx.x - n_router_wg;
     const int t = chunk / chunks, i = (chunk % chunks) * kK1Threads + threadIdx.x;
-    const float v = i < H ? a.x[(size_t) t * H + i] : 0.0f;
+    float v = i < H ? a.x[(size_t) t * H + i] : 0.0f;
+    if (NORM && i < H) v = (s_scale[t] * v) * a.norm_w[i];
     const Q8Lane r = q8_1_lane(v);  // whole 32-lane blocks: the lanes past npad form whole blocks and store nothing
     if (i < npad) {
         uint8_t *b = a.xq + (size_t) t * a.xq_row_bytes + (size_t) (i / 32) * 36;
@@ -218,7 +264,7 @@ template <int NT, int LPR> constexpr int gu_rows_per_group() { return (NT / LPR)
 
 // LDS of the routing preamble.
 struct alignas(16) RouteLds {
-    uint64_t key[256];
+    uint64_t key[kTopkScratch];
     int ids[kMaxCh];
     float pv[16];
     int sel[16];
@@ -242,6 +288,15 @@ __device__ __forceinline__ int route_channel(const LayerArgs &a, RouteLds &rs) {
     const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
     const int T = a.T, K = a.K;
     const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
+    if (a.dense_gu) {  // dense mode: every token, in order
+        if (tid == 0) {
+            rs.e = 0;
+            rs.ncol = T;
+            for (int i = 0; i < kMaxTok; ++i) rs.xrow[i] = rs.orow[i] = i < T ? i : 0;
+        }
+        __syncthreads();
+        return 0;
+    }
     if (T == 1) {
         if (tid == 0) {
             rs.ncol = 1;
@@ -614,7 +669,7 @@ __global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
     const int nblk = H / 256;
     const int row_bytes = nblk * BB;
     const int rowb = blockIdx.x * kGuRows;
-    const uint8_t *slot = s_tab[e];
+    const uint8_t *slot = a.dense_gu ? a.dense_gu : s_tab[e];
     const uint8_t *wa = slot + a.up_off + (int64_t) rowb * row_bytes;
     const uint8_t *wb = slot + a.gate_off + (int64_t) rowb * row_bytes;
     const int region = kGuRows * row_bytes;  // a multiple of 16 (block sizes are even)
@@ -909,8 +964,9 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
     FNS_MARK(2, blockIdx.x, 0);
 
     if (tid < CH) {
-        s_dp[tid] = gload<const uint8_t *>((const uint8_t *) (a.dptr + tid)) + (int64_t) r0 * row_bytes;
-        s_w[tid] = a.w[tid];
+        const uint8_t *dp = a.dense_down ? a.dense_down : gload<const uint8_t *>((const uint8_t *) (a.dptr + tid));
+        s_dp[tid] = dp + (int64_t) r0 * row_bytes;
+        s_w[tid] = a.dense_down ? 1.0f : a.w[tid];
     }
     __syncthreads();
     FNS_MARK(2, blockIdx.x, 1);
@@ -992,7 +1048,7 @@ __device__ __forceinline__ void store_dev(uint32_t *p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int TGU, int TDN>
+template <int TGU, int TDN, bool SH>
 __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ RouteLds rs;
@@ -1008,14 +1064,21 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     const int nbg = H / 256, rbg = nbg * BG;
     const int nbd = F / 256, rbd = nbd * BD;
     const int upc = F / kGuRows;                          // producers per slot
-    const bool producer = (int) blockIdx.x < K * upc;
-    const int c = blockIdx.x / upc, u = blockIdx.x % upc;  // meaningful for producers
+    // the shared expert (when fused) is slot K: its producers follow the routed ones, its act image and down rows
+    // follow theirs, and its down output joins the combine with weight 1
+    const int Fs = SH ? a.Fs : 0, fspad = (Fs + 511) / 512 * 512, fsbytes = SH ? img_bytes(fspad) : 0;
+    const int nbd_s = Fs / 256, rbd_s = nbd_s * BD;
+    const int nprod = K * upc + Fs / kGuRows;
+    const bool producer = (int) blockIdx.x < nprod;
+    const bool shared_p = SH && producer && (int) blockIdx.x >= K * upc;
+    const int c = shared_p ? K : blockIdx.x / upc;
+    const int u = shared_p ? blockIdx.x - K * upc : blockIdx.x % upc;  // meaningful for producers
     const int r0 = blockIdx.x * kFusedRows;
-    const int gu_region = kGuRows * rbg, dn_region = kFusedRows * rbd;  // multiples of 16
+    const int gu_region = kGuRows * rbg, dn_region = kFusedRows * rbd, dn_region_s = kFusedRows * rbd_s;
     uint8_t *s_x = smem;
-    uint8_t *s_a = s_x + xbytes;         // [K] act images
-    uint8_t *s_gu = s_a + K * fbytes;    // [32 up rows | 32 gate rows]
-    uint8_t *s_dn = s_gu + 2 * gu_region;  // [K][8 down rows]
+    uint8_t *s_a = s_x + xbytes;         // [K] act images, then the shared expert's
+    uint8_t *s_gu = s_a + K * fbytes + fsbytes;  // [32 up rows | 32 gate rows]
+    uint8_t *s_dn = s_gu + 2 * gu_region;  // [K][8 down rows], then the shared expert's 8 rows
     FNS_MARK(1, blockIdx.x, 0);
 
     // 1. waves 1-15: x image and expert table; wave 0: logits. Routing (all selected slots are needed here).
@@ -1037,11 +1100,12 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     FNS_MARK(1, blockIdx.x, 1);
 
     // 2. weights: each wave its two gate/up rows (producers), then its share of the down rows
-    const uint8_t *slot = s_tab[rs.sel[producer ? c : 0]];
-    const uint8_t *wa = slot + a.up_off + (int64_t) (u * kGuRows) * rbg;
-    const uint8_t *wb = slot + a.gate_off + (int64_t) (u * kGuRows) * rbg;
+    const uint8_t *slot = s_tab[rs.sel[producer && !shared_p ? c : 0]];
+    const uint8_t *wa = (shared_p ? a.shu : slot + a.up_off) + (int64_t) (u * kGuRows) * rbg;
+    const uint8_t *wb = (shared_p ? a.shg : slot + a.gate_off) + (int64_t) (u * kGuRows) * rbg;
     uintptr_t mis = producer ? ((uintptr_t) wa | (uintptr_t) wb) : 0;
     for (int j = 0; j < K; ++j) mis |= (uintptr_t) (s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd);
+    if (SH) mis |= (uintptr_t) (a.shd + (int64_t) r0 * rbd_s);
     const bool staged = (mis & 15u) == 0;
     // down: wave w takes pieces [w * dn_piece, (w + 1) * dn_piece) of the flattened [K][dn_region] image
     auto dma_down = [&]() {
@@ -1050,6 +1114,11 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         for (int j = p_lo / dn_region; j < K && j * dn_region < p_hi; ++j) {
             const int lo = max(p_lo - j * dn_region, 0), hi = min(p_hi - j * dn_region, dn_region);
             dma_wave(s_dn + j * dn_region, s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd, lo, hi);
+        }
+        if (SH) {  // the shared expert's rows, split over the waves the same way
+            const int sp = ((dn_region_s + kQWaves * 16 - 1) / (kQWaves * 16)) * 16;
+            dma_wave(s_dn + K * dn_region, a.shd + (int64_t) r0 * rbd_s, min(wave * sp, dn_region_s),
+                     min((wave + 1) * sp, dn_region_s));
         }
     };
     // Producers fetch their gate/up rows first and their down rows only once those are consumed: the gate/up bytes,
@@ -1096,10 +1165,12 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
             const int i = u * kGuRows + lane64 % 32;
             const Q8Lane r = q8_1_lane(lane64 < 32 ? s_act[lane64] : 0.0f);
             if (lane64 < 32) {
-                store_dev(a.act + (size_t) c * F + i, s_act[lane64]);
+                // (the shared expert's image follows the routed ones; it has no f32 act or guard)
+                const int ip = shared_p ? fspad : fpad;
+                if (!shared_p) store_dev(a.act + (size_t) c * F + i, s_act[lane64]);
                 uint8_t *img_g = a.apack + (size_t) c * fbytes;
                 const float dh = half_to_float(float_to_half(r.d));
-                float *dg = (float *) (img_g + img_q_bytes(fpad));
+                float *dg = (float *) (img_g + img_q_bytes(ip));
                 // q: 32 bytes = 8 dwords; lane 4j stores dword j, gathered from lanes 4j .. 4j+3
                 const uint32_t qb = (uint32_t) (uint8_t) (int8_t) r.q;
                 uint32_t word = 0;
@@ -1108,10 +1179,10 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
                 if ((lane64 & 3) == 0) store_dev((uint32_t *) (img_g + img_q_index(i)), word);
                 if (lane64 == 0) {
                     store_dev(dg + i / 32, dh);
-                    store_dev(dg + fpad / 32 + fpad / 16 + i / 32, dh * (float) r.qsum32);
-                    store_dev(a.blk_amax + (size_t) c * (fpad / 32) + i / 32, r.amax);
+                    store_dev(dg + ip / 32 + ip / 16 + i / 32, dh * (float) r.qsum32);
+                    if (!shared_p) store_dev(a.blk_amax + (size_t) c * (fpad / 32) + i / 32, r.amax);
                 }
-                if (lane64 % 16 == 0) store_dev(dg + fpad / 32 + i / 16, dh * (float) r.qsum16);
+                if (lane64 % 16 == 0) store_dev(dg + ip / 32 + i / 16, dh * (float) r.qsum16);
             }
         }
         FNS_MARK(1, blockIdx.x, 7);
@@ -1119,7 +1190,6 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     if (producer && wave == 0) dma_wait();  // the act stores have completed
     FNS_MARK(1, blockIdx.x, 3);
     // 4. arrival (producers) and wait (everyone; bounded: a timeout poisons this workgroup's outputs with NaN)
-    const int nprod = K * upc;
     if (tid == 0) {
         int *sy = a.sync;
         if (producer) {
@@ -1152,8 +1222,9 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     FNS_MARK(1, blockIdx.x, 8);
     // 5. act images (device-scope LDS-DMA) and the F16 guard: a slot whose scale is not 1 is divided and re-quantised
     //    (reference src/kernels.cu:554-577)
-    for (int p = wave * 1024; p < K * fbytes; p += kQThreads * 16)
-        if (p + lane64 * 16 < K * fbytes)
+    const int abytes = K * fbytes + fsbytes;
+    for (int p = wave * 1024; p < abytes; p += kQThreads * 16)
+        if (p + lane64 * 16 < abytes)
             __builtin_amdgcn_global_load_lds(
                 (const __attribute__((address_space(1))) void *) (a.apack + p + lane64 * 16),
                 (__attribute__((address_space(3))) void *) (s_a + p), 16, 0, kCpolDevice);
@@ -1191,14 +1262,16 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     FNS_MARK(1, blockIdx.x, 10);
     // 6. down rows (16 lanes per (row, slot) item, as k_down_q), then the combine in slot order
     const int lane16 = tid % 16;
-    for (int it = tid / 16; it < kFusedRows * K; it += kQThreads / 16) {
+    for (int it = tid / 16; it < kFusedRows * (K + (SH ? 1 : 0)); it += kQThreads / 16) {
         const int ch = it / kFusedRows, rr = it % kFusedRows;
-        const ActImg img = act_img(s_a + ch * fbytes, fpad);
-        const uint8_t *gsrc = s_tab[rs.sel[ch]] + a.down_off + (int64_t) (r0 + rr) * rbd;
+        const bool shc = SH && ch == K;  // the shared expert's rows
+        const ActImg img = act_img(s_a + ch * fbytes, shc ? fspad : fpad);
+        const int nb_c = shc ? nbd_s : nbd, rb_c = shc ? rbd_s : rbd;
+        const uint8_t *gsrc = (shc ? a.shd : s_tab[rs.sel[ch]] + a.down_off) + (int64_t) (r0 + rr) * rb_c;
         float acc = 0.0f;
-        for (int qi = lane16; qi < 4 * nbd; qi += 16) {
+        for (int qi = lane16; qi < 4 * nb_c; qi += 16) {
             const int bb = qi >> 2, qt = qi & 3;
-            if (staged) acc += quarter_dot<TDN, Aligned16>(s_dn + ch * dn_region + rr * rbd + bb * BD, img, bb, qt);
+            if (staged) acc += quarter_dot<TDN, Aligned16>(s_dn + ch * dn_region + rr * rb_c + bb * BD, img, bb, qt);
             else acc += quarter_dot<TDN, Any2>(gsrc + bb * BD, img, bb, qt);
         }
         acc = lanes_sum<16>(acc);
@@ -1211,7 +1284,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         const int r = r0 + tid;
         float moe = (s_dexp[0][tid] * s_e[0]) * s_w[0];
         for (int j = 1; j < K; ++j) moe = moe + (s_dexp[j][tid] * s_e[j]) * s_w[j];
-        moe = moe + s_sh[tid];
+        moe = moe + (SH ? s_dexp[K][tid] : s_sh[tid]);
         float o = a.x_resid ? moe + s_res[tid] : moe;
         if (s_fail) o = __builtin_nanf("");
         a.out[r] = o;
@@ -1220,11 +1293,14 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
 }
 
 // Fused-kernel plan for one layer shape (n_tok = 1): LDS bytes, or 0 when the shape does not fit the scheme.
-inline size_t fused_lds(int H, int F, int K, int BG, int BD) {
-    if (F % kGuRows || (int64_t) K * (F / kGuRows) > H / kFusedRows) return 0;  // every producer is a workgroup
-    if (K > 16) return 0;
-    const size_t lds = (size_t) img_bytes((int) host::pad512(H)) + (size_t) K * img_bytes((int) host::pad512(F)) +
-                       2 * (size_t) kGuRows * (H / 256) * BG + (size_t) K * kFusedRows * (F / 256) * BD + 48;
+// Fs > 0: with the shared expert (width Fs, the routed types) as slot K.
+inline size_t fused_lds(int H, int F, int K, int BG, int BD, int Fs = 0) {
+    // every producer is a workgroup
+    if (F % kGuRows || (int64_t) K * (F / kGuRows) + Fs / kGuRows > H / kFusedRows) return 0;
+    if (K + (Fs > 0 ? 1 : 0) > 16) return 0;
+    size_t lds = (size_t) img_bytes((int) host::pad512(H)) + (size_t) K * img_bytes((int) host::pad512(F)) +
+                 2 * (size_t) kGuRows * (H / 256) * BG + (size_t) K * kFusedRows * (F / 256) * BD + 48;
+    if (Fs > 0) lds += (size_t) img_bytes((int) host::pad512(Fs)) + (size_t) kFusedRows * (Fs / 256) * BD;
     return lds <= kLdsBudget ? lds : 0;
 }
 
@@ -1363,23 +1439,26 @@ template <int TQ> int dispatch_down(const LayerArgs &a, hipStream_t st) {
 
 // The fused kernel runs only when every workgroup can be resident at once (it waits on other workgroups): the
 // occupancy of each (gate/up type, down type, LDS size) is queried once per device and cached.
-template <int TGU, int TDN> const void *fused_fn() { return (const void *) k_layer_fused<TGU, TDN>; }
+// (sh: the instantiation with the shared expert as slot K)
+template <int TGU, int TDN> const void *fused_fn(bool sh) {
+    return sh ? (const void *) k_layer_fused<TGU, TDN, true> : (const void *) k_layer_fused<TGU, TDN, false>;
+}
 
-template <int TGU> const void *fused_fn_by_down(int tdn) {
+template <int TGU> const void *fused_fn_by_down(int tdn, bool sh) {
     switch (tdn) {
-        case T_Q3_K: return fused_fn<TGU, T_Q3_K>();
-        case T_Q4_K: return fused_fn<TGU, T_Q4_K>();
-        case T_Q5_K: return fused_fn<TGU, T_Q5_K>();
-        case T_Q6_K: return fused_fn<TGU, T_Q6_K>();
+        case T_Q3_K: return fused_fn<TGU, T_Q3_K>(sh);
+        case T_Q4_K: return fused_fn<TGU, T_Q4_K>(sh);
+        case T_Q5_K: return fused_fn<TGU, T_Q5_K>(sh);
+        case T_Q6_K: return fused_fn<TGU, T_Q6_K>(sh);
     }
     return nullptr;
 }
-const void *fused_kernel(int tgu, int tdn) {
+const void *fused_kernel(int tgu, int tdn, bool sh) {
     switch (tgu) {
-        case T_Q3_K: return fused_fn_by_down<T_Q3_K>(tdn);
-        case T_Q4_K: return fused_fn_by_down<T_Q4_K>(tdn);
-        case T_Q5_K: return fused_fn_by_down<T_Q5_K>(tdn);
-        case T_Q6_K: return fused_fn_by_down<T_Q6_K>(tdn);
+        case T_Q3_K: return fused_fn_by_down<T_Q3_K>(tdn, sh);
+        case T_Q4_K: return fused_fn_by_down<T_Q4_K>(tdn, sh);
+        case T_Q5_K: return fused_fn_by_down<T_Q5_K>(tdn, sh);
+        case T_Q6_K: return fused_fn_by_down<T_Q6_K>(tdn, sh);
     }
     return nullptr;
 }
@@ -1410,16 +1489,17 @@ int resident_groups(const void *fn, size_t lds) {
 // True when this call (n_tok = 1, a shape that fits) takes the fused kernel.
 bool use_fused(const FnsMoeLayer *L, const LayerArgs &a) {
     if (!a.fused) return false;
-    const size_t lds = fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type));
-    const void *fn = fused_kernel(L->gu_type, L->down_type);
+    const size_t lds = fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type), a.shd ? a.Fs : 0);
+    const void *fn = fused_kernel(L->gu_type, L->down_type, a.shd != nullptr);
     return fn && resident_groups(fn, lds) >= a.H / kFusedRows;
 }
 
 int launch_fused(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t st) {
-    const size_t lds = fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type));
+    const size_t lds = fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type), a.shd ? a.Fs : 0);
     LayerArgs arg = a;
     void *args[] = {&arg};
-    const hipError_t e = hipLaunchKernel(fused_kernel(L->gu_type, L->down_type), dim3((unsigned) (a.H / kFusedRows)),
+    const hipError_t e = hipLaunchKernel(fused_kernel(L->gu_type, L->down_type, a.shd != nullptr),
+                                         dim3((unsigned) (a.H / kFusedRows)),
                                          dim3(kQThreads), args, lds, st);
     if (e != hipSuccess) return host::set_error(host::ERR_LAUNCH, "moe fused layer: %s", hipGetErrorString(e));
     return host::check_launch("moe fused layer");
@@ -1446,11 +1526,12 @@ int by_type_down(int t, const LayerArgs &a, hipStream_t st) {
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
-constexpr int kSections = 17;
+constexpr int kSections = 19;
 
 // Byte sizes of the workspace sections: 0 logits, 1 xq, 2 ids, 3 w, 4 act, 5 escale (documented in fns_hip.h),
 // then internal: 6 xpack, 7 apack, 8 blk_amax, 9 dptr, 10 sync, 11 channel table + arrival count (n_tok > 1),
-// 12 RMSNorm output h, 13 shared-expert act, 14 its gate (n_tok > 1), 15 Q8_1 of its act, 16 its output sh.
+// 12 (unused), 13 shared-expert act, 14 its gate (n_tok > 1), 15 Q8_1 of its act, 16 its output sh,
+// 17 its act images, 18 their block maxima (the dense-mode kernels).
 void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     const size_t hpad = (size_t) host::pad512(L->hidden), fpad = (size_t) host::pad512(L->inter);
     const size_t ch = (size_t) n_tok * L->k;
@@ -1461,17 +1542,19 @@ void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     sizes[4] = ch * L->inter * 4;
     sizes[5] = ch * 4;
     sizes[6] = (size_t) n_tok * img_bytes((int) hpad);
-    sizes[7] = ch * img_bytes((int) fpad);
+    sizes[7] = ch * img_bytes((int) fpad) + (L->shexp_inter > 0 ? img_bytes((int) host::pad512(L->shexp_inter)) : 0);
     sizes[8] = ch * (fpad / 32) * 4;
     sizes[9] = ch * 8;
     sizes[10] = (size_t) kSyncLines * kSyncStride * 4;
     sizes[11] = (size_t) (kMaxCh * kChanInts + 2) * 4;
     const size_t fs = L->shexp_inter > 0 ? (size_t) L->shexp_inter : 0;
-    sizes[12] = L->ffn_norm ? (size_t) n_tok * L->hidden * 4 : 0;
+    sizes[12] = 0;  // (unused: the router kernel applies the RMSNorm)
     sizes[13] = (size_t) n_tok * fs * 4;
     sizes[14] = n_tok > 1 ? (size_t) n_tok * fs * 4 : 0;
     sizes[15] = fs ? (size_t) n_tok * host::q8_1_row_bytes((int64_t) fs) : 0;
     sizes[16] = fs ? (size_t) n_tok * L->hidden * 4 : 0;
+    sizes[17] = fs ? (size_t) n_tok * img_bytes((int) host::pad512((int64_t) fs)) : 0;
+    sizes[18] = fs ? (size_t) n_tok * (host::pad512((int64_t) fs) / 32) * 4 : 0;
 }
 
 }  // namespace
@@ -1562,15 +1645,34 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     a.sync = (int *) sec[10];
     a.chan = (int *) sec[11];
     a.xq_row_bytes = host::q8_1_row_bytes(L->hidden);
-    a.fused = n_tok == 1 && fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type)) > 0;
+    // the shared expert rides in the fused kernel when it has the routed types and the shape still fits
+    const bool sh_same = L->shexp_inter > 0 && (!L->shexp_gu_type || L->shexp_gu_type == L->gu_type) &&
+                         (!L->shexp_down_type || L->shexp_down_type == L->down_type);
+    const int fs_fused = n_tok == 1 && sh_same &&
+                                 fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type),
+                                           L->shexp_inter) > 0
+                             ? L->shexp_inter
+                             : 0;
+    a.fused = n_tok == 1 && fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type),
+                                      L->shexp_inter > 0 ? fs_fused : 0) > 0 &&
+              (L->shexp_inter == 0 || fs_fused > 0);
     a.x_in = x;
-    if (L->ffn_norm) a.x = (const float *) sec[12];  // the router and the experts read h = RMSNorm(x)
+    a.norm_w = L->ffn_norm;  // the router kernel reads h = RMSNorm(x) in place of x
+    a.norm_eps = L->norm_eps;
     if (L->shexp_inter > 0) {
         a.act_sh = (float *) sec[13];
         a.tmp_sh = (float *) sec[14];
         a.xq_sh = sec[15];
         a.sh_out = (float *) sec[16];
+        a.apack_sh = sec[17];
+        a.amax_sh = (float *) sec[18];
         a.sh = a.sh_out;
+        if (a.fused) {  // candidate for the fused kernel; launch_stage falls back when it cannot be resident
+            a.shg = (const uint8_t *) L->shexp_gate;
+            a.shu = (const uint8_t *) L->shexp_up;
+            a.shd = (const uint8_t *) L->shexp_down;
+            a.Fs = L->shexp_inter;
+        }
     }
     return host::OK;
 }
@@ -1581,6 +1683,29 @@ static int launch_shared(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t s
     const int gt = L->shexp_gu_type ? L->shexp_gu_type : L->gu_type;
     const int dt = L->shexp_down_type ? L->shexp_down_type : L->down_type;
     const int64_t H = a.H, Fs = L->shexp_inter;
+    if (gate_up_q_fits(a.H, block_bytes(gt)) && down_q_fits((int) Fs, block_bytes(dt))) {
+        // The quarter kernels of the routed experts in dense mode: per (row, token) the arithmetic of the fused
+        // kernel's shared expert, so a verify column equals its batch-1 result bit for bit.
+        LayerArgs s = a;
+        s.F = (int) Fs;
+        s.K = 1;
+        s.NE = 1;
+        s.guard = 0;
+        s.gate_off = 0;
+        s.up_off = (const uint8_t *) L->shexp_up - (const uint8_t *) L->shexp_gate;
+        s.dense_gu = (const uint8_t *) L->shexp_gate;
+        s.dense_down = (const uint8_t *) L->shexp_down;
+        s.act = a.act_sh;
+        s.apack = a.apack_sh;
+        s.blk_amax = a.amax_sh;
+        s.out = a.sh_out;
+        s.x_resid = nullptr;
+        s.sh = nullptr;
+        s.fused = 0;
+        s.shd = nullptr;
+        FNS_TRY(by_type_gate_up(gt, s, st));
+        return by_type_down(dt, s, st);
+    }
     if (a.T == 1) {
         FNS_TRY(mmvq_swiglu(gt, L->shexp_gate, L->shexp_up, H, Fs, a.xq, a.act_sh, st));
     } else {
@@ -1593,14 +1718,18 @@ static int launch_shared(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t s
 }
 
 static int launch_stage(const FnsMoeLayer *L, const LayerArgs &a, int stage, hipStream_t st) {
-    if (stage == 0) {  // [RMSNorm], router + Q8_1 of x, [shared expert]
-        if (L->ffn_norm)
-            FNS_TRY(rms_norm_q8_1(a.x_in, L->ffn_norm, (float *) a.x, a.xq, a.H, L->norm_eps, a.T, st));
+    if (stage == 0) {  // [RMSNorm +] router + Q8_1 of x, [shared expert]
         const int chunks = (int) ((host::pad512(L->hidden) + kK1Threads - 1) / kK1Threads);
         const int n_router_wg = (L->n_expert + kK1Rows - 1) / kK1Rows;
-        hipLaunchKernelGGL(k_route_quant, dim3((unsigned) (n_router_wg + chunks * a.T)), dim3(kK1Threads), 0, st, a);
+        if (a.norm_w)
+            hipLaunchKernelGGL(k_route_quant<true>, dim3((unsigned) (n_router_wg + chunks * a.T)), dim3(kK1Threads), 0,
+                               st, a);
+        else
+            hipLaunchKernelGGL(k_route_quant<false>, dim3((unsigned) (n_router_wg + chunks * a.T)), dim3(kK1Threads), 0,
+                               st, a);
         FNS_TRY(host::check_launch("moe route_quant"));
-        return L->shexp_inter > 0 ? launch_shared(L, a, st) : host::OK;
+        // (the shared expert runs inside the fused kernel when that takes the call)
+        return L->shexp_inter > 0 && !(a.shd && use_fused(L, a)) ? launch_shared(L, a, st) : host::OK;
     }
     // n_tok = 1 shapes that fit take the fused kernel as stage 1; stage 2 then has nothing left to do
     if (stage == 1) return use_fused(L, a) ? launch_fused(L, a, st) : by_type_gate_up(L->gu_type, a, st);

@@ -154,7 +154,7 @@ constexpr int kRouteThreads = 256;
 __global__ __launch_bounds__(kRouteThreads) void k_route_topk(const float *__restrict__ logits, int32_t *__restrict__ ids,
                                                               float *__restrict__ w, int n_expert, int k, int gating,
                                                               int norm) {
-    __shared__ __align__(16) uint64_t s_key[256];
+    __shared__ __align__(16) uint64_t s_key[kTopkScratch];
     __shared__ int s_sel[16];
     __shared__ float s_pv[16];
     const int t = blockIdx.x;

@@ -52,7 +52,8 @@ def mv(qtype, m, ncols, nrows, xq_row):
     return orc.mmvq_experts(qtype, [m], ncols, nrows, xq_row[None], 1, 1, np.zeros(1, np.int32))[0]
 
 
-def block_ref(mats, h: np.ndarray, ids: np.ndarray, w: np.ndarray, resid: np.ndarray) -> np.ndarray:
+def block_ref(mats, h: np.ndarray, ids: np.ndarray, w: np.ndarray, resid: np.ndarray, sgu: int = GU,
+              sdn: int = DN) -> np.ndarray:
     """float64 chain of the whole block for given h and routing (each act re-quantised from its own fp32 value)."""
     slots, sh = mats
     xq = orc.quantize_q8_1(h)
@@ -66,8 +67,8 @@ def block_ref(mats, h: np.ndarray, ids: np.ndarray, w: np.ndarray, resid: np.nda
             esc = orc.amax_guard_scale(act)
             aq = orc.quantize_q8_1((act / np.float32(esc)).astype(np.float32)[None])[0]
             out[t] += mv(DN, slots["down"][e].reshape(H, -1), F, H, aq) * esc * float(w[t, j])
-        act_sh = orc.swiglu(mv(GU, sh["gate"], H, FS, xq[t]), mv(GU, sh["up"], H, FS, xq[t])).astype(np.float32)
-        out[t] += mv(DN, sh["down"], FS, H, orc.quantize_q8_1(act_sh[None])[0])
+        act_sh = orc.swiglu(mv(sgu, sh["gate"], H, FS, xq[t]), mv(sgu, sh["up"], H, FS, xq[t])).astype(np.float32)
+        out[t] += mv(sdn, sh["down"], FS, H, orc.quantize_q8_1(act_sh[None])[0])
     return out + resid
 
 
@@ -138,3 +139,32 @@ def test_flint_block_prefill(ops, layer, mats):
     toks = [0, 1, 33, 64, 69]
     ref = block_ref(mats, h[toks], ids[toks], w[toks], host(x)[toks])
     assert_close(out[toks], ref, "flint block prefill", 1e-3, 1e-4)
+
+
+def test_flint_block_shared_types_differ(ops, layer, mats):
+    """A shared expert whose types differ from the routed ones (Q6_K gate/up, Q4_K down) is not fused into the decode
+    kernel: the dense-mode gate/up and down kernels compute it, at one token and at four."""
+    from flintnsteel_amd import synth
+    sgu, sdn = orc.Q6_K, orc.Q4_K
+    seed = synth.tensor_seed(SEED, 22, synth.KIND_SHEXP)
+    g = torch.empty(1, ops.row_bytes(sgu, H) * FS, dtype=torch.uint8, device="cuda")
+    u = torch.empty_like(g)
+    d = torch.empty(1, ops.row_bytes(sdn, FS) * H, dtype=torch.uint8, device="cuda")
+    synth.quantized_matrices(sgu, 1, FS, H, seed, 0.02, g)
+    synth.quantized_matrices(sgu, 1, FS, H, seed + 1, 0.02, u)
+    synth.quantized_matrices(sdn, 1, H, FS, seed + 2, 0.02, d)
+    shexp = {"gate": g, "up": u, "down": d, "inter": FS, "gu_type": sgu, "down_type": sdn}
+    lay2 = ops.MoeLayer(layer.router_w, layer.slots, GU, DN, H, F, K, gating=ops.GATING_SIGMOID, guard=True,
+                        ffn_norm=layer.ffn_norm, norm_eps=1e-6, shexp=shexp)
+    sh_np = {"gate": host(g).reshape(FS, -1), "up": host(u).reshape(FS, -1), "down": host(d).reshape(H, -1)}
+    x4 = synth.activations(4, H, SEED, layer=35)
+    out4 = host(lay2(x4, ws=lay2.workspace(4), x_resid=x4))
+    for t in range(4):
+        xt = x4[t:t + 1].contiguous()
+        ws1 = lay2.workspace(1)
+        out1 = host(lay2(xt, ws=ws1, x_resid=xt))
+        assert np.array_equal(out4[t], out1[0]), f"column {t}"
+        tr = {k: host(v) for k, v in lay2.trace(ws1, 1).items()}
+        h, ids, w = check_front(ops, lay2, xt, tr["logits"], tr["xq"], bf16_x=False)
+        ref = block_ref((mats[0], sh_np), h, ids, w, host(xt), sgu, sdn)
+        assert_close(out1, ref, f"flint block, shared {orc.TYPE_NAMES[sgu]}/{orc.TYPE_NAMES[sdn]}", 1e-3, 1e-4)
