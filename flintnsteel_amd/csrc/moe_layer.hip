@@ -652,7 +652,6 @@ __global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
     const int T = a.T, H = a.H;
     const int npad = (H + 511) / 512 * 512;
     const int xbytes = img_bytes(npad);
-    uint8_t *s_w = s_x + T * xbytes;  // [32 up rows | 32 gate rows]
     const int wgid = blockIdx.y * gridDim.x + blockIdx.x;
     FNS_MARK(1, wgid, 0);
 
@@ -672,14 +671,10 @@ __global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
     const uint8_t *slot = a.dense_gu ? a.dense_gu : s_tab[e];
     const uint8_t *wa = slot + a.up_off + (int64_t) rowb * row_bytes;
     const uint8_t *wb = slot + a.gate_off + (int64_t) rowb * row_bytes;
-    const int region = kGuRows * row_bytes;  // a multiple of 16 (block sizes are even)
-    const bool staged = (((uintptr_t) wa | (uintptr_t) wb) & 15u) == 0;
+    // weights straight from global memory (each lane reads its own quarters; staging them through LDS cost an LDS
+    // footprint of 74 KB and a DMA wait per workgroup), with 16-byte loads when the blocks are 16-byte aligned
+    const bool al16 = (((uintptr_t) wa | (uintptr_t) wb | (uintptr_t) BB) & 15u) == 0;
     const int r2 = 2 * wave;  // this wave's rows r2, r2 + 1
-    if (staged) {
-        dma_wave(s_w, wa, r2 * row_bytes, (r2 + 2) * row_bytes);
-        dma_wave(s_w + region, wb, r2 * row_bytes, (r2 + 2) * row_bytes);
-    }
-    dma_wait();
     FNS_MARK(1, wgid, 2);
 
     const int lane = tid % 32;
@@ -693,9 +688,9 @@ __global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
     for (int qi = lane; qi < 4 * nblk; qi += 32) {
         const int bb = qi >> 2, qt = qi & 3;
         const int off = rl * row_bytes + bb * BB;
-        if (staged) {
-            quarter_dot_nc<TQ, Aligned16, NC>(s_w + off, img, ncol, bb, qt, acc);
-            quarter_dot_nc<TQ, Aligned16, NC>(s_w + region + off, img, ncol, bb, qt, accg);
+        if (al16) {
+            quarter_dot_nc<TQ, Aligned16, NC>(wa + off, img, ncol, bb, qt, acc);
+            quarter_dot_nc<TQ, Aligned16, NC>(wb + off, img, ncol, bb, qt, accg);
         } else {
             quarter_dot_nc<TQ, Any2, NC>(wa + off, img, ncol, bb, qt, acc);
             quarter_dot_nc<TQ, Any2, NC>(wb + off, img, ncol, bb, qt, accg);
@@ -1313,9 +1308,8 @@ inline size_t gate_up_lds_bytes(int T, int H, int BB, int NC) {
 // Quarter forms: sized for kMaxTok tokens whatever the call's n_tok, so a verify call and a decode call of the same
 // layer take the same kernels (and so the same arithmetic).
 inline size_t gate_up_q_lds_bytes(int T, int H, int BB, int NC) {
-    const size_t b = (size_t) NC * kGuRows * 4 + (size_t) T * img_bytes((int) host::pad512(H)) +
-                     2 * (size_t) kGuRows * (H / 256) * BB + 16;
-    return b;
+    (void) BB;
+    return (size_t) NC * kGuRows * 4 + (size_t) T * img_bytes((int) host::pad512(H)) + 16;
 }
 inline bool gate_up_q_fits(int H, int BB) { return gate_up_q_lds_bytes(kMaxTok, H, BB, kMaxTok) <= kLdsBudget; }
 inline size_t down_q_lds_bytes(int F, int BB) {
