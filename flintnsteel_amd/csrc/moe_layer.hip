@@ -941,6 +941,8 @@ __global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
 // rows into a private LDS area, waits only for its own copies and computes its four rows with 16 lanes per row.
 template <int TQ>
 __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
+    // the act images of every (token, slot) channel, staged once by the whole workgroup; the down weights are read
+    // by each lane straight from global memory
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float s_e[kMaxCh], s_w[kMaxCh];
     __shared__ float s_dexp[kMaxCh][kDownRows];
@@ -954,30 +956,19 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
     const int r0 = blockIdx.x * kDownRows;  // hidden is a multiple of 256: all 8 rows exist
     const int nblk = F / 256;
     const int row_bytes = nblk * BB;
-    const int wbuf = fbytes + 4 * row_bytes + 48;  // image | four rows (+ rounding to 16 bytes, + over-read)
-    uint8_t *priv = smem + wave * ((wbuf + 15) & ~15);
     FNS_MARK(2, blockIdx.x, 0);
 
+    dma_waves_from<kQWaves>(smem, a.apack, CH * fbytes, 0);
     if (tid < CH) {
         const uint8_t *dp = a.dense_down ? a.dense_down : gload<const uint8_t *>((const uint8_t *) (a.dptr + tid));
         s_dp[tid] = dp + (int64_t) r0 * row_bytes;
         s_w[tid] = a.dense_down ? 1.0f : a.w[tid];
     }
+    dma_wait();
     __syncthreads();
     FNS_MARK(2, blockIdx.x, 1);
-    uintptr_t mis = 0;
-    for (int c = 0; c < CH; ++c) mis |= (uintptr_t) s_dp[c];
-    const bool staged = (mis & 15u) == 0;
-    const int sub = lane64 / 16, lane = tid % 16;
-    for (int g = wave; g < 2 * CH; g += kQWaves) {
-        const int ch = g >> 1, rb = 4 * (g & 1);  // rows rb .. rb + 3 of the workgroup's eight
-        if (g != wave) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): earlier reads of the area are done
-        dma_wave(priv, a.apack + (size_t) ch * fbytes, 0, fbytes);
-        const int beg = rb * row_bytes, gs = beg & ~15;
-        if (staged) dma_wave(priv + fbytes - gs, s_dp[ch], beg, beg + 4 * row_bytes);
-        dma_wait();
-        if (g == wave) FNS_MARK(2, blockIdx.x, 2);
-        // F16 guard: a row whose scale is not 1 is divided and re-quantised (reference src/kernels.cu:554-577)
+    // F16 guard: a channel whose scale is not 1 is divided and re-quantised (reference src/kernels.cu:554-577)
+    for (int ch = wave; ch < CH; ch += kQWaves) {
         float esc = 1.0f;
         if (a.guard) {
             float m = 0.0f;
@@ -989,7 +980,7 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
                 for (int i0 = 0; i0 < fpad; i0 += kWave) {
                     const int i = i0 + lane64;
                     const Q8Lane r = q8_1_lane(i < F ? src[i] / esc : 0.0f);
-                    pack_store(priv, fpad, i, r);
+                    pack_store(smem + (size_t) ch * fbytes, fpad, i, r);
                 }
             }
         }
@@ -997,13 +988,22 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
             s_e[ch] = esc;
             if (blockIdx.x == 0) a.escale[ch] = esc;
         }
-        const ActImg img = act_img(priv, fpad);
+    }
+    __syncthreads();
+    uintptr_t mis = (uintptr_t) BB;
+    for (int c = 0; c < CH; ++c) mis |= (uintptr_t) s_dp[c];
+    const bool al16 = (mis & 15u) == 0;
+    const int sub = lane64 / 16, lane = tid % 16;
+    for (int g = wave; g < 2 * CH; g += kQWaves) {
+        const int ch = g >> 1, rb = 4 * (g & 1);  // rows rb .. rb + 3 of the workgroup's eight
+        const ActImg img = act_img(smem + (size_t) ch * fbytes, fpad);
         const int rr = rb + sub;
+        const uint8_t *wr = s_dp[ch] + rr * row_bytes;
         float acc = 0.0f;
         for (int qi = lane; qi < 4 * nblk; qi += 16) {
             const int bb = qi >> 2, qt = qi & 3;
-            if (staged) acc += quarter_dot<TQ, Aligned16>(priv + fbytes - gs + rr * row_bytes + bb * BB, img, bb, qt);
-            else acc += quarter_dot<TQ, Any2>(s_dp[ch] + rr * row_bytes + bb * BB, img, bb, qt);
+            if (al16) acc += quarter_dot<TQ, Aligned16>(wr + bb * BB, img, bb, qt);
+            else acc += quarter_dot<TQ, Any2>(wr + bb * BB, img, bb, qt);
         }
         acc = lanes_sum<16>(acc);
         if (lane == 0) s_dexp[ch][rr] = acc;
@@ -1312,11 +1312,8 @@ inline size_t gate_up_q_lds_bytes(int T, int H, int BB, int NC) {
     return (size_t) NC * kGuRows * 4 + (size_t) T * img_bytes((int) host::pad512(H)) + 16;
 }
 inline bool gate_up_q_fits(int H, int BB) { return gate_up_q_lds_bytes(kMaxTok, H, BB, kMaxTok) <= kLdsBudget; }
-inline size_t down_q_lds_bytes(int F, int BB) {
-    const size_t wbuf = (size_t) img_bytes((int) host::pad512(F)) + 4 * (size_t) (F / 256) * BB + 48;
-    return kQWaves * ((wbuf + 15) & ~(size_t) 15);
-}
-inline bool down_q_fits(int F, int BB) { return down_q_lds_bytes(F, BB) <= kLdsBudget; }
+inline size_t down_q_lds_bytes(int CH, int F) { return (size_t) CH * img_bytes((int) host::pad512(F)) + 16; }
+inline bool down_q_fits(int CH, int F) { return down_q_lds_bytes(CH, F) <= kLdsBudget; }
 inline size_t down_lds_bytes(int CH, int F, int BB) {
     const size_t b = (size_t) CH * img_bytes((int) host::pad512(F)) + (size_t) CH * kDownRows * (F / 256) * BB + 16;
     return b <= kLdsBudget ? b : 0;
@@ -1411,9 +1408,9 @@ template <int TQ, int LPR> int launch_down_lds(const LayerArgs &a, size_t lds, h
 
 template <int TQ> int dispatch_down(const LayerArgs &a, hipStream_t st) {
     const int nblk = a.F / 256;
-    if (down_q_fits(a.F, Traits<TQ>::bytes)) {
+    if (down_q_fits(a.T * a.K, a.F)) {
         hipLaunchKernelGGL((k_down_q<TQ>), dim3((unsigned) (a.H / kDownRows)), dim3(kQThreads),
-                           down_q_lds_bytes(a.F, Traits<TQ>::bytes), st, a);
+                           down_q_lds_bytes(a.T * a.K, a.F), st, a);
         return host::check_launch("moe down_combine (quarters)");
     }
     const size_t lds = down_lds_bytes(a.T * a.K, a.F, Traits<TQ>::bytes);
@@ -1677,7 +1674,7 @@ static int launch_shared(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t s
     const int gt = L->shexp_gu_type ? L->shexp_gu_type : L->gu_type;
     const int dt = L->shexp_down_type ? L->shexp_down_type : L->down_type;
     const int64_t H = a.H, Fs = L->shexp_inter;
-    if (gate_up_q_fits(a.H, block_bytes(gt)) && down_q_fits((int) Fs, block_bytes(dt))) {
+    if (gate_up_q_fits(a.H, block_bytes(gt)) && down_q_fits(a.T, (int) Fs)) {
         // The quarter kernels of the routed experts in dense mode: per (row, token) the arithmetic of the fused
         // kernel's shared expert, so a verify column equals its batch-1 result bit for bit.
         LayerArgs s = a;
