@@ -101,15 +101,17 @@ constexpr int kTopkScratch = 432;
 // per candidate). The result is the same as k rounds of argmax with ties to the lower index. Must be called by every
 // thread of the workgroup (it contains barriers). Results: sel[0..k) and their probabilities pv[0..k) in LDS, visible
 // to the whole workgroup on return.
+// gtid: the thread's index in its group of NT (NT = the workgroup, or one of its equal groups each ranking its own
+// token: the barriers are the workgroup's, reached by every group in step).
 template <int NT>
-__device__ __forceinline__ void route_topk_filter(const float *__restrict__ lg, int n_expert, int k, int gating,
-                                                 uint64_t *scratch, int *sel, float *pv) {
+__device__ __forceinline__ void route_topk_filter(int gtid, const float *__restrict__ lg, int n_expert, int k,
+                                                  int gating, uint64_t *scratch, int *sel, float *pv) {
     static_assert(NT >= 64 && NT % 64 == 0 && NT <= 1024, "whole waves");
     constexpr int P = 8;         // threads per candidate
     constexpr int CPP = NT / P;  // candidates per pass
     uint64_t *s_key = scratch, *s_cand = scratch + 256, *s_gm = scratch + 384, *s_t0 = scratch + 416;
     int *s_cnt = (int *) (scratch + 417);  // candidates per wave (16 at most)
-    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int tid = gtid, lane = tid % kWave, wave = tid / kWave;
     if (tid < kWave) {
         float p[4];
         if (gating == 0) {
@@ -277,7 +279,7 @@ template <int NT>
 __device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, int n_expert, int k, int gating,
                                                  uint64_t *scratch, int *sel, float *pv) {
     if (n_expert <= 128) route_topk_pairs<NT>(lg, n_expert, k, gating, scratch, sel, pv);
-    else route_topk_filter<NT>(lg, n_expert, k, gating, scratch, sel, pv);
+    else route_topk_filter<NT>((int) threadIdx.x, lg, n_expert, k, gating, scratch, sel, pv);
 }
 
 // Combine weight of slot j (0 <= j < k < 16) from the selected probabilities pv[0..k): renormalised by their sum in

@@ -331,10 +331,9 @@ __device__ __forceinline__ int route_channel(const LayerArgs &a, RouteLds &rs) {
     return rs.e;
 }
 
-// Routing of n_tok > 1 tokens, run once by the last router workgroup to finish (kK1Threads = 1024 threads): wave t
-// computes token t's probabilities with route_topk_block's fp32 operations (same bits as the batch-1 routing) as
-// 64-bit keys (bits(p) << 32) | ~e and takes its top k by k rounds of wave argmax (the same order as the batch-1
-// rank); the weights follow route_weight (slot-order sum). The distinct experts are listed in ascending order with
+// Routing of n_tok > 1 tokens, run once by the last router workgroup to finish (kK1Threads = 1024 threads): group t
+// of 256 threads ranks token t with the block top-k (the batch-1 routing's probabilities and selection, so the same
+// bits); the weights follow route_weight (slot-order sum). The distinct experts are listed in ascending order with
 // their (token, slot) columns - the channel table the gate/up workgroups read (ggml mm_ids_helper-style compaction:
 // each distinct expert's weights are read once per call) - and ids, weights and down pointers are published.
 __device__ void route_all(const LayerArgs &a) {
@@ -345,54 +344,15 @@ __device__ void route_all(const LayerArgs &a) {
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int T = a.T, K = a.K, NE = a.NE;
     for (int i = tid; i < 256 * kMaxTok; i += kK1Threads) (&s_col[0][0])[i] = 0;
-    if (wave < T) {  // device-scope loads: the logits were written by other workgroups
-        float v[4], p[4], m = -__builtin_inff();
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = lane + 64 * j;
-            v[j] = e < NE ? __hip_atomic_load(a.logits + (size_t) wave * NE + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                          : -__builtin_inff();
-            m = fmaxf(m, v[j]);
-        }
-        if (a.gating == 0) {
-            m = lanes_max<64>(m);
-            float ev[4], sum = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                ev[j] = lane + 64 * j < NE ? fns_expf(v[j] - m) : 0.0f;
-                sum = sum + ev[j];
-            }
-            sum = lanes_sum<64>(sum);
-            const float inv = 1.0f / sum;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) p[j] = ev[j] * inv;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) p[j] = lane + 64 * j < NE ? 1.0f / (1.0f + fns_expf(-v[j])) : 0.0f;
-        }
-        // top-k of the token by k rounds of wave argmax over its 64-bit keys (bits(p) << 32 | ~e: unique; larger =
-        // higher probability, then lower index - the order of the reference's ties-to-lower-index top-k)
-        uint64_t key[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = lane + 64 * j;
-            key[j] = e < NE ? ((uint64_t) __builtin_bit_cast(uint32_t, p[j]) << 32) | (uint32_t) ~e : 0ull;
-        }
-        for (int r = 0; r < K; ++r) {
-            uint64_t m = key[0];
-#pragma unroll
-            for (int j = 1; j < 4; ++j) m = key[j] > m ? key[j] : m;
-            m = lanes_max_u64(m);
-            const int e = (int) ~(uint32_t) m;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (lane + 64 * j == e) key[j] = 0ull;  // the owner drops the winner
-            if (lane == 0) {
-                s_sel[wave][r] = e;
-                s_pv[wave][r] = __builtin_bit_cast(float, (uint32_t) (m >> 32));
-            }
-        }
-    }
+    // each token's logits into LDS (device-scope loads: other workgroups wrote them), then each group of 256 threads
+    // ranks one token with the block top-k (the groups past T repeat the last token; their result is unused)
+    __shared__ __align__(16) uint64_t s_tk[kMaxTok][kTopkScratch];
+    __shared__ float s_lg[kMaxTok][256];
+    const int grp = tid / 256, gt = tid % 256;
+    if (grp < T && gt < NE)
+        s_lg[grp][gt] = __hip_atomic_load(a.logits + (size_t) grp * NE + gt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    route_topk_filter<256>(gt, s_lg[grp < T ? grp : T - 1], NE, K, a.gating, s_tk[grp], s_sel[grp], s_pv[grp]);
     __syncthreads();
     FNS_MARK(0, blockIdx.x, 6);
     if (tid < T * K) {  // (token, slot): ids, weights, down pointers
