@@ -80,3 +80,29 @@ def test_mmq_preconditions():
     assert L.fns_hip_mmq(12, _buf(), 2048, 64, _buf(), 0, _buf(), _buf(), None) == 0     # no tokens: no-op
     assert L.fns_hip_mmq_compact(_buf(), 4, 8, 300, 1, _buf(), _buf(), _buf(), None) == -2  # > 256 experts
     assert L.fns_hip_mmq_compact(_buf(), 4, 8, 128, 3, _buf(), _buf(), _buf(), None) == -2  # rows per token 1 or k
+
+
+def test_moe_block_extras_host_checks():
+    """The whole-block fields of FnsMoeLayer (RMSNorm, shared expert): the workspace grows with them, and a bad shared
+    expert is rejected on the host before any launch."""
+    from flintnsteel_amd import ops
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    ptr = ctypes.addressof(buf)
+    d = ops.MoeLayerDesc(2048, 512, 256, 6, 1, 1, 1, 30, ptr, 12, 13, ptr, 0, 1024, 2048, None)
+    total = ctypes.c_size_t()
+    offs = (ctypes.c_size_t * 6)()
+    assert L.fns_hip_moe_workspace_layout(ctypes.byref(d), 1, offs, ctypes.byref(total)) == 0
+    plain = total.value
+    d.shexp_inter, d.shexp_gate, d.shexp_up, d.shexp_down = 1024, ptr, ptr, ptr
+    assert L.fns_hip_moe_workspace_layout(ctypes.byref(d), 4, offs, ctypes.byref(total)) == 0
+    with_sh4 = total.value
+    assert L.fns_hip_moe_workspace_layout(ctypes.byref(d), 1, offs, ctypes.byref(total)) == 0
+    assert plain < total.value < with_sh4
+    ws = ctypes.create_string_buffer(with_sh4)
+    d.shexp_inter = 1000  # not a multiple of 256
+    assert L.fns_hip_moe_layer(ctypes.byref(d), ptr, None, ptr, 1, ctypes.addressof(ws), with_sh4, None) == -2
+    d.shexp_inter, d.shexp_down = 1024, None  # down missing
+    assert L.fns_hip_moe_layer(ctypes.byref(d), ptr, None, ptr, 1, ctypes.addressof(ws), with_sh4, None) == -2
+    d.shexp_down, d.shexp_gu_type = ptr, 8  # Q8_0: not a K-quant
+    assert L.fns_hip_moe_layer(ctypes.byref(d), ptr, None, ptr, 1, ctypes.addressof(ws), with_sh4, None) == -1
