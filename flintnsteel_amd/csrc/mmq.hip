@@ -54,9 +54,10 @@ inline size_t gprefix_bytes(int64_t n_expert) { return (size_t) 2 * (n_expert + 
 // ---- compaction (ggml mm_ids_helper semantics, stable) ------------------------------------------------------------
 // ids [n_tok][k] -> pairs p = t k + j sorted by expert, ties in p order: ids_dst[q] = p, ids_src1[q] = the activation
 // row of p (t when x_rows_per_tok = 1, p when x_rows_per_tok = k), bounds[e] = first sorted position of expert e.
-// One workgroup; wave w owns a contiguous chunk of the pairs: per-wave histograms (LDS atomics), one prefix over
-// (expert, wave) in that order, then each wave walks its chunk again in order, ranking the lanes that share an expert
-// by ballots on the expert id bits, and advances its own running positions - two passes over the ids, three barriers.
+// One workgroup; wave w owns a contiguous chunk of the pairs (its first 8 ids per lane kept in registers): per-wave
+// histograms (LDS atomics), one prefix over (expert, wave) in that order, then each wave walks its chunk again in
+// order, ranking the lanes that share an expert by ballots on the expert id bits, and advances its own running
+// positions - two passes over the ids, four barriers.
 __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *__restrict__ ids, int n, int k, int ne,
                                                                  int x_rows_per_tok, int32_t *__restrict__ ids_src1,
                                                                  int32_t *__restrict__ ids_dst, int32_t *bounds,
@@ -69,8 +70,25 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
     __syncthreads();
     const int chunk = (n + NW * kWave - 1) / (NW * kWave) * kWave;  // pairs per wave, a multiple of 64
     const int p0 = wave * chunk, p1 = min(n, p0 + chunk);
-    for (int p = p0 + lane; p < p0 + chunk; p += kWave) {  // wave-uniform trip count
-        const int e = p < p1 ? ids[p] : -1;
+    // the first kCache ids of each lane stay in registers for the second pass; their loads are clamped into the
+    // array and unconditional (under the uniform n > 0: an empty batch still writes the bounds), so they are all in
+    // flight together
+    constexpr int kCache = 8;
+    int ev[kCache];
+#pragma unroll
+    for (int it = 0; it < kCache; ++it) {
+        const int p = p0 + lane + kWave * it;
+        const int v = n > 0 ? ids[min(p, n - 1)] : -1;
+        ev[it] = kWave * it < chunk && p < p1 ? v : -1;
+    }
+    auto id_at = [&](int p) { return p < p1 ? ids[p] : -1; };
+#pragma unroll
+    for (int it = 0; it < kCache; ++it) {
+        const int e = ev[it];
+        if (e >= 0 && e < ne) atomicAdd(&wpos[wave][e], 1);
+    }
+    for (int p = p0 + lane + kWave * kCache; p < p0 + chunk; p += kWave) {  // wave-uniform trip count
+        const int e = id_at(p);
         if (e >= 0 && e < ne) atomicAdd(&wpos[wave][e], 1);
     }
     __syncthreads();
@@ -108,14 +126,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         for (int j = 0; j < 4; ++j) {
             const int e = 4 * lane + j;
             if (e < ne) {
-                // the expert's sorted positions, split over the waves in wave order
-                int pos = run;
-#pragma unroll
-                for (int w = 0; w < NW; ++w) {
-                    const int c = wpos[w][e];
-                    wpos[w][e] = pos;
-                    pos += c;
-                }
+                cnt[e] = run;  // the expert's first sorted position (its count is no longer needed)
                 bounds[e] = run;
                 gprefix[e] = rung;
                 gprefix[ne + 1 + e] = rung2;
@@ -131,8 +142,22 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         }
     }
     __syncthreads();
-    for (int p = p0 + lane; p < p0 + chunk; p += kWave) {
-        const int e = p < p1 ? ids[p] : -1;
+    if (tid < ne) {  // the expert's sorted positions, split over the waves in wave order
+        int pos = cnt[tid];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int c = wpos[w][tid];
+            wpos[w][tid] = pos;
+            pos += c;
+        }
+    }
+    __syncthreads();
+    for (int it = 0, p = p0 + lane; p < p0 + chunk; ++it, p += kWave) {
+        int e = -1;
+#pragma unroll
+        for (int c = 0; c < kCache; ++c)
+            if (it == c) e = ev[c];
+        if (it >= kCache) e = id_at(p);
         const bool live = e >= 0 && e < ne;
         // lanes with the same expert id: intersect the ballots of each id bit (and of liveness)
         uint64_t same = __ballot(live);

@@ -76,6 +76,11 @@ __device__ __forceinline__ float4 ld4_guard(const float *row, int k, int ncols) 
     for (int m = 0; m < 4; ++m) v[m] = k + m < ncols ? row[k + m] : 0.0f;
     return make_float4(v[0], v[1], v[2], v[3]);
 }
+__device__ __forceinline__ float4 ld4_bf16(const uint16_t *p) {
+    const uint2 v = *(const uint2 *) p;
+    return make_float4(__builtin_bit_cast(float, v.x << 16), __builtin_bit_cast(float, v.x & 0xffff0000u),
+                       __builtin_bit_cast(float, v.y << 16), __builtin_bit_cast(float, v.y & 0xffff0000u));
+}
 __device__ __forceinline__ float4 ld4_bf16_guard(const uint16_t *row, int k, int ncols) {
     float v[4];
 #pragma unroll
@@ -87,7 +92,9 @@ __device__ __forceinline__ float round_bf16(float v) {
     b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
     return __builtin_bit_cast(float, b);
 }
-template <bool BF16>
+// FULL: ncols is a multiple of 64, so every chunk is whole and the loads need no guard (a guarded load is a branch,
+// and the compiler then waits for each load before issuing the next).
+template <bool BF16, bool FULL>
 __global__ __launch_bounds__(512) void k_gemm_router(const void *__restrict__ w, const float *__restrict__ bias,
                                                      const float *__restrict__ x, float *__restrict__ y, int ncols,
                                                      int nrows, int n_tok) {
@@ -106,9 +113,15 @@ __global__ __launch_bounds__(512) void k_gemm_router(const void *__restrict__ w,
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int k = k0 + 16 * u + 4 * kk;
-            a[u] = ld4_guard(xr, k, ncols);
-            if constexpr (BF16) b[u] = ld4_bf16_guard((const uint16_t *) w + (size_t) ea * ncols, k, ncols);
-            else b[u] = ld4_guard((const float *) w + (size_t) ea * ncols, k, ncols);
+            if constexpr (FULL) {
+                a[u] = *(const float4 *) (xr + k);
+                if constexpr (BF16) b[u] = ld4_bf16((const uint16_t *) w + (size_t) ea * ncols + k);
+                else b[u] = *(const float4 *) ((const float *) w + (size_t) ea * ncols + k);
+            } else {
+                a[u] = ld4_guard(xr, k, ncols);
+                if constexpr (BF16) b[u] = ld4_bf16_guard((const uint16_t *) w + (size_t) ea * ncols, k, ncols);
+                else b[u] = ld4_guard((const float *) w + (size_t) ea * ncols, k, ncols);
+            }
         }
     };
     int k0 = wave * 64;
@@ -180,6 +193,41 @@ __global__ void k_moe_combine(const float *__restrict__ dexp, const float *__res
     out[(size_t) t * n + i] = (moe + s) + (x_in ? x_in[(size_t) t * n + i] : 0.0f);
 }
 
+// Four adjacent columns per thread and the k expert rows unrolled, every load issued before the sums; the same
+// arithmetic and order per column as k_moe_combine.
+template <int K>
+__global__ void k_moe_combine4(const float *__restrict__ dexp, const float *__restrict__ escale,
+                               const float *__restrict__ w, const float *__restrict__ sh, const float *x_in, float *out,
+                               int n) {
+    const int t = blockIdx.y;
+    const int i = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= n) return;
+    const float *d = dexp + (size_t) t * K * n + i;
+    float4 dv[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) dv[j] = *(const float4 *) (d + (size_t) j * n);
+    const float4 s = sh ? *(const float4 *) (sh + (size_t) t * n + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 xv = x_in ? *(const float4 *) (x_in + (size_t) t * n + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float ws[K], es[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        ws[j] = w[(size_t) t * K + j];
+        es[j] = escale ? escale[(size_t) t * K + j] : 1.0f;
+    }
+    auto col = [&](auto get) {
+        float moe = (get(dv[0]) * es[0]) * ws[0];
+#pragma unroll
+        for (int j = 1; j < K; ++j) moe = moe + (get(dv[j]) * es[j]) * ws[j];
+        return moe;
+    };
+    float4 o;
+    o.x = (col([](float4 v) { return v.x; }) + s.x) + xv.x;
+    o.y = (col([](float4 v) { return v.y; }) + s.y) + xv.y;
+    o.z = (col([](float4 v) { return v.z; }) + s.z) + xv.z;
+    o.w = (col([](float4 v) { return v.w; }) + s.w) + xv.w;
+    *(float4 *) (out + (size_t) t * n + i) = o;
+}
+
 __global__ void k_count_routes(const int32_t *ids, uint32_t *counts, int k) {
     if ((int) threadIdx.x < k) atomicAdd(&counts[ids[threadIdx.x]], 1u);
 }
@@ -218,9 +266,13 @@ int gemm_router_bias(int dtype, const void *w, const float *bias, const float *x
         return host::set_error(host::ERR_SHAPE, "gemm_router: bad arguments");
     if (n_tok == 0) return host::OK;
     const dim3 g((unsigned) ((n_tok + 15) / 16), (unsigned) ((nrows + 15) / 16));
-    if (dtype == T_BF16) hipLaunchKernelGGL(k_gemm_router<true>, g, dim3(512), 0, st, w, bias, x, y, ncols, nrows, n_tok);
-    else if (dtype == 0) hipLaunchKernelGGL(k_gemm_router<false>, g, dim3(512), 0, st, w, bias, x, y, ncols, nrows, n_tok);
-    else return host::set_error(host::ERR_TYPE, "gemm_router: dtype %d not supported", dtype);
+    if (dtype != T_BF16 && dtype != 0)
+        return host::set_error(host::ERR_TYPE, "gemm_router: dtype %d not supported", dtype);
+    // Whole 64-column chunks on 16-byte (f32) / 8-byte (bf16) aligned rows take the unguarded loads.
+    const bool full = ncols % 64 == 0 && ((uintptr_t) x & 15) == 0 && ((uintptr_t) w & (dtype == T_BF16 ? 7 : 15)) == 0;
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, g, dim3(512), 0, st, w, bias, x, y, ncols, nrows, n_tok); };
+    if (dtype == T_BF16) full ? go(k_gemm_router<true, true>) : go(k_gemm_router<true, false>);
+    else full ? go(k_gemm_router<false, true>) : go(k_gemm_router<false, false>);
     return host::check_launch("gemm_router");
 }
 
@@ -244,8 +296,21 @@ int moe_combine(const float *dexp, const float *escale, const float *w, const fl
     if (!dexp || !w || !out || n < 0 || k < 1 || n_tok < 0)
         return host::set_error(host::ERR_SHAPE, "moe_combine: bad arguments");
     if (n == 0 || n_tok == 0) return host::OK;
-    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned) ((n + 255) / 256), (unsigned) n_tok), dim3(256), 0, st, dexp,
-                       escale, w, sh, x_in, out, n, k);
+    const bool vec = n % 4 == 0 && k <= 8 && (((uintptr_t) dexp | (uintptr_t) out | (uintptr_t) (sh ? sh : out) |
+                                                (uintptr_t) (x_in ? x_in : out)) & 15) == 0;
+    if (vec) {
+        const dim3 g((unsigned) ((n / 4 + 255) / 256), (unsigned) n_tok);
+        switch (k) {
+#define FNS_COMBINE4(K) \
+    case K: hipLaunchKernelGGL(k_moe_combine4<K>, g, dim3(256), 0, st, dexp, escale, w, sh, x_in, out, n); break;
+            FNS_COMBINE4(1) FNS_COMBINE4(2) FNS_COMBINE4(3) FNS_COMBINE4(4)
+            FNS_COMBINE4(5) FNS_COMBINE4(6) FNS_COMBINE4(7) FNS_COMBINE4(8)
+#undef FNS_COMBINE4
+        }
+    } else {
+        hipLaunchKernelGGL(k_moe_combine, dim3((unsigned) ((n + 255) / 256), (unsigned) n_tok), dim3(256), 0, st, dexp,
+                           escale, w, sh, x_in, out, n, k);
+    }
     return host::check_launch("moe_combine");
 }
 

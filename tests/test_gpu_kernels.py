@@ -227,13 +227,30 @@ def test_gemv_router_f32_and_bf16(ops):
     assert_close(got, np.tile(orc.router_f32(w, x), (20, 1)), "router gemm f32", 1e-5, 1e-6)
 
 
-def test_moe_combine_bit_exact(ops):
-    rng = np.random.default_rng(4)
-    dexp = gaussian(rng, (3, 8, H))
-    w = np.abs(gaussian(rng, (3, 8)))
-    e = np.exp2(rng.integers(0, 3, (3, 8))).astype(np.float32)
-    sh = gaussian(rng, (3, H))
-    x = gaussian(rng, (3, H))
+@pytest.mark.parametrize("ncols", [200, 1000])
+def test_gemm_router_ragged_width(ops, ncols):
+    """Widths that are not a multiple of 64 take the guarded loads of the router GEMM (f32 and bf16 weights)."""
+    rng = np.random.default_rng(ncols)
+    w = gaussian(rng, (40, ncols), 0.02)
+    x = gaussian(rng, (19, ncols))
+    got = host(ops.gemm_router(dev(w), dev(x)))
+    assert_close(got, orc.router_f32(w, x), "router gemm f32 ragged", 1e-5, 1e-6)
+    wb = torch.from_numpy(w).to(torch.bfloat16)
+    xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    got = host(ops.gemm_router(wb.cuda(), dev(x)))
+    ref = xb.astype(np.float64) @ wb.float().numpy().astype(np.float64).T
+    assert_close(got, ref, "router gemm bf16 ragged", 1e-5, 1e-6)
+
+
+@pytest.mark.parametrize("k,n", [(8, H), (6, H), (1, 256), (3, 2050), (12, H)])
+def test_moe_combine_bit_exact(ops, k, n):
+    """k <= 8 with n % 4 == 0 takes the four-column kernel; the others the per-column one: same bits either way."""
+    rng = np.random.default_rng(4 + k)
+    dexp = gaussian(rng, (3, k, n))
+    w = np.abs(gaussian(rng, (3, k)))
+    e = np.exp2(rng.integers(0, 3, (3, k))).astype(np.float32)
+    sh = gaussian(rng, (3, n))
+    x = gaussian(rng, (3, n))
     got = host(ops.moe_combine(dev(dexp), dev(w), dev(e), dev(sh), dev(x)))
     ref = orc.moe_combine(dexp, w, e, sh, x)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))

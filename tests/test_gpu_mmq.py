@@ -45,7 +45,8 @@ def table_of(mats_dev):
 
 
 @pytest.mark.parametrize("n_tok,k,n_expert,xr", [(77, 8, 16, 1), (77, 8, 16, 8), (1, 1, 1, 1), (600, 8, 128, 1),
-                                                 (5, 6, 256, 6), (1100, 4, 8, 1), (4096, 8, 128, 1)])
+                                                 (5, 6, 256, 6), (1100, 4, 8, 1), (4096, 8, 128, 1),
+                                                 (1024, 8, 128, 1), (1023, 8, 64, 8)])
 def test_compaction_bit_exact(ops, n_tok, k, n_expert, xr):
     rng = np.random.default_rng(n_tok * 31 + k)
     ids = distinct_ids(rng, n_tok, k, n_expert)
