@@ -5,6 +5,7 @@
 // src/prefill_kernels.cu:133-183,217-242 (batch router, route_topk_batch, moe_combine_batch). Gating is
 // generalised to softmax (the configs, llama.cpp build_moe_ffn) or sigmoid (the Flint model), any expert count up to
 // 256 and k up to 16; the reference hard-codes sigmoid, 256 experts and k <= 8.
+#include <algorithm>
 #include "fns/kernels.h"
 #include "fns_common.hpp"
 #include "fns_host.hpp"
@@ -124,6 +125,57 @@ __global__ __launch_bounds__(512) void k_gemm_router(const void *__restrict__ w,
             }
         }
     };
+    if constexpr (FULL) {
+        // Coalesced loads, each instruction covering 4 whole 256-byte row pieces of the chunk (8 full cache lines
+        // instead of 16 half lines in the MFMA operand layout), through a wave-private padded LDS tile back into
+        // that layout. Same chunk order and products as the direct loop below.
+        __shared__ __align__(16) float tile[NW][2][16][68];
+        float (*xs)[68] = tile[wave][0], (*wsh)[68] = tile[wave][1];
+        const int lr = lane / 16, lc = 4 * (lane % 16);
+        // element offsets of this lane's four rows (clamped rows: results discarded)
+        const int xo0 = min(t0 + lr, n_tok - 1) * ncols + lc, xo1 = min(t0 + 4 + lr, n_tok - 1) * ncols + lc;
+        const int xo2 = min(t0 + 8 + lr, n_tok - 1) * ncols + lc, xo3 = min(t0 + 12 + lr, n_tok - 1) * ncols + lc;
+        const int wo0 = min(e0 + lr, nrows - 1) * ncols + lc, wo1 = min(e0 + 4 + lr, nrows - 1) * ncols + lc;
+        const int wo2 = min(e0 + 8 + lr, nrows - 1) * ncols + lc, wo3 = min(e0 + 12 + lr, nrows - 1) * ncols + lc;
+        auto ldw = [&](int off) {
+            if constexpr (BF16) return ld4_bf16((const uint16_t *) w + off);
+            else return *(const float4 *) ((const float *) w + off);
+        };
+        float4 ga0, ga1, ga2, ga3, gb0, gb1, gb2, gb3;
+        int k0 = wave * 64;
+        if (k0 < ncols) {
+            ga0 = *(const float4 *) (x + xo0 + k0), ga1 = *(const float4 *) (x + xo1 + k0);
+            ga2 = *(const float4 *) (x + xo2 + k0), ga3 = *(const float4 *) (x + xo3 + k0);
+            gb0 = ldw(wo0 + k0), gb1 = ldw(wo1 + k0), gb2 = ldw(wo2 + k0), gb3 = ldw(wo3 + k0);
+        }
+        for (; k0 < ncols; k0 += NW * 64) {
+            *(float4 *) &xs[lr][lc] = ga0, *(float4 *) &xs[4 + lr][lc] = ga1;
+            *(float4 *) &xs[8 + lr][lc] = ga2, *(float4 *) &xs[12 + lr][lc] = ga3;
+            *(float4 *) &wsh[lr][lc] = gb0, *(float4 *) &wsh[4 + lr][lc] = gb1;
+            *(float4 *) &wsh[8 + lr][lc] = gb2, *(float4 *) &wsh[12 + lr][lc] = gb3;
+            const int kn = k0 + NW * 64;
+            if (kn < ncols) {
+                ga0 = *(const float4 *) (x + xo0 + kn), ga1 = *(const float4 *) (x + xo1 + kn);
+                ga2 = *(const float4 *) (x + xo2 + kn), ga3 = *(const float4 *) (x + xo3 + kn);
+                gb0 = ldw(wo0 + kn), gb1 = ldw(wo1 + kn), gb2 = ldw(wo2 + kn), gb3 = ldw(wo3 + kn);
+            }
+            float4 ca[4], cb[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                ca[u] = *(const float4 *) &xs[il][16 * u + 4 * kk];
+                cb[u] = *(const float4 *) &wsh[il][16 * u + 4 * kk];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float av[4] = {ca[u].x, ca[u].y, ca[u].z, ca[u].w}, bv[4] = {cb[u].x, cb[u].y, cb[u].z, cb[u].w};
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const float xa = BF16 ? round_bf16(av[m]) : av[m];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, bv[m], acc, 0, 0, 0);
+                }
+            }
+        }
+    } else {
     int k0 = wave * 64;
     if (k0 < ncols) load(k0);
     for (; k0 < ncols; k0 += NW * 64) {
@@ -141,6 +193,7 @@ __global__ __launch_bounds__(512) void k_gemm_router(const void *__restrict__ w,
                 const float xa = BF16 ? round_bf16(av[u][m]) : av[u][m];
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, bv[u][m], acc, 0, 0, 0);
             }
+    }
     }
     part[wave][lane] = acc;
     __syncthreads();
@@ -268,8 +321,9 @@ int gemm_router_bias(int dtype, const void *w, const float *bias, const float *x
     const dim3 g((unsigned) ((n_tok + 15) / 16), (unsigned) ((nrows + 15) / 16));
     if (dtype != T_BF16 && dtype != 0)
         return host::set_error(host::ERR_TYPE, "gemm_router: dtype %d not supported", dtype);
-    // Whole 64-column chunks on 16-byte (f32) / 8-byte (bf16) aligned rows take the unguarded loads.
-    const bool full = ncols % 64 == 0 && ((uintptr_t) x & 15) == 0 && ((uintptr_t) w & (dtype == T_BF16 ? 7 : 15)) == 0;
+    // Whole 64-column chunks on 16-byte (f32) / 8-byte (bf16) aligned rows, with 32-bit element offsets, take the
+    // unguarded loads.
+    const bool full = ncols % 64 == 0 && (int64_t) ncols * std::max(n_tok, nrows) < ((int64_t) 1 << 31) && ((uintptr_t) x & 15) == 0 && ((uintptr_t) w & (dtype == T_BF16 ? 7 : 15)) == 0;
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, g, dim3(512), 0, st, w, bias, x, y, ncols, nrows, n_tok); };
     if (dtype == T_BF16) full ? go(k_gemm_router<true, true>) : go(k_gemm_router<true, false>);
     else full ? go(k_gemm_router<false, true>) : go(k_gemm_router<false, false>);
