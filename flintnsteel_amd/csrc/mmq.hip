@@ -251,7 +251,8 @@ struct MmqArgs {
     int64_t x_img;             // bytes per activation image row
     const int32_t *bounds;     // [n_expert + 1] (null: dense)
     const int32_t *gprefix;    // [2][n_expert + 1] group prefixes: 64-row groups, then the <= 32-row remainders
-    int n_main;                // launch: workgroup rows (blockIdx.y) of the 64-row list
+    int n_main;                // launch: groups of the 64-row list (then the remainder list up to n_groups)
+    int n_groups, n_cb;        // launch: groups in both lists; weight row blocks per group
     const int32_t *src;        // sorted position -> activation image row (null: identity)
     const int32_t *dst_rows;   // sorted position -> output row (null: identity)
     int n_rows;                // dense: number of activation rows
@@ -839,9 +840,12 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
     MMQ_MARK(12);
 }
 
-// One launch runs both lists, the 64-row groups first (blockIdx.y < n_main) and then the experts' <= 32-row
-// remainders, so the smaller workgroups fill the machine while the last large ones finish; blockIdx.x is the weight
-// row block.
+// One launch runs both lists, the 64-row groups first (g < n_main) and then the experts' <= 32-row remainders, so the
+// smaller workgroups fill the machine while the last large ones finish. The grid is one-dimensional and XCD-aware:
+// workgroup L runs on XCD L % 8 (the hardware's round-robin dispatch), and the n_cb weight row blocks of a group are
+// consecutive items of one XCD, so the group's activation rows are fetched into that XCD's L2 once, not once per
+// row block; groups go to the XCDs in turn (group u on XCD u % 8) in increasing order.
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 template <int T, bool GLU>
 __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 4))) void k_mmq(const MmqArgs a) {
     __shared__ __align__(16) uint8_t sh_a0[kMmqTok * kRowA];
@@ -849,9 +853,11 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     __shared__ __align__(16) uint8_t sh_s[(T == T_Q4_K || T == T_Q5_K) ? kMmqTok * kRowS : 16];
     __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok], sh_grp[4];
     const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp};
-    const int g = blockIdx.y;
-    if (g < a.n_main) mmq_group<T, GLU, 2>(a, g, blockIdx.x, L);
-    else mmq_group<T, GLU, 1>(a, g - a.n_main, blockIdx.x, L);
+    const int lid = blockIdx.x, r = lid / kXcds;
+    const int g = (r / a.n_cb) * kXcds + lid % kXcds, wb = r % a.n_cb;
+    if (g >= a.n_groups) return;
+    if (g < a.n_main) mmq_group<T, GLU, 2>(a, g, wb, L);
+    else mmq_group<T, GLU, 1>(a, g - a.n_main, wb, L);
 }
 
 template <bool GLU> const void *mmq_kernel(int type) {
@@ -875,8 +881,11 @@ int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st)
     const int total = groups + (a.bounds ? a.n_expert : 0);
     void *args[] = {&arg};
     const int rows = glu ? 128 : 256;  // weight rows per workgroup
-    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) ((a.nrows + rows - 1) / rows), (unsigned) total),
-                                         dim3(kMmqThreads), args, 0, st);
+    arg.n_groups = total;
+    arg.n_cb = (a.nrows + rows - 1) / rows;
+    const int64_t items = (int64_t) arg.n_cb * kXcds * ((total + kXcds - 1) / kXcds);
+    if (items > INT32_MAX) return host::set_error(host::ERR_SHAPE, "mmq: grid too large");
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) items), dim3(kMmqThreads), args, 0, st);
     if (e != hipSuccess) return host::set_error(host::ERR_LAUNCH, "mmq: %s", hipGetErrorString(e));
     return host::check_launch("mmq");
 }
