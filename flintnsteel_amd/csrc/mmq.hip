@@ -24,11 +24,13 @@
 //
 // Outputs match the float64 oracle (oracle/fns_oracle.c) on the same Q8_1 activations within the fp32 tolerance of
 // the tests.
+#include <algorithm>
 #include "fns_block.hpp"
 #include "fns_common.hpp"
 #include "fns_host.hpp"
 #include "fns_internal.hpp"
 #include "fns_lanes.hpp"
+#include "fns_router_gemm.hpp"
 
 #include "fns/ggml_kernels.h"
 
@@ -238,6 +240,29 @@ __global__ __launch_bounds__(256) void k_quant_image(const float *__restrict__ x
     const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
     const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
     q8_split8<true>(v, out + (size_t) row * img_row_bytes, ncols, col, true);
+}
+
+// Router GEMM tiles and the split activation image of the same rows in one launch (the two only read x): workgroups
+// [0, n_rt) are router tiles (tile (id % tiles_x, id / tiles_x)), the rest quantise two 2048-column pieces of x each,
+// as k_quant_image does, so the image is built on the CUs the router tiles leave free.
+template <bool BF16>
+__global__ __launch_bounds__(512) void k_router_image(const void *__restrict__ w, const float *__restrict__ bias,
+                                                      const float *__restrict__ x, float *__restrict__ y, int ncols,
+                                                      int nrows, int n_tok, int tiles_x, int n_rt,
+                                                      uint8_t *__restrict__ img, int64_t img_row_bytes, int nxb) {
+    const int id = blockIdx.x;
+    if (id < n_rt) {
+        router_gemm_tile<BF16, true>(w, bias, x, y, ncols, nrows, n_tok, id % tiles_x, id / tiles_x);
+        return;
+    }
+    const int item = 2 * (id - n_rt) + (int) threadIdx.x / 256;
+    if (item >= nxb * n_tok) return;
+    const int row = item / nxb, col = ((item % nxb) * 256 + (int) threadIdx.x % 256) * 8;
+    if (col >= ncols) return;
+    const float *src = x + (size_t) row * ncols + col;
+    const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    q8_split8<true>(v, img + (size_t) row * img_row_bytes, ncols, col, true);
 }
 
 // ---- grouped GEMM -------------------------------------------------------------------------------------------------
@@ -1100,11 +1125,32 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
         FNS_TRY(rms_norm_q8_1(x, L->ffn_norm, (float *) sec[11], sec[12], (int) L->hidden, L->norm_eps, (int) n_tok, st));
         x = (const float *) sec[11];
     }
-    FNS_TRY(gemm_router_bias(L->router_dtype, L->router_w, L->router_bias, x, logits, L->hidden, L->n_expert, (int) n_tok,
-                             st));
+    // the router GEMM and the activation image in one launch when the GEMM takes its unguarded path (whole 64-column
+    // chunks, aligned rows, 32-bit offsets), else as two launches
+    const int H = (int) L->hidden, NE = (int) L->n_expert;
+    const bool bf = L->router_dtype == T_BF16;
+    const bool one = (bf || L->router_dtype == 0) && H % 64 == 0 && (int64_t) H * std::max<int64_t>(n_tok, NE) < INT32_MAX &&
+                     ((uintptr_t) x & 15) == 0 && ((uintptr_t) L->router_w & (bf ? 7 : 15)) == 0;
+    if (one) {
+        const int tiles_x = (int) ((n_tok + 15) / 16), n_rt = tiles_x * ((NE + 15) / 16);
+        const int nxb = (H + 2047) / 2048;
+        const int64_t n_img = (nxb * n_tok + 1) / 2;
+        if (n_rt + n_img > INT32_MAX) return host::set_error(host::ERR_SHAPE, "prefill: grid too large");
+        const dim3 g((unsigned) (n_rt + n_img));
+        if (bf)
+            hipLaunchKernelGGL(k_router_image<true>, g, dim3(512), 0, st, L->router_w, L->router_bias, x, logits, H, NE,
+                               (int) n_tok, tiles_x, n_rt, (uint8_t *) sec[3], (int64_t) mmq_image_bytes(H), nxb);
+        else
+            hipLaunchKernelGGL(k_router_image<false>, g, dim3(512), 0, st, L->router_w, L->router_bias, x, logits, H,
+                               NE, (int) n_tok, tiles_x, n_rt, (uint8_t *) sec[3], (int64_t) mmq_image_bytes(H), nxb);
+        FNS_TRY(host::check_launch("prefill router + image"));
+    } else {
+        FNS_TRY(gemm_router_bias(L->router_dtype, L->router_w, L->router_bias, x, logits, L->hidden, L->n_expert,
+                                 (int) n_tok, st));
+        FNS_TRY(mmq_quant_image(x, L->hidden, n_tok, sec[3], st));
+    }
     FNS_TRY(route_topk(logits, ids, w, L->n_expert, L->k, (int) n_tok, L->gating, L->norm_w, st));
     FNS_TRY(mmq_compact(ids, n_tok, L->k, L->n_expert, 1, src1, dstr, bounds, bounds + L->n_expert + 1, st));
-    FNS_TRY(mmq_quant_image(x, L->hidden, n_tok, sec[3], st));
     FNS_TRY(mmq_gemm_experts(L->gu_type, table, L->gate_off, L->up_off, true, L->hidden, L->inter, L->n_expert, sec[3],
                              P, src1, dstr, bounds, bounds + L->n_expert + 1, nullptr, sec[4], L->guard ? act : nullptr,
                              st));
