@@ -54,7 +54,7 @@ int fns_hip_mmvq_experts(int type, const void *const *table, size_t off, int64_t
                               S(stream));
 }
 
-int fns_hip_mmvq_supports(int type) { return host::is_kquant(type) ? 1 : 0; }
+int fns_hip_mmvq_supports(int type) { return host::is_supported(type) ? 1 : 0; }
 
 int fns_hip_rms_norm_q8_1(const float *x, const float *w, float *out, void *xq, int n, float eps, int rows,
                           void *stream) {

@@ -7,6 +7,7 @@
 //   Q4_K 144 B / 256 values: half d @0 | half dmin @2 | scales[12] @4 | qs[128] @16
 //   Q5_K 176 B / 256 values: half d @0 | half dmin @2 | scales[12] @4 | qh[32] @16 | qs[128] @48
 //   Q6_K 210 B / 256 values: ql[128] @0 | qh[64] @128 | int8 scales[16] @192 | half d @208
+//   Q8_0  34 B / 32 values : half d | int8 qs[32]  (the kernels handle 8 consecutive blocks, 272 B, as one unit)
 // Q3_K and Q6_K blocks are only 2-byte aligned inside a row; gfx950 global loads accept unaligned addresses, so the
 // 16-byte fragments below are read with memcpy-style loads at their true addresses.
 #pragma once
@@ -29,9 +30,11 @@ template <> struct Traits<T_Q3_K> { static constexpr int bytes = 110, slots = 4;
 template <> struct Traits<T_Q4_K> { static constexpr int bytes = 144, slots = 8; };
 template <> struct Traits<T_Q5_K> { static constexpr int bytes = 176, slots = 8; };
 template <> struct Traits<T_Q6_K> { static constexpr int bytes = 210, slots = 8; };
+// Q8_0 (34 B per 32 values: half d | int8 qs[32]): the kernels' 256-value unit is 8 consecutive blocks (272 B).
+template <> struct Traits<T_Q8_0> { static constexpr int bytes = 272, slots = 4; };
 
 __host__ __device__ constexpr int block_bytes(int t) {
-    return t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 34 : 0;
+    return t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 272 : 0;
 }
 
 __device__ __forceinline__ float half_to_float(uint32_t bits16) {

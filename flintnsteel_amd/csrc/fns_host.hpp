@@ -32,8 +32,13 @@ void abort_on_error(int rc, const char *what);
 
 inline int64_t pad512(int64_t n) { return (n + 511) / 512 * 512; }
 inline bool is_kquant(int t) { return t == 11 || t == 12 || t == 13 || t == 14; }
+// Types that only the quarter-block kernels decode (no K-quant sub-block machinery): Q8_0.
+inline bool is_quarter_only(int t) { return t == 8; }
+// Every weight type the GEMV paths accept (mmvq_supports).
+inline bool is_supported(int t) { return is_kquant(t) || is_quarter_only(t); }
+// Bytes of 256 consecutive values of a row (a K-quant block; 8 Q8_0 blocks).
 inline int64_t kquant_block_bytes(int t) {
-    return t == 11 ? 110 : t == 12 ? 144 : t == 13 ? 176 : t == 14 ? 210 : 0;
+    return t == 11 ? 110 : t == 12 ? 144 : t == 13 ? 176 : t == 14 ? 210 : t == 8 ? 272 : 0;
 }
 inline int64_t q8_1_row_bytes(int64_t ncols) { return pad512(ncols) / 32 * 36; }
 

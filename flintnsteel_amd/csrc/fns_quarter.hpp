@@ -8,6 +8,7 @@
 //                          d * sum_g sc_g * (d8 * (u . a) - 32 * d8 * sum a) over its four 16-value groups
 //   Q3_K quarter 2n+h    : values 128n + 64h .. +63: qs[32n..32n+31] bit pairs 2j (j = 2h, 2h+1), hmask bit 4n+j;
 //                          d * sum_g (sc_g - 32) * (d8 * (u . a) - 4 * d8 * sum a)
+//   Q8_0 quarter q       : blocks 2q and 2q+1 of 8 consecutive 34-byte blocks; sum_b (d_b * d8) * (q_b . a)
 // The integer products are exact (v_dot4 on int8 lanes); the zero points (32 for Q6_K, 4 for Q3_K) are folded into
 // the activation sums, as in block_dot.
 #pragma once
@@ -211,6 +212,34 @@ template <> __device__ __forceinline__ float quarter_dot<T_Q3_K, Aligned16>(cons
 template <> __device__ __forceinline__ float quarter_dot<T_Q3_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
                                                                        int qt) {
     return q3k_quarter(blk, x, bb, qt);
+}
+
+// Q8_0 quarter qt = blocks 2qt and 2qt+1 of the 8-block unit (68 bytes at offset 68 qt, 2-byte aligned at least):
+// sum over the two blocks of (d_w * d8) * (q_w . a), the block product of ggml vec_dot_q8_0_q8_1.
+__device__ __forceinline__ float q80_quarter(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+    const uint8_t *p = blk + 68 * qt;
+    const uint4 A0 = lds16u(p), A1 = lds16u(p + 16), A2 = lds16u(p + 32), A3 = lds16u(p + 48);
+    const uint32_t W[17] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w, A2.x,
+                            A2.y, A2.z, A2.w, A3.x, A3.y, A3.z, A3.w, ld32u(p + 64)};
+    int a[16];
+    act_quarter(x, bb, qt, a);
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        s0 = dot4((int) __builtin_amdgcn_alignbit(W[i + 1], W[i], 16), a[i], s0);  // block 0 codes: bytes 2 .. 33
+        s1 = dot4((int) W[9 + i], a[8 + i], s1);                                    // block 1 codes: bytes 36 .. 67
+    }
+    const int b32 = bb * 8 + 2 * qt;
+    const float d0 = half_to_float(W[0] & 0xffffu) * x.d[b32], d1 = half_to_float(W[8] >> 16) * x.d[b32 + 1];
+    return fmaf_(d1, (float) s1, d0 * (float) s0);
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q8_0, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                            int qt) {
+    return q80_quarter(blk, x, bb, qt);
+}
+template <> __device__ __forceinline__ float quarter_dot<T_Q8_0, Any2>(const uint8_t *blk, const ActImg &x, int bb,
+                                                                       int qt) {
+    return q80_quarter(blk, x, bb, qt);
 }
 
 // The same dot for NC activation columns (n < ncol live; NC == 1 ignores ncol): acc[n] += quarter_dot(blk, x[n]).

@@ -15,6 +15,7 @@
 // src/ggml/ggml_mmvq.cu:25-27).
 #include "fns/ggml_kernels.h"
 #include "fns_common.hpp"
+#include "fns_quarter.hpp"
 #include "fns_host.hpp"
 #include "fns_internal.hpp"
 
@@ -41,24 +42,10 @@ struct MmvqParams {
     int ncols, nrows;
 };
 
-template <int LPR> constexpr int rows_per_group() { return LPR >= 32 ? 2 : 1; }
-
-template <int T, int LPR, int SPL, int NC, bool GLU>
-__global__ __launch_bounds__(256) void k_mmvq(const MmvqParams p) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int SPB = Traits<T>::slots;
-    constexpr int BB = Traits<T>::bytes;
-    constexpr int G = 256 / LPR;
-    constexpr int RPG = rows_per_group<LPR>();
-    constexpr int SPLX = SPL > 0 ? SPL : 1;
-    const int tid = threadIdx.x;
-    const int c = blockIdx.y;
-
-    // channel -> matrices, activation rows, outputs
-    const uint8_t *wa, *wb;
-    int ncol;
-    int xrow[NC];
-    float *out[NC];
+// Channel c -> its matrices (A; B = gate for GLU), live columns, activation rows and output rows.
+template <int NC>
+__device__ __forceinline__ void channel_of(const MmvqParams &p, int c, const uint8_t *&wa, const uint8_t *&wb,
+                                           int &ncol, int (&xrow)[NC], float *(&out)[NC]) {
     if (p.ncol_dense > 0) {
         wa = p.base + p.off_a;
         wb = p.base + p.off_b;
@@ -83,6 +70,26 @@ __global__ __launch_bounds__(256) void k_mmvq(const MmvqParams p) {
         xrow[0] = (c / p.x_div) % p.n_xq;
         out[0] = p.dst + (size_t) c * p.nrows;
     }
+}
+
+template <int LPR> constexpr int rows_per_group() { return LPR >= 32 ? 2 : 1; }
+
+template <int T, int LPR, int SPL, int NC, bool GLU>
+__global__ __launch_bounds__(256) void k_mmvq(const MmvqParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int SPB = Traits<T>::slots;
+    constexpr int BB = Traits<T>::bytes;
+    constexpr int G = 256 / LPR;
+    constexpr int RPG = rows_per_group<LPR>();
+    constexpr int SPLX = SPL > 0 ? SPL : 1;
+    const int tid = threadIdx.x;
+    const int c = blockIdx.y;
+
+    const uint8_t *wa, *wb;
+    int ncol;
+    int xrow[NC];
+    float *out[NC];
+    channel_of<NC>(p, c, wa, wb, ncol, xrow, out);
 
     const int nblk = p.ncols / 256;
     const int nslots = nblk * SPB;
@@ -204,18 +211,110 @@ template <int T, int NC, bool GLU> int launch_nc(const MmvqParams &p, int n_chan
     return launch_shape<T, 64, 0, NC, GLU>(p, n_chan, st);
 }
 
+
+// Quarter-block form, for the types without slot decoders (Q8_0): LPR lanes per row (16 or 32), lane l takes the
+// 64-value quarters l, l + LPR, ... of its row; the activation rows are staged in LDS as row images (fns_block.hpp
+// layout, built from the Q8_1 blocks). Per (row, column) the arithmetic does not depend on the launch shape.
+__device__ __forceinline__ void stage_q8_1_img(const uint8_t *__restrict__ src, int npad, uint8_t *img, int tid,
+                                               int nthreads) {
+    float *d = (float *) (img + img_q_bytes(npad)), *s16 = d + npad / 32, *s32 = s16 + npad / 16;
+    for (int b = tid; b < npad / 32; b += nthreads) {
+        const uint32_t *w = (const uint32_t *) (src + (size_t) b * 36);
+        uint32_t v[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) v[i] = w[i];
+        const float db = half_to_float(v[0] & 0xffffu);
+        int sa = 0, sb = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sa = dot4((int) v[1 + i], 0x01010101, sa);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sb = dot4((int) v[5 + i], 0x01010101, sb);
+        uint4 *dq = (uint4 *) (img + img_q_index(32 * b));
+        dq[0] = make_uint4(v[1], v[2], v[3], v[4]);
+        dq[1] = make_uint4(v[5], v[6], v[7], v[8]);
+        d[b] = db;
+        s16[2 * b] = db * (float) sa;
+        s16[2 * b + 1] = db * (float) sb;
+        s32[b] = db * (float) (sa + sb);
+    }
+}
+
+template <int T, int LPR, int NC, bool GLU>
+__global__ __launch_bounds__(256) void k_mmvq_q(const MmvqParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int BB = Traits<T>::bytes;
+    const int tid = threadIdx.x;
+    const uint8_t *wa, *wb;
+    int ncol;
+    int xrow[NC];
+    float *out[NC];
+    channel_of<NC>(p, blockIdx.y, wa, wb, ncol, xrow, out);
+    const int npad = (p.ncols + 511) / 512 * 512, ib = img_bytes(npad);
+    ActImg img[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        img[j] = act_img(smem + j * ib, npad);
+        if (j < ncol) stage_q8_1_img(p.xq + (int64_t) xrow[j] * p.xq_row_bytes, npad, smem + j * ib, tid, 256);
+    }
+    __syncthreads();
+    const int nblk = p.ncols / 256, lane = tid % LPR;
+    const int row = blockIdx.x * (256 / LPR) + tid / LPR;
+    const int64_t row_bytes = (int64_t) nblk * BB;
+    float acc[NC], accg[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) acc[j] = accg[j] = 0.0f;
+    if (row < p.nrows) {
+        for (int qi = lane; qi < 4 * nblk; qi += LPR) {
+            const int bb = qi >> 2, qt = qi & 3;
+            const uint8_t *ba = wa + row * row_bytes + (int64_t) bb * BB;
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                if (j < ncol) {
+                    acc[j] += quarter_dot<T, Any2>(ba, img[j], bb, qt);
+                    if constexpr (GLU) accg[j] += quarter_dot<T, Any2>(wb + row * row_bytes + (int64_t) bb * BB, img[j], bb, qt);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        float v = lanes_sum<LPR>(acc[j]);
+        if constexpr (GLU) {
+            const float gsum = lanes_sum<LPR>(accg[j]);
+            v += 0.0f;  // fused-GLU epilogue with zero biases (reference src/ggml/ggml_mmvq.cu:240-247)
+            v *= silu(gsum + 0.0f);
+        }
+        if (lane == 0 && j < ncol && row < p.nrows) out[j][row] = v;
+    }
+}
+
+template <int T, int NC, bool GLU> int launch_q(const MmvqParams &p, int n_chan, hipStream_t st) {
+    const int npad = (int) host::pad512(p.ncols);
+    const size_t lds = (size_t) NC * img_bytes(npad);
+    if (lds > 160 * 1024) return host::set_error(host::ERR_SHAPE, "mmvq: ncols %d too large for LDS staging", p.ncols);
+    if (p.ncols / 256 * 4 <= 16) {
+        hipLaunchKernelGGL((k_mmvq_q<T, 16, NC, GLU>), dim3((unsigned) ((p.nrows + 15) / 16), (unsigned) n_chan),
+                           dim3(256), lds, st, p);
+    } else {
+        hipLaunchKernelGGL((k_mmvq_q<T, 32, NC, GLU>), dim3((unsigned) ((p.nrows + 7) / 8), (unsigned) n_chan),
+                           dim3(256), lds, st, p);
+    }
+    return host::check_launch("mmvq (quarters)");
+}
+
 template <int NC, bool GLU> int launch_type(int type, const MmvqParams &p, int n_chan, hipStream_t st) {
     switch (type) {
         case T_Q3_K: return launch_nc<T_Q3_K, NC, GLU>(p, n_chan, st);
         case T_Q4_K: return launch_nc<T_Q4_K, NC, GLU>(p, n_chan, st);
         case T_Q5_K: return launch_nc<T_Q5_K, NC, GLU>(p, n_chan, st);
         case T_Q6_K: return launch_nc<T_Q6_K, NC, GLU>(p, n_chan, st);
+        case T_Q8_0: return launch_q<T_Q8_0, NC, GLU>(p, n_chan, st);
         default: return host::set_error(host::ERR_TYPE, "mmvq: ggml type %d not supported", type);
     }
 }
 
 int check_shape(int type, int64_t ncols, int64_t nrows) {
-    if (!host::is_kquant(type)) return host::set_error(host::ERR_TYPE, "mmvq: ggml type %d not supported", type);
+    if (!host::is_supported(type)) return host::set_error(host::ERR_TYPE, "mmvq: ggml type %d not supported", type);
     if (ncols <= 0 || ncols % 256 || nrows <= 0 || ncols > (1 << 20) || nrows > (1 << 24))
         return host::set_error(host::ERR_SHAPE, "mmvq: ncols %lld must be a positive multiple of 256, nrows %lld > 0",
                                (long long) ncols, (long long) nrows);
@@ -398,6 +497,6 @@ void mmvq_experts(ggml_type type, const char *const *table, size_t off, int64_t 
     host::abort_on_error(impl::mmvq_experts(type, table, off, ncols, nrows, xq, n_xq, ids, n_ids, dst, stream),
                          "mmvq_experts");
 }
-bool mmvq_supports(ggml_type type) { return host::is_kquant((int) type); }
+bool mmvq_supports(ggml_type type) { return host::is_supported((int) type); }
 
 }  // namespace fns

@@ -1320,6 +1320,9 @@ template <int TQ, int LPR> int launch_gate_up_lds(const LayerArgs &a, size_t lds
     return host::check_launch("moe gate_up (lds)");
 }
 
+// Types that only the quarter kernels decode (the register- and LDS-staged whole-block forms are K-quant only).
+template <int T> constexpr bool kQuarterOnly = T == T_Q8_0;
+
 template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
     const int nblk = a.H / 256;
     if (gate_up_q_fits(a.H, Traits<TQ>::bytes)) {
@@ -1333,6 +1336,9 @@ template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
                                gate_up_q_lds_bytes(a.T, a.H, Traits<TQ>::bytes, kMaxTok), st, a);
         return host::check_launch("moe gate_up (quarters)");
     }
+    if constexpr (kQuarterOnly<TQ>) {
+        return host::set_error(host::ERR_SHAPE, "moe_layer: hidden %d too large for the quarter kernels", a.H);
+    } else {
     const size_t lds = gate_up_lds_bytes(a.T, a.H, Traits<TQ>::bytes, a.T == 1 ? 1 : kMaxTok);
     if (lds) {
         if (nblk <= 2) return launch_gate_up_lds<TQ, 2>(a, lds, st);
@@ -1345,6 +1351,7 @@ template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
         case 2: return launch_gate_up_b<TQ, 2>(a, s.bpl, st);
         case 4: return launch_gate_up_b<TQ, 4>(a, s.bpl, st);
         default: return launch_gate_up_b<TQ, 8>(a, s.bpl, st);
+    }
     }
 }
 
@@ -1373,6 +1380,9 @@ template <int TQ> int dispatch_down(const LayerArgs &a, hipStream_t st) {
                            down_q_lds_bytes(a.T * a.K, a.F), st, a);
         return host::check_launch("moe down_combine (quarters)");
     }
+    if constexpr (kQuarterOnly<TQ>) {
+        return host::set_error(host::ERR_SHAPE, "moe_layer: n_tok * k * inter too large for the quarter kernels");
+    } else {
     const size_t lds = down_lds_bytes(a.T * a.K, a.F, Traits<TQ>::bytes);
     if (lds) {
         if (nblk <= 2) return launch_down_lds<TQ, 2>(a, lds, st);
@@ -1385,6 +1395,7 @@ template <int TQ> int dispatch_down(const LayerArgs &a, hipStream_t st) {
         case 2: return launch_down_b<TQ, 2>(a, s.bpl, st);
         case 4: return launch_down_b<TQ, 4>(a, s.bpl, st);
         default: return launch_down_b<TQ, 8>(a, s.bpl, st);
+    }
     }
 }
 
@@ -1405,6 +1416,7 @@ template <int TGU> const void *fused_fn_by_down(int tdn, bool sh) {
     return nullptr;
 }
 const void *fused_kernel(int tgu, int tdn, bool sh) {
+    if (tgu == T_Q8_0 || tdn == T_Q8_0) return tgu == tdn ? fused_fn<T_Q8_0, T_Q8_0>(sh) : nullptr;
     switch (tgu) {
         case T_Q3_K: return fused_fn_by_down<T_Q3_K>(tdn, sh);
         case T_Q4_K: return fused_fn_by_down<T_Q4_K>(tdn, sh);
@@ -1462,6 +1474,7 @@ int by_type_gate_up(int t, const LayerArgs &a, hipStream_t st) {
         case T_Q4_K: return dispatch_gate_up<T_Q4_K>(a, st);
         case T_Q5_K: return dispatch_gate_up<T_Q5_K>(a, st);
         case T_Q6_K: return dispatch_gate_up<T_Q6_K>(a, st);
+        case T_Q8_0: return dispatch_gate_up<T_Q8_0>(a, st);
     }
     return host::set_error(host::ERR_TYPE, "moe_layer: gate/up type %d not supported", t);
 }
@@ -1472,6 +1485,7 @@ int by_type_down(int t, const LayerArgs &a, hipStream_t st) {
         case T_Q4_K: return dispatch_down<T_Q4_K>(a, st);
         case T_Q5_K: return dispatch_down<T_Q5_K>(a, st);
         case T_Q6_K: return dispatch_down<T_Q6_K>(a, st);
+        case T_Q8_0: return dispatch_down<T_Q8_0>(a, st);
     }
     return host::set_error(host::ERR_TYPE, "moe_layer: down type %d not supported", t);
 }
@@ -1545,13 +1559,13 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
         (L->shexp_inter > 0 && (!L->shexp_gate || !L->shexp_up || !L->shexp_down)))
         return host::set_error(host::ERR_SHAPE, "moe_layer: shared expert: width a multiple of 256 (<= 16384), "
                                                 "gate, up and down given");
-    if (L->shexp_inter > 0 && ((L->shexp_gu_type && !host::is_kquant(L->shexp_gu_type)) ||
-                               (L->shexp_down_type && !host::is_kquant(L->shexp_down_type))))
+    if (L->shexp_inter > 0 && ((L->shexp_gu_type && !host::is_supported(L->shexp_gu_type)) ||
+                               (L->shexp_down_type && !host::is_supported(L->shexp_down_type))))
         return host::set_error(host::ERR_TYPE, "moe_layer: shared expert types %d/%d not supported", L->shexp_gu_type,
                                L->shexp_down_type);
     if (L->router_dtype != 0 && L->router_dtype != T_BF16)
         return host::set_error(host::ERR_TYPE, "moe_layer: router dtype %d not supported", L->router_dtype);
-    if (!host::is_kquant(L->gu_type) || !host::is_kquant(L->down_type))
+    if (!host::is_supported(L->gu_type) || !host::is_supported(L->down_type))
         return host::set_error(host::ERR_TYPE, "moe_layer: expert types %d/%d not supported", L->gu_type, L->down_type);
     const size_t lds_down = (size_t) n_tok * L->k * img_bytes((int) host::pad512(L->inter));
     if (lds_down > 64 * 1024)

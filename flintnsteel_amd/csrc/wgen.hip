@@ -385,6 +385,20 @@ __device__ void quant_q3_K(const float *x, uint8_t *y) {
     for (int i = 0; i < 110; ++i) y[i] = blk[i];
 }
 
+// ggml quantize_row_q8_0_ref over 8 consecutive blocks of 32: d = amax / 127, q = roundf(x / d) (x * (1/d), as ggml).
+__device__ void quant_q8_0(const float *x, uint8_t *y) {
+    for (int b = 0; b < 8; ++b) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[32 * b + i]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint32_t dh = float_to_half(d);
+        y[34 * b] = dh & 0xff;
+        y[34 * b + 1] = dh >> 8;
+        for (int i = 0; i < 32; ++i) y[34 * b + 2 + i] = (uint8_t) (int8_t) roundf(x[32 * b + i] * id);
+    }
+}
+
 template <int T>
 __global__ __launch_bounds__(64) void k_quantize_blocks(const float *__restrict__ x, uint8_t *__restrict__ y,
                                                         int64_t nblocks) {
@@ -396,6 +410,7 @@ __global__ __launch_bounds__(64) void k_quantize_blocks(const float *__restrict_
     if constexpr (T == T_Q5_K) quant_q5_K(xb, yb);
     if constexpr (T == T_Q6_K) quant_q6_K(xb, yb);
     if constexpr (T == T_Q3_K) quant_q3_K(xb, yb);
+    if constexpr (T == T_Q8_0) quant_q8_0(xb, yb);
 }
 
 }  // namespace
@@ -412,7 +427,7 @@ int fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, float mea
 }
 
 int quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, hipStream_t st) {
-    if (!host::is_kquant(type)) return host::set_error(host::ERR_TYPE, "quantize_weights: type %d not supported", type);
+    if (!host::is_supported(type)) return host::set_error(host::ERR_TYPE, "quantize_weights: type %d not supported", type);
     if (!x || !out || nrows < 0 || ncols <= 0 || ncols % 256)
         return host::set_error(host::ERR_SHAPE, "quantize_weights: ncols must be a positive multiple of 256");
     const int64_t nb = nrows * (ncols / 256);
@@ -423,6 +438,7 @@ int quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t
         case T_Q4_K: hipLaunchKernelGGL(k_quantize_blocks<T_Q4_K>, g, dim3(64), 0, st, x, (uint8_t *) out, nb); break;
         case T_Q5_K: hipLaunchKernelGGL(k_quantize_blocks<T_Q5_K>, g, dim3(64), 0, st, x, (uint8_t *) out, nb); break;
         case T_Q6_K: hipLaunchKernelGGL(k_quantize_blocks<T_Q6_K>, g, dim3(64), 0, st, x, (uint8_t *) out, nb); break;
+        case T_Q8_0: hipLaunchKernelGGL(k_quantize_blocks<T_Q8_0>, g, dim3(64), 0, st, x, (uint8_t *) out, nb); break;
     }
     return host::check_launch("quantize_weights");
 }

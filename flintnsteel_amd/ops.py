@@ -12,11 +12,12 @@ import torch
 
 from ._lib import call, lib
 
-Q8_1, Q3_K, Q4_K, Q5_K, Q6_K = 9, 11, 12, 13, 14
+Q8_0, Q8_1, Q3_K, Q4_K, Q5_K, Q6_K = 8, 9, 11, 12, 13, 14
 F32, BF16 = 0, 30
 GATING_SOFTMAX, GATING_SIGMOID = 0, 1
-BLOCK_BYTES = {Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
-TYPE_NAMES = {Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+# bytes per 256 values of a row (a K-quant block; 8 Q8_0 blocks)
+BLOCK_BYTES = {Q8_0: 272, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+TYPE_NAMES = {Q8_0: "Q8_0", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
 
 
 def _p(t: torch.Tensor | None):

@@ -98,7 +98,15 @@ void mmq_experts(ggml_type type, const char *const *table, size_t off, int64_t n
                  const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
                  MmqIdsScratch &s, float *dst, hipStream_t stream);
 
-// Quantized types this path accepts (Q3_K added for the configs' UD-Q3_K_XL-like mix).
+// FlashAttention over a prefill chunk: declared with the reference's signature so that Engine::prefill_chunk, which
+// includes this header, keeps compiling; attention is not part of the MoE FFN path and libfns_hip.so does NOT define
+// it: the engine keeps linking its own implementation (the reference's src/ggml/ggml_fattn.cu).
+// out[t][h] = softmax(scale * q[t][h] . K^T + mask[t]; sink_h) . V. Reference: include/fns/ggml_kernels.h:71-77.
+void flash_attn_prefill(const float *q, const void *kc, const void *vc, const void *mask, const float *sinks,
+                        float *out, int n_tok, int n_kv, int n_head, int n_head_kv, int head_dim, float scale,
+                        hipStream_t stream);
+
+// Quantized types this path accepts: Q8_0 and the K-quants (Q3_K added for the configs' UD-Q3_K_XL-like mix).
 // Reference: include/fns/ggml_kernels.h:79-80, src/ggml/ggml_mmvq.cu:403-411.
 bool mmvq_supports(ggml_type type);
 

@@ -30,7 +30,7 @@ def test_q8_1_row_bytes_padding():
 
 def test_supported_types():
     L = _lib.lib()
-    assert [t for t in range(40) if L.fns_hip_mmvq_supports(t)] == [11, 12, 13, 14]
+    assert [t for t in range(40) if L.fns_hip_mmvq_supports(t)] == [8, 11, 12, 13, 14]
 
 
 def _buf():
@@ -39,7 +39,7 @@ def _buf():
 
 def test_unsupported_type_is_rejected():
     L = _lib.lib()
-    rc = L.fns_hip_mmvq(8, _buf(), 2048, 16, _buf(), _buf(), 1, None)
+    rc = L.fns_hip_mmvq(10, _buf(), 2048, 16, _buf(), _buf(), 1, None)  # Q2_K: not accepted
     assert rc == -1
     assert b"not supported" in L.fns_hip_last_error()
     with pytest.raises(_lib.FnsError, match="not supported"):
@@ -104,5 +104,5 @@ def test_moe_block_extras_host_checks():
     assert L.fns_hip_moe_layer(ctypes.byref(d), ptr, None, ptr, 1, ctypes.addressof(ws), with_sh4, None) == -2
     d.shexp_inter, d.shexp_down = 1024, None  # down missing
     assert L.fns_hip_moe_layer(ctypes.byref(d), ptr, None, ptr, 1, ctypes.addressof(ws), with_sh4, None) == -2
-    d.shexp_down, d.shexp_gu_type = ptr, 8  # Q8_0: not a K-quant
+    d.shexp_down, d.shexp_gu_type = ptr, 10  # Q2_K: not accepted
     assert L.fns_hip_moe_layer(ctypes.byref(d), ptr, None, ptr, 1, ctypes.addressof(ws), with_sh4, None) == -1

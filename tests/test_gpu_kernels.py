@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 H, F = 2048, 768
 NE = 16
 REF_IDS = [0, 255, 17, 128, 3, 200, 64, 9]
-TYPES = [orc.Q3_K, orc.Q4_K, orc.Q5_K, orc.Q6_K]
+TYPES = [orc.Q8_0, orc.Q3_K, orc.Q4_K, orc.Q5_K, orc.Q6_K]
 
 
 @pytest.fixture(scope="module")
@@ -151,7 +151,7 @@ def test_table_equals_contiguous_bitwise(ops, down_mats, gate_up_mats, qtype):
     assert np.array_equal(host(a), host(b))
 
 
-@pytest.mark.parametrize("qtype", [orc.Q4_K, orc.Q6_K])
+@pytest.mark.parametrize("qtype", [orc.Q4_K, orc.Q6_K, orc.Q8_0])
 def test_mmvq_columns_bit_identical(ops, down_mats, qtype):
     """Column c of a 4-column launch == the single-column launch (reference src/ggml/ggml_mmvq.cu:25-27)."""
     w = down_mats[qtype][1].reshape(H, -1)

@@ -73,6 +73,7 @@ CASES = {
     "cfg1_q3k_q5k": (11, 13, 0),
     "cfg3_q4k_q6k": (12, 14, 0),
     "flint_sigmoid": (12, 14, 1),
+    "q8_0": (8, 8, 0),         # the reference's dense / Q8_0 expert type (src/ggml/ggml_mmvq.cu:377,405)
 }
 
 
@@ -109,9 +110,10 @@ def test_moe_layer_decode(ops, synth, case):
     assert_close(out, out_ind, "combined out (independent chain)", 1e-3, 1e-4)
 
 
-def test_moe_layer_verify_columns(ops, synth):
+@pytest.mark.parametrize("qtype", [12, 8])
+def test_moe_layer_verify_columns(ops, synth, qtype):
     """Config 2: 4 tokens with compacted experts; each column is bit-identical to its batch-1 run."""
-    layer = synth.build_layer(H, F, NE, K, 12, 12, SEED, layer=3)
+    layer = synth.build_layer(H, F, NE, K, qtype, qtype, SEED, layer=3)
     x4 = synth.activations(4, H, SEED, layer=9)
     ws4 = layer.workspace(4)
     out4 = host(layer(x4, ws=ws4))
