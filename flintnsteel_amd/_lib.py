@@ -49,6 +49,8 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_moe_layer": [_P, _P, _P, _P, _I, _P, _SZ, _P],
     "fns_hip_moe_layer_profiled": [_P, _P, _P, _P, _I, _P, _SZ, _P, _P],
     "fns_hip_moe_layer_stage": [_P, _I, _P, _P, _P, _I, _P, _SZ, _P],
+    "fns_hip_moe_layer_noalloc": [_P, _P, _P, _P, _I, _P],
+    "fns_hip_moe_noalloc_max_bytes": [],
     "fns_hip_mmq_q8_1_bytes": [_I64, _I64],
     "fns_hip_mmq_bounds_bytes": [_I64],
     "fns_hip_mmq": [_I, _P, _I64, _I64, _P, _I64, _P, _P, _P],
@@ -65,6 +67,7 @@ _RESTYPE = {
     "fns_hip_q8_1_row_bytes": _SZ,
     "fns_hip_mmq_q8_1_bytes": _SZ,
     "fns_hip_mmq_bounds_bytes": _SZ,
+    "fns_hip_moe_noalloc_max_bytes": _SZ,
 }
 
 _lib = None

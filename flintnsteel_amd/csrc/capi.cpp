@@ -115,6 +115,13 @@ int fns_hip_moe_layer_profiled(const FnsMoeLayer *layer, const float *x, const f
     return impl::moe_layer(layer, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream), events);
 }
 
+int fns_hip_moe_layer_noalloc(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int n_tok,
+                              void *stream) {
+    return impl::moe_layer_noalloc(layer, x, x_resid, out, n_tok, S(stream));
+}
+
+size_t fns_hip_moe_noalloc_max_bytes(void) { return impl::moe_noalloc_max_bytes(); }
+
 int fns_hip_moe_layer_stage(const FnsMoeLayer *layer, int stage, const float *x, const float *x_resid, float *out,
                             int n_tok, void *workspace, size_t workspace_bytes, void *stream) {
     return impl::moe_layer_stage(layer, stage, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream));

@@ -47,6 +47,8 @@ int count_routes(const int32_t *ids, uint32_t *counts, int k, hipStream_t st);
 int moe_workspace_layout(const FnsMoeLayer *L, int n_tok, size_t *offsets, size_t *total);
 int moe_layer(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int n_tok, void *ws,
               size_t ws_bytes, hipStream_t st, void *const *events = nullptr);
+int moe_layer_noalloc(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int n_tok, hipStream_t st);
+size_t moe_noalloc_max_bytes();
 int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float *x_resid, float *out, int n_tok,
                     void *ws, size_t ws_bytes, hipStream_t st);
 

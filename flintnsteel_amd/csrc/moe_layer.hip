@@ -1718,6 +1718,59 @@ int moe_layer(const FnsMoeLayer *L, const float *x, const float *x_resid, float 
     return mark(3);
 }
 
+// ---- no-allocation variant -------------------------------------------------------------------------------------------
+// fns_hip_moe_layer_noalloc takes its workspace from this file-scope device array instead of a caller buffer, for
+// callers that cannot allocate (HIP graph capture, serving loops that forbid hipMalloc). Each GPU the library runs on
+// holds its own copy until the process ends. In host code `scratch` is only a stand-in symbol: its device address is
+// looked up once per device with hipGetSymbolAddress and kept in g_scratch_ptr, and only that address reaches kernels.
+// Every call on one GPU shares the array (calls that overlap on one GPU race; order them on one stream).
+constexpr size_t kScratchBytes = (size_t) 4 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices];
+
+__global__ void k_zero_words(uint32_t *p, size_t n) {
+    for (size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t) gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// The scratch address on the current device; the first call on a device also clears the array (a kernel on `st`,
+// ordered before the call's own kernels; a fill kernel rather than a memset node, so a captured first call replays
+// correctly). The layer kernels keep the arrival counter consistent from call to call after that.
+int scratch_of_device(hipStream_t st, uint8_t **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return host::set_error(host::ERR_LAUNCH, "moe_layer_noalloc: no current HIP device");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return host::set_error(host::ERR_LAUNCH, "moe_layer_noalloc: hipGetSymbolAddress(scratch): %s",
+                                   hipGetErrorString(e));
+        hipLaunchKernelGGL(k_zero_words, dim3(256), dim3(256), 0, st, (uint32_t *) ptr, kScratchBytes / 4);
+        FNS_TRY(host::check_launch("moe_layer_noalloc: clearing the scratch"));
+        g_scratch_ptr[dev] = (uint8_t *) ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return host::OK;
+}
+
+int moe_layer_noalloc(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int n_tok,
+                      hipStream_t st) {
+    size_t need = 0;
+    FNS_TRY(moe_workspace_layout(L, n_tok, nullptr, &need));
+    if (need > kScratchBytes)
+        return host::set_error(host::ERR_NOMEM, "moe_layer_noalloc: the layer needs %zu workspace bytes, more than the "
+                                                "%zu-byte device scratch", need, kScratchBytes);
+    uint8_t *ws = nullptr;
+    FNS_TRY(scratch_of_device(st, &ws));
+    return moe_layer(L, x, x_resid, out, n_tok, ws, kScratchBytes, st);
+}
+
+size_t moe_noalloc_max_bytes() { return kScratchBytes; }
+
 int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float *x_resid, float *out, int n_tok,
                     void *ws, size_t ws_bytes, hipStream_t st) {
     LayerArgs a;

@@ -140,6 +140,16 @@ int fns_hip_moe_layer(const FnsMoeLayer *layer, const float *x, const float *x_r
  * gate/up kernel, before the down kernel and after it: per-kernel durations for measurement. */
 int fns_hip_moe_layer_profiled(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int n_tok,
                                void *workspace, size_t workspace_bytes, void *const *events, void *stream);
+/* No counterpart in the reference: the same layer as fns_hip_moe_layer for callers that cannot allocate (code under HIP
+ * graph capture, serving loops or harnesses that forbid hipMalloc). The workspace is a device array inside the
+ * library, fns_hip_moe_noalloc_max_bytes() bytes (4 MiB) per GPU, held until the process ends; a layer whose
+ * fns_hip_moe_workspace_layout total exceeds it is rejected with FNS_ERR_NOMEM. The call allocates nothing. Every call
+ * on one GPU shares that array and leaves its intermediates there (as fns_hip_moe_layer leaves them in its
+ * workspace): calls that overlap on one GPU race, so order them (one stream). The first call on a device clears the
+ * array with a kernel on `stream`. */
+int fns_hip_moe_layer_noalloc(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int n_tok,
+                              void *stream);
+size_t fns_hip_moe_noalloc_max_bytes(void);
 /* One of the three kernels of fns_hip_moe_layer (stage 0 router + Q8_1 of x, 1 routing + gate/up + SwiGLU,
  * 2 F16 guard + Q8_1 of act + down + combine), each reading what the previous stage left in the workspace:
  * per-stage tracing (the reference's FNS_TRACE nodes, src/engine.cu:590-599) and per-kernel timing. */
