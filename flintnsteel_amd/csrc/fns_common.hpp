@@ -19,6 +19,16 @@
 
 #include "fns_lanes.hpp"
 
+// Phase-timing hooks. The library build defines them as no-ops; a tuning build passes -DFNS_PROBE_HEADER=<file> to
+// record wall-clock marks at these points instead.
+#ifdef FNS_PROBE_HEADER
+#include FNS_PROBE_HEADER
+#else
+#define FNS_MARK(k, wg, i) ((void) (wg))
+#define MMQ_MARK(i) ((void) 0)
+#define MMQ_NOTE(v) ((void) 0)
+#endif
+
 namespace fns::dev {
 
 constexpr int kWave = 64;

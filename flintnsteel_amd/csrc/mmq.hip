@@ -504,12 +504,6 @@ struct MmqLds {
     int (&grp)[4];  // the group's expert, first sorted row and row count
 };
 
-#ifdef FNS_MPROBE
-__device__ unsigned long long g_mprobe[2][8192][14];
-#define MMQ_MARK(i) do { if (threadIdx.x == 0) g_mprobe[GLU][blockIdx.x + gridDim.x * blockIdx.y][i] = wall_clock64(); } while (0)
-#else
-#define MMQ_MARK(i) do { } while (0)
-#endif
 // Group g of the launch's list (NT = 2: the 64-row groups and remainders > 32 rows; NT = 1: the expert's <= 32-row
 // remainder), weight row block wb.
 template <int T, bool GLU, int NT>
@@ -559,9 +553,7 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
     }
     if (cnt <= 0) return;
     MMQ_MARK(0);
-#ifdef FNS_MPROBE
-    if (threadIdx.x == 0) g_mprobe[GLU][blockIdx.x + gridDim.x * blockIdx.y][13] = NT * 1000 + cnt;
-#endif
+    MMQ_NOTE(NT * 1000 + cnt);
     for (int i = tid; i < ROWS; i += kMmqThreads) {
         const int q = seg + min(i, cnt - 1);
         sh_src[i] = a.src ? a.src[q] : q;
@@ -915,19 +907,6 @@ int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st)
     return host::check_launch("mmq");
 }
 
-#ifdef FNS_MPROBE
-}  // namespace
-}  // namespace fns
-extern "C" int fns_mprobe_read(void *host) {
-    return (int) hipMemcpyFromSymbol(host, HIP_SYMBOL(fns::g_mprobe), sizeof(fns::g_mprobe));
-}
-extern "C" int fns_mprobe_clear() {
-    static unsigned long long z[2][8192][14];
-    return (int) hipMemcpyToSymbol(HIP_SYMBOL(fns::g_mprobe), z, sizeof(z));
-}
-namespace fns {
-namespace {
-#endif
 int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
     if (!host::is_kquant(type)) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
     if (ncols <= 0 || ncols % 256 || nrows <= 0 || nrows % kMmqRows || ncols > 65536)

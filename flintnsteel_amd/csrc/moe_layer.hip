@@ -36,19 +36,6 @@ namespace fns {
 
 using namespace fns::dev;
 
-// Phase timestamps for tuning builds (-DFNS_PROBE): FNS_MARK(kernel, workgroup, point) records the 100 MHz wall clock.
-#ifdef FNS_PROBE
-__device__ unsigned long long g_probe[3][4096][16];
-#define FNS_MARK(k, wg, i) \
-    do { \
-        if (threadIdx.x == 0) g_probe[k][wg][i] = wall_clock64(); \
-    } while (0)
-#else
-#define FNS_MARK(k, wg, i) \
-    do { \
-        (void) (wg); \
-    } while (0)
-#endif
 
 namespace {
 
@@ -1091,7 +1078,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
 
     // 3. producers: gate/up rows (32 lanes per row, as k_gate_up_q) -> act -> its Q8_1 block, stored device-coherent
     if (producer) {
-        const int lane = tid % 32, rl = 2 * wave + lane64 / 32, row = u * kGuRows + rl;
+        const int lane = tid % 32, rl = 2 * wave + lane64 / 32;
         const ActImg img = act_img(s_x, npad);
         float acc = 0.0f, accg = 0.0f;
         for (int qi = lane; qi < 4 * nbg; qi += 32) {
@@ -1782,12 +1769,3 @@ int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float
 
 }  // namespace fns
 
-#ifdef FNS_PROBE
-extern "C" int fns_probe_read(void *host) {
-    return (int) hipMemcpyFromSymbol(host, HIP_SYMBOL(fns::g_probe), sizeof(fns::g_probe));
-}
-extern "C" int fns_probe_clear() {
-    static unsigned long long z[3][4096][16];
-    return (int) hipMemcpyToSymbol(HIP_SYMBOL(fns::g_probe), z, sizeof(z));
-}
-#endif
