@@ -172,7 +172,8 @@ def cpu_baseline(torch, layer, budget_s: float = 15.0) -> dict:
     import numpy as np
 
     from oracle import oracle as orc
-    nthreads = min(os.cpu_count() or 1, 16)
+    host = host_cpus()
+    nthreads = host["threads"]
     router = layer.router_w.cpu().numpy()
     slots = [layer.slots.expert_bytes(e).cpu().numpy() for e in range(NE)]
     xs = [torch.randn(H, generator=torch.Generator().manual_seed(SEED + i)).numpy().astype(np.float32) for i in range(4)]
@@ -183,11 +184,40 @@ def cpu_baseline(torch, layer, budget_s: float = 15.0) -> dict:
         orc.cpu_moe_layer(*args, xs[n % 4], H, F, K_TOP, nthreads)
         n += 1
         dt = time.perf_counter() - t0
-        if dt > budget_s or n >= 2000:
+        if dt > budget_s:
             break
     return {"value": dt / n * 1e6, "unit": "us/layer", "cores": nthreads, "kind": "port",
-            "sample": f"{n} batch-1 config-0 layers (Q4_K, 128 experts, top-8) with fresh x; OpenMP restatement in "
-                      f"oracle/fns_oracle.c (int8 x K-quant integer dots), not ggml (llama.cpp is not on the box)"}
+            "sample": f"{n} batch-1 config-0 layers (Q4_K, 128 experts, top-8) with fresh x, {dt:.1f} s; OpenMP "
+                      f"restatement in oracle/fns_oracle.c (int8 x K-quant integer dots), not ggml (llama.cpp is not "
+                      f"on the box)", **{k: v for k, v in host.items() if k != "threads"}}
+
+
+def host_cpus() -> dict:
+    """The host's CPU model and counts, and the threads the baseline runs: every CPU this process may use (its
+    affinity mask and cgroup CPU quota), or OMP_NUM_THREADS when the job sets it (the GPU boxes allot 16 cores per
+    GPU that way)."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    threads = affinity if quota is None else max(1, min(affinity, int(quota)))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = int(omp)
+    return {"threads": threads, "cpu_model": model, "host_cpus": os.cpu_count(), "affinity_cpus": affinity,
+            "cgroup_cpu_quota": quota, "omp_num_threads": omp or None}
 
 
 def run_stack(torch, synth, gu: int, dn: int, n_layers: int, n_tok: int, steps: int, warmup: int, seed_base: int,

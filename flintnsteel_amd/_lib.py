@@ -51,12 +51,15 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_moe_layer_stage": [_P, _I, _P, _P, _P, _I, _P, _SZ, _P],
     "fns_hip_moe_layer_noalloc": [_P, _P, _P, _P, _I, _P],
     "fns_hip_moe_noalloc_max_bytes": [],
+    "fns_hip_moe_layer_status": [_P, _I, _P, _I, _P, _P],
+    "fns_hip_moe_set_test_hooks": [_I, _I],
     "fns_hip_mmq_q8_1_bytes": [_I64, _I64],
     "fns_hip_mmq_bounds_bytes": [_I64],
     "fns_hip_mmq": [_I, _P, _I64, _I64, _P, _I64, _P, _P, _P],
     "fns_hip_mmq_experts": [_I, _P, _SZ, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P, _P],
     "fns_hip_mmq_compact": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P],
     "fns_hip_moe_prefill_workspace": [_P, _I64, _P, _P],
+    "fns_hip_moe_prefill_section": [_P, _I64, _I, _P, _P],
     "fns_hip_moe_prefill": [_P, _P, _P, _P, _I64, _P, _SZ, _P],
     "fns_hip_fill_normal": [_P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F, _F, _P],
     "fns_hip_quantize_weights": [_I, _P, _P, _I64, _I64, _P],

@@ -122,6 +122,15 @@ int fns_hip_moe_layer_noalloc(const FnsMoeLayer *layer, const float *x, const fl
 
 size_t fns_hip_moe_noalloc_max_bytes(void) { return impl::moe_noalloc_max_bytes(); }
 
+int fns_hip_moe_layer_status(const FnsMoeLayer *layer, int n_tok, void *workspace, int clear, uint32_t *status,
+                             void *stream) {
+    return impl::moe_layer_status(layer, n_tok, workspace, clear, status, S(stream));
+}
+
+int fns_hip_moe_set_test_hooks(int spin_limit, int withhold_arrivals) {
+    return impl::moe_set_test_hooks(spin_limit, withhold_arrivals);
+}
+
 int fns_hip_moe_layer_stage(const FnsMoeLayer *layer, int stage, const float *x, const float *x_resid, float *out,
                             int n_tok, void *workspace, size_t workspace_bytes, void *stream) {
     return impl::moe_layer_stage(layer, stage, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream));
@@ -161,6 +170,10 @@ int fns_hip_mmq_compact(const int32_t *ids, int64_t n_tok, int64_t n_used, int64
 
 int fns_hip_moe_prefill_workspace(const FnsMoeLayer *layer, int64_t n_tok, size_t *offsets, size_t *total_bytes) {
     return impl::moe_prefill_workspace(layer, n_tok, offsets, total_bytes);
+}
+
+int fns_hip_moe_prefill_section(const FnsMoeLayer *layer, int64_t n_tok, int section, size_t *offset, size_t *bytes) {
+    return impl::moe_prefill_section(layer, n_tok, section, offset, bytes);
 }
 
 int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int64_t n_tok,

@@ -242,6 +242,18 @@ __global__ __launch_bounds__(256) void k_quant_image(const float *__restrict__ x
     q8_split8<true>(v, out + (size_t) row * img_row_bytes, ncols, col, true);
 }
 
+// F16-guard form: only the rows whose guard scale is not 1 are re-quantised (the others already hold the image of
+// the same values, written by the GEMM epilogue); grid as k_quant_image.
+__global__ __launch_bounds__(256) void k_quant_image_scaled(const float *__restrict__ x, const float *__restrict__ escale,
+                                                            int ncols, uint8_t *__restrict__ out, int64_t img_row_bytes) {
+    const int row = blockIdx.y, col = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (escale[row] == 1.0f || col >= ncols) return;
+    const float *src = x + (size_t) row * ncols + col;
+    const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    q8_split8<true>(v, out + (size_t) row * img_row_bytes, ncols, col, true);
+}
+
 // Router GEMM tiles and the split activation image of the same rows in one launch (the two only read x): workgroups
 // [0, n_rt) are router tiles (tile (id % tiles_x, id / tiles_x)), the rest quantise two 2048-column pieces of x each,
 // as k_quant_image does, so the image is built on the CUs the router tiles leave free.
@@ -844,9 +856,9 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
             const float *src = (const float *) (blk < 2 ? sh_a0 : sh_a1) + i * kAct + 32 * (blk & 1) + 8 * q;
             const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
             const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            // v / d as v * (1 / d): act itself is an fp32 GEMM result, not bit-comparable with the reference's, so
-            // the quotient's last-ulp rounding carries no parity
-            q8_split8<false>(v, a.out_pack + (size_t) sh_dst[i] * a.out_img, a.nrows, col, live);
+            // the reference's Q8_1 arithmetic (q = roundf(v / d), IEEE division): the same codes as the quantiser of
+            // the f32 act rows would give
+            q8_split8<true>(v, a.out_pack + (size_t) sh_dst[i] * a.out_img, a.nrows, col, live);
             if (live && a.act_out) {
                 float *ao = a.act_out + (size_t) sh_dst[i] * a.nrows + col;
                 *(float4 *) ao = x0;
@@ -928,6 +940,16 @@ int mmq_quant_image(const float *x, int64_t ncols, int64_t rows, void *xpack, hi
     hipLaunchKernelGGL(k_quant_image, dim3((unsigned) ((ncols + 2047) / 2048), (unsigned) rows), dim3(256), 0, st, x, (int) ncols,
                        (uint8_t *) xpack, (int64_t) mmq_image_bytes(ncols));
     return host::check_launch("mmq quantize");
+}
+
+int mmq_quant_image_scaled(const float *x, const float *escale, int64_t ncols, int64_t rows, void *xpack,
+                           hipStream_t st) {
+    if (!x || !escale || !xpack || ncols <= 0 || ncols % 256 || ncols > 65536 || rows < 0 || rows > 65535)
+        return host::set_error(host::ERR_SHAPE, "mmq quantize: bad arguments");
+    if (rows == 0) return host::OK;
+    hipLaunchKernelGGL(k_quant_image_scaled, dim3((unsigned) ((ncols + 2047) / 2048), (unsigned) rows), dim3(256), 0, st,
+                       x, escale, (int) ncols, (uint8_t *) xpack, (int64_t) mmq_image_bytes(ncols));
+    return host::check_launch("mmq quantize (guarded rows)");
 }
 
 int mmq_compact(const int32_t *ids, int64_t n_tok, int64_t k, int64_t n_expert, int64_t x_rows_per_tok,
@@ -1028,6 +1050,17 @@ void prefill_sizes(const FnsMoeLayer *L, int64_t T, size_t *sz) {
     sz[14] = fs ? (size_t) T * L->hidden * 4 : 0;                                  // shared-expert output
 }
 }  // namespace
+
+int moe_prefill_section(const FnsMoeLayer *L, int64_t n_tok, int section, size_t *offset, size_t *bytes) {
+    FNS_TRY(moe_prefill_workspace(L, n_tok, nullptr, nullptr));
+    if (section < 0 || section >= kPrefillSections) return host::set_error(host::ERR_SHAPE, "moe_prefill: no section %d", section);
+    size_t sz[kPrefillSections], off = 0;
+    prefill_sizes(L, n_tok, sz);
+    for (int i = 0; i < section; ++i) off += (sz[i] + 255) / 256 * 256;
+    if (offset) *offset = off;
+    if (bytes) *bytes = sz[section];
+    return host::OK;
+}
 
 int moe_prefill_workspace(const FnsMoeLayer *L, int64_t n_tok, size_t *offsets, size_t *total) {
     if (!L || n_tok < 1 || n_tok * L->k > 65536)
@@ -1135,7 +1168,7 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
                              st));
     if (L->guard) {  // whole-row amax: a second pass over the f32 act rows (reference src/kernels.cu:534-552)
         FNS_TRY(amax_guard(act, escale, L->inter, (int) P, st));
-        FNS_TRY(mmq_quant_image(act, L->inter, P, sec[4], st));
+        FNS_TRY(mmq_quant_image_scaled(act, escale, L->inter, P, sec[4], st));
     }
     // down: one act row per (token, slot), in the same expert order as gate/up: the sorted rows are the pairs
     // themselves (activation row = output row = p), so the gate/up sort is reused with ids_dst as the source list

@@ -75,6 +75,8 @@ struct LayerArgs {
     int *chan;            // n_tok > 1: [kMaxCh][kChanInts] channel table, then n_distinct, then the router arrival count
     int64_t xq_row_bytes;
     int fused;            // the shape fits the fused kernel (n_tok = 1)
+    int spin_limit;       // fused kernel: polls of the release flag before a workgroup gives up
+    int withhold;         // test hook: arrivals each producer group withholds (> 0: the release never comes)
     const float *sh;      // [T][H] shared-expert output added in the combine, or null
     const float *norm_w;  // [H] RMSNorm weights, or null: the router kernel normalises x first
     float norm_eps;
@@ -981,6 +983,7 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
 // two-kernel path, so results are the same bit for bit.
 constexpr int kFusedRows = 8;
 constexpr int kSpinLimit = 1 << 16;
+constexpr uint32_t kStatusTimeout = 1u;  // FNS_STATUS_EXCHANGE_TIMEOUT
 constexpr int kCpolDevice = 16;  // cache-policy bits of a device-scope (sc1) load: not served from a stale L2 line
 
 __device__ __forceinline__ void store_dev(float *p, float v) {
@@ -1136,7 +1139,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         int *sy = a.sync;
         if (producer) {
             const int g = blockIdx.x % kSyncGroups;
-            const int members = (nprod - g + kSyncGroups - 1) / kSyncGroups;
+            const int members = (nprod - g + kSyncGroups - 1) / kSyncGroups + a.withhold;
             const int groups = nprod < kSyncGroups ? nprod : kSyncGroups;
             if (__hip_atomic_fetch_add(sy + g * kSyncStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                     members - 1 &&
@@ -1153,8 +1156,10 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         const int *flag = sy + (kSyncGroups + 1 + blockIdx.x % kSyncGroups) * kSyncStride;
         int spins = 0;
         while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-            if (++spins > kSpinLimit) {
+            if (++spins > a.spin_limit) {  // give up: outputs NaN, the sticky status word says why
                 s_fail = 1;
+                __hip_atomic_fetch_or((unsigned *) (a.sync + kSyncLines * kSyncStride), kStatusTimeout, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
             __builtin_amdgcn_s_sleep(4);
@@ -1497,7 +1502,7 @@ void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     sizes[7] = ch * img_bytes((int) fpad) + (L->shexp_inter > 0 ? img_bytes((int) host::pad512(L->shexp_inter)) : 0);
     sizes[8] = ch * (fpad / 32) * 4;
     sizes[9] = ch * 8;
-    sizes[10] = (size_t) kSyncLines * kSyncStride * 4;
+    sizes[10] = (size_t) (kSyncLines + 1) * kSyncStride * 4;  // + the status line (not cleared per call)
     sizes[11] = (size_t) (kMaxCh * kChanInts + 2) * 4;
     const size_t fs = L->shexp_inter > 0 ? (size_t) L->shexp_inter : 0;
     sizes[12] = 0;  // (unused: the router kernel applies the RMSNorm)
@@ -1526,6 +1531,17 @@ int moe_workspace_layout(const FnsMoeLayer *L, int n_tok, size_t *offsets, size_
         off += align256(sizes[i]);
     }
     if (total) *total = off;
+    return host::OK;
+}
+
+// Test hooks (fns_hip_moe_set_test_hooks): the fused kernel's poll limit and withheld arrivals for the calls that
+// follow. Set them only while no other thread launches layers.
+static int g_spin_limit = kSpinLimit, g_withhold = 0;
+
+int moe_set_test_hooks(int spin_limit, int withhold) {
+    if (spin_limit < 0 || withhold < 0) return host::set_error(host::ERR_SHAPE, "moe_set_test_hooks: negative value");
+    g_spin_limit = spin_limit ? spin_limit : kSpinLimit;
+    g_withhold = withhold;
     return host::OK;
 }
 
@@ -1595,6 +1611,8 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     a.blk_amax = (float *) sec[8];
     a.dptr = (const uint8_t **) sec[9];
     a.sync = (int *) sec[10];
+    a.spin_limit = g_spin_limit;
+    a.withhold = g_withhold;
     a.chan = (int *) sec[11];
     a.xq_row_bytes = host::q8_1_row_bytes(L->hidden);
     // the shared expert rides in the fused kernel when it has the routed types and the shape still fits
@@ -1757,6 +1775,27 @@ int moe_layer_noalloc(const FnsMoeLayer *L, const float *x, const float *x_resid
 }
 
 size_t moe_noalloc_max_bytes() { return kScratchBytes; }
+
+// The sticky status word of a workspace (ws null: this device's no-allocation scratch), read after the stream's work
+// so far has completed; clear: zero it afterwards (a kernel on `st`).
+int moe_layer_status(const FnsMoeLayer *L, int n_tok, void *ws, int clear, uint32_t *status, hipStream_t st) {
+    if (!status) return host::set_error(host::ERR_SHAPE, "moe_layer_status: null status");
+    size_t sizes[kSections];
+    FNS_TRY(moe_workspace_layout(L, n_tok, nullptr, nullptr));
+    section_sizes(L, n_tok, sizes);
+    size_t off = 0;
+    for (int i = 0; i < 10; ++i) off += align256(sizes[i]);
+    uint8_t *base = (uint8_t *) ws;
+    if (!base) FNS_TRY(scratch_of_device(st, &base));
+    uint32_t *word = (uint32_t *) (base + off) + kSyncLines * kSyncStride;
+    if (hipMemcpyAsync(status, word, 4, hipMemcpyDeviceToHost, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+        return host::set_error(host::ERR_LAUNCH, "moe_layer_status: reading the status word failed");
+    if (clear) {
+        hipLaunchKernelGGL(k_zero_words, dim3(1), dim3(64), 0, st, word, (size_t) 1);
+        FNS_TRY(host::check_launch("moe_layer_status: clearing"));
+    }
+    return host::OK;
+}
 
 int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float *x_resid, float *out, int n_tok,
                     void *ws, size_t ws_bytes, hipStream_t st) {

@@ -292,6 +292,12 @@ class MoeLayer:
         call("fns_hip_moe_layer", ctypes.byref(self.desc), _p(x), _p(x_resid), _p(out), n_tok, _p(ws), ws.numel(), _s())
         return out
 
+    def status(self, ws: torch.Tensor | None, n_tok: int = 1, clear: bool = False) -> int:
+        """The workspace's sticky status word (FNS_STATUS_* bits; 0: every call so far completed its exchange)."""
+        st = ctypes.c_uint32()
+        call("fns_hip_moe_layer_status", ctypes.byref(self.desc), n_tok, _p(ws), int(clear), ctypes.byref(st), _s())
+        return st.value
+
     def stage(self, stage: int, x: torch.Tensor, out: torch.Tensor, ws: torch.Tensor,
               x_resid: torch.Tensor | None = None) -> None:
         """Launch one of the layer's three kernels (0 router, 1 gate/up, 2 down + combine)."""
@@ -349,16 +355,28 @@ class MoePrefill:
              ws.numel(), _s())
         return out
 
+    def section(self, n_tok: int, index: int) -> tuple[int, int]:
+        """(byte offset, bytes) of workspace section `index` (fns_hip_moe_prefill_section)."""
+        off, size = ctypes.c_size_t(), ctypes.c_size_t()
+        call("fns_hip_moe_prefill_section", ctypes.byref(self.layer.desc), n_tok, index, ctypes.byref(off),
+             ctypes.byref(size))
+        return off.value, size.value
+
     def trace(self, ws: torch.Tensor, n_tok: int) -> dict:
-        offs, _ = self.workspace_layout(n_tok)
+        """Views of the intermediates a call left in its workspace: logits, ids, w, dexp, the split activation images
+        of x ("xpack", [n_tok][image bytes]) and act ("apack", [n_tok * k][image bytes], by (token, slot)), the guard
+        scales ("escale") and, with the F16 guard, the f32 act rows after the division ("act")."""
         d = self.layer.desc
-        spec = {"logits": (torch.float32, (n_tok, d.n_expert)), "ids": (torch.int32, (n_tok, d.k)),
-                "w": (torch.float32, (n_tok, d.k)), "dexp": (torch.float32, (n_tok, d.k, d.hidden))}
+        P = n_tok * d.k
+        spec = {"logits": (0, torch.float32, (n_tok, d.n_expert)), "ids": (1, torch.int32, (n_tok, d.k)),
+                "w": (2, torch.float32, (n_tok, d.k)), "xpack": (3, torch.uint8, (n_tok, -1)),
+                "apack": (4, torch.uint8, (P, -1)), "dexp": (5, torch.float32, (n_tok, d.k, d.hidden)),
+                "act": (9, torch.float32, (P, d.inter)), "escale": (10, torch.float32, (P,))}
         out = {}
-        for name, (dt, shape) in spec.items():
-            off = offs[PREFILL_SECTIONS.index(name)]
-            n = int(np.prod(shape)) * torch.tensor([], dtype=dt).element_size()
-            out[name] = ws[off: off + n].view(dt).view(*shape)
+        for name, (idx, dt, shape) in spec.items():
+            off, n = self.section(n_tok, idx)
+            if n:
+                out[name] = ws[off: off + n].view(dt).view(*shape)
         return out
 
 

@@ -150,6 +150,21 @@ int fns_hip_moe_layer_profiled(const FnsMoeLayer *layer, const float *x, const f
 int fns_hip_moe_layer_noalloc(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int n_tok,
                               void *stream);
 size_t fns_hip_moe_noalloc_max_bytes(void);
+/* No counterpart in the reference (its kernels have no cross-workgroup wait). The decode kernel's workgroups exchange
+ * the act rows through a bounded wait in device memory; a workgroup that gives up (its producers were never
+ * scheduled, e.g. other work held the CUs) writes NaN to its output rows and sets FNS_STATUS_EXCHANGE_TIMEOUT in the
+ * workspace's status word. The word is sticky across calls (the engine can check once per token or graph replay):
+ * this call waits for the stream's work so far, stores the word in *status and, with clear = 1, zeroes it (a kernel
+ * on `stream`). workspace NULL: the no-allocation array of the current device. Not graph-capturable (it
+ * synchronises). */
+#define FNS_STATUS_EXCHANGE_TIMEOUT 1u
+int fns_hip_moe_layer_status(const FnsMoeLayer *layer, int n_tok, void *workspace, int clear, uint32_t *status,
+                             void *stream);
+/* Test hook, no counterpart in the reference: the decode kernel's poll limit (0: the default, 65536 polls) and a
+ * number of producer arrivals to withhold (> 0: the exchange never completes, every workgroup gives up after
+ * spin_limit polls) for the calls that follow; the failure path is then exercised with every kernel exiting normally.
+ * Process-wide; set it only while no other thread launches layers. */
+int fns_hip_moe_set_test_hooks(int spin_limit, int withhold_arrivals);
 /* One of the three kernels of fns_hip_moe_layer (stage 0 router + Q8_1 of x, 1 routing + gate/up + SwiGLU,
  * 2 F16 guard + Q8_1 of act + down + combine), each reading what the previous stage left in the workspace:
  * per-stage tracing (the reference's FNS_TRACE nodes, src/engine.cu:590-599) and per-kernel timing. */
@@ -188,6 +203,11 @@ int fns_hip_mmq_compact(const int32_t *ids, int64_t n_tok, int64_t n_used, int64
  * workspace: fns_hip_moe_prefill_workspace() bytes; sections (byte offsets in offsets[6]): 0 logits f32 [n_tok][n_expert],
  * 1 ids i32 [n_tok][k], 2 w f32 [n_tok][k], 3 x images, 4 act images [n_tok * k], 5 down outputs f32 [n_tok][k][hidden]. */
 int fns_hip_moe_prefill_workspace(const FnsMoeLayer *layer, int64_t n_tok, size_t *offsets, size_t *total_bytes);
+/* Byte offset and size of any workspace section of fns_hip_moe_prefill (the six above, then 6 ids_src1, 7 ids_dst,
+ * 8 expert bounds, 9 f32 act [n_tok * k][inter] (F16 guard only, after the division), 10 guard scales [n_tok * k],
+ * 11 RMSNorm output, 12 its Q8_1 blocks, 13 shared-expert act images, 14 shared-expert output). Inspection and tests;
+ * the image layouts are internal. */
+int fns_hip_moe_prefill_section(const FnsMoeLayer *layer, int64_t n_tok, int section, size_t *offset, size_t *bytes);
 int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int64_t n_tok,
                         void *workspace, size_t workspace_bytes, void *stream);
 

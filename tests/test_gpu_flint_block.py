@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.helpers import assert_close
+from tests.helpers import assert_close, assert_close_chain
 
 pytestmark = pytest.mark.gpu
 
@@ -95,7 +95,7 @@ def test_flint_block_decode(ops, layer, mats):
     h, ids, w = check_front(ops, layer, x, tr["logits"], tr["xq"], bf16_x=False)
     assert np.array_equal(ids, tr["ids"]) and np.array_equal(w.view(np.uint32), tr["w"].view(np.uint32))
     ref = block_ref(mats, h, ids, w, host(x))
-    assert_close(out, ref, "flint block decode", 1e-3, 1e-4)
+    assert_close_chain(out, ref, "flint block decode")
 
 
 def test_flint_block_in_place(ops, layer):
@@ -123,7 +123,7 @@ def test_flint_block_verify_columns(ops, layer, mats):
         assert np.array_equal(out4[t], out1[0]), f"column {t}"
     h, ids, w = check_front(ops, layer, x4, tr4["logits"], tr4["xq"], bf16_x=False)
     assert np.array_equal(ids, tr4["ids"])
-    assert_close(out4, block_ref(mats, h, ids, w, host(x4)), "flint block verify", 1e-3, 1e-4)
+    assert_close_chain(out4, block_ref(mats, h, ids, w, host(x4)), "flint block verify")
 
 
 def test_flint_block_prefill(ops, layer, mats):
@@ -138,7 +138,7 @@ def test_flint_block_prefill(ops, layer, mats):
     assert np.array_equal(ids, tr["ids"]) and np.array_equal(w, tr["w"])
     toks = [0, 1, 33, 64, 69]
     ref = block_ref(mats, h[toks], ids[toks], w[toks], host(x)[toks])
-    assert_close(out[toks], ref, "flint block prefill", 1e-3, 1e-4)
+    assert_close_chain(out[toks], ref, "flint block prefill")
 
 
 def test_flint_block_shared_types_differ(ops, layer, mats):
@@ -167,4 +167,4 @@ def test_flint_block_shared_types_differ(ops, layer, mats):
         tr = {k: host(v) for k, v in lay2.trace(ws1, 1).items()}
         h, ids, w = check_front(ops, lay2, xt, tr["logits"], tr["xq"], bf16_x=False)
         ref = block_ref((mats[0], sh_np), h, ids, w, host(xt), sgu, sdn)
-        assert_close(out1, ref, f"flint block, shared {orc.TYPE_NAMES[sgu]}/{orc.TYPE_NAMES[sdn]}", 1e-3, 1e-4)
+        assert_close_chain(out1, ref, f"flint block, shared {orc.TYPE_NAMES[sgu]}/{orc.TYPE_NAMES[sdn]}")

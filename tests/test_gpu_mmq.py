@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.helpers import assert_close, gaussian, make_expert_mats
+from tests.helpers import assert_close, assert_close_chain, gaussian, image_to_q8_1, make_expert_mats, split_image
 
 pytestmark = pytest.mark.gpu
 
@@ -55,6 +55,47 @@ def test_compaction_bit_exact(ops, n_tok, k, n_expert, xr):
     assert np.array_equal(host(bounds), rb)
     assert np.array_equal(host(src), rs)
     assert np.array_equal(host(dst), rd)
+
+
+@pytest.mark.parametrize("n_tok,ncols", [(77, 2048), (512, 2048), (33, 768), (1, 256)])
+def test_mmq_activation_image_bit_exact(ops, n_tok, ncols):
+    """The MMQ activation quantiser (the split image fns_hip_mmq writes into its xq scratch) holds exactly the
+    reference's Q8_1 codes and f16 scales of x (oracle quantize_q8_1), byte for byte; zero rows and values at a
+    rounding half included."""
+    from flintnsteel_amd._lib import call
+    rng = np.random.default_rng(n_tok + ncols)
+    x = gaussian(rng, (n_tok, ncols))
+    if n_tok > 2:
+        x[1] = 0.0                                   # amax = 0: q = 0, d = 0
+        x[2, :32] = np.arange(32, dtype=np.float32) - 15.5   # halfway quotients round away from zero
+    w = make_expert_mats(orc.Q4_K, 1, 128, ncols, 3)[0]
+    xq = torch.full((ops.mmq_q8_1_bytes(ncols, n_tok),), 0xA5, dtype=torch.uint8, device="cuda")
+    dst = torch.empty(n_tok, 128, dtype=torch.float32, device="cuda")
+    call("fns_hip_mmq", orc.Q4_K, dev(w).data_ptr(), ncols, 128, dev(x).data_ptr(), n_tok, xq.data_ptr(),
+         dst.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    img = host(xq)
+    want = split_image(orc.quantize_q8_1(x), ncols)
+    got = img[: want.size].reshape(want.shape)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} image bytes differ, first at (row, byte) {tuple(bad[0])}"
+
+
+def check_routing(tr_logits, ref_logits, gpu_ids, k, gating, min_clear=1.0):
+    """The GPU's expert ids against the oracle's routing of its own logits (float64-accumulated router). With b twice
+    the measured GPU-oracle logit difference: every token's selection is a valid top-k of the oracle's gate values
+    within b (no selected expert below, no unselected one above, the oracle's k-th value by more than b); tokens whose
+    oracle margin (k-th minus (k+1)-th logit) exceeds b have exactly the oracle's ids, in order, and they are at least
+    `min_clear` of all tokens."""
+    ids_o, _, probs, margin = orc.route_topk(ref_logits, k, gating, True)
+    bound = 2.0 * float(np.abs(tr_logits - ref_logits).max()) + 1e-7
+    clear = margin > bound
+    assert clear.mean() >= min_clear, f"{(~clear).sum()} of {len(clear)} tokens are near-ties"
+    assert np.array_equal(ids_o[clear], gpu_ids[clear]), "ids differ from the oracle's routing of its own logits"
+    kth = np.sort(probs, axis=1)[:, -k][:, None]
+    sel = np.zeros(probs.shape, bool)
+    np.put_along_axis(sel, gpu_ids.astype(np.int64), True, axis=1)
+    assert (probs[sel].reshape(-1, k) >= kth - bound).all() and (np.where(sel, -np.inf, probs) <= kth + bound).all(), \
+        "a selection is not a top-k of the oracle's gate values"
 
 
 @pytest.mark.parametrize("qtype", TYPES)
@@ -166,45 +207,96 @@ def test_mmq_repeatable(ops, qtype):
         assert np.array_equal(host(ops.mmq(qtype, w, ncols, nrows, x)), first)
 
 
-def _oracle_layer_tokens(layer, slots_np, x, toks, ids, w, gu, dn, H, F):
-    """float64 chain per token: act = swiglu(gate . q8(x), up . q8(x)); out = sum_j w_j down . q8(act_j)."""
+def _oracle_layer_tokens(layer, slots_np, x, toks, ids, w, gu, dn, H, F, aq_gpu=None, esc=None):
+    """float64 chain per token: act = swiglu(gate . q8(x), up . q8(x)); out = sum_j w_j e_j down . q8(act_j / e_j).
+    aq_gpu [n_tok * k] Q8_1 rows: take the GPU's act codes (decoded from its act image) for the down products instead
+    of the oracle's own; esc [n_tok * k]: guard scales (default 1). Returns (out [len(toks)][H], act [len(toks)][k][F])."""
     xq = orc.quantize_q8_1(x[toks])
+    K = ids.shape[1]
     out = np.zeros((len(toks), H))
+    acts = np.zeros((len(toks), K, F), np.float32)
+    z = np.zeros(1, np.int32)
     for n, t in enumerate(toks):
-        for j in range(ids.shape[1]):
-            e = int(ids[t, j])
-            g = orc.mmvq_experts(gu, [slots_np["gate"][e].reshape(F, -1)], H, F, xq[n:n + 1], 1, 1, np.zeros(1, np.int32))
-            u = orc.mmvq_experts(gu, [slots_np["up"][e].reshape(F, -1)], H, F, xq[n:n + 1], 1, 1, np.zeros(1, np.int32))
-            act = orc.swiglu(g, u).astype(np.float32)
-            aq = orc.quantize_q8_1(act)
-            d = orc.mmvq_experts(dn, [slots_np["down"][e].reshape(H, -1)], F, H, aq, 1, 1, np.zeros(1, np.int32))[0]
-            out[n] += d * float(w[t, j])
-    return out
+        for j in range(K):
+            e, p = int(ids[t, j]), t * K + j
+            g = orc.mmvq_experts(gu, [slots_np["gate"][e].reshape(F, -1)], H, F, xq[n:n + 1], 1, 1, z)
+            u = orc.mmvq_experts(gu, [slots_np["up"][e].reshape(F, -1)], H, F, xq[n:n + 1], 1, 1, z)
+            acts[n, j] = orc.swiglu(g, u).astype(np.float32)[0]
+            s = 1.0 if esc is None else float(esc[p])
+            aq = aq_gpu[p:p + 1] if aq_gpu is not None else orc.quantize_q8_1((acts[n, j] / np.float32(s))[None])
+            d = orc.mmvq_experts(dn, [slots_np["down"][e].reshape(H, -1)], F, H, aq, 1, 1, z)[0]
+            out[n] += d * s * float(w[t, j])
+    return out, acts
 
 
-@pytest.mark.parametrize("gu,dn", [(orc.Q4_K, orc.Q4_K), (orc.Q3_K, orc.Q5_K), (orc.Q4_K, orc.Q6_K)])
-def test_moe_prefill_vs_oracle(ops, gu, dn):
+def check_prefill_chains(tr, layer, slots_np, xh, toks, ids, gu, dn, H, F, what, resid=None):
+    """The prefill output against two float64 chains: (a) fed with the GPU's act codes (decoded from its act image),
+    held to the tight bounds; (b) fully independent, held to the chain bounds. The GPU's act image itself lies within
+    half a quantisation step (plus the GEMM tolerance) of the oracle's act / e."""
+    K = ids.shape[1]
+    esc = tr["escale"] if layer.desc.guard else np.ones(tr["apack"].shape[0], np.float32)  # written with the guard only
+    aq = image_to_q8_1(tr["apack"], F)
+    out = tr["out"][toks] - (0.0 if resid is None else resid[toks])
+    ref_g, act_ref = _oracle_layer_tokens(layer, slots_np, xh, toks, ids, tr["w"], gu, dn, H, F, aq, esc)
+    assert_close(out, ref_g, what + " (GPU act codes)")
+    ref_i, _ = _oracle_layer_tokens(layer, slots_np, xh, toks, ids, tr["w"], gu, dn, H, F, None, esc)
+    assert_close_chain(out, ref_i, what)
+    rows = np.array([t * K + j for t in toks for j in range(K)])
+    esc_ref = np.array([orc.amax_guard_scale(a) for a in act_ref.reshape(-1, F)], np.float32)
+    assert (esc[rows] == 1.0).all() or np.array_equal(esc[rows], esc_ref), f"{what}: guard scales differ"
+    vals = orc.dequantize_q8_1(aq[rows], F).reshape(len(toks), K, F)
+    dstep = np.repeat(np.abs(vals).reshape(len(toks), K, F // 32, 32).max(axis=3) / 127.0, 32, axis=2)
+    want = act_ref / esc[rows].reshape(len(toks), K, 1)
+    # half a step of the image's own scale plus the fp32 difference of the two act computations (1e-3 of the row's
+    # max: act = up * silu(gate) carries the GEMV errors of both factors; still a fraction of one step, max / 127)
+    slack = 0.5 * dstep + 1e-3 * np.abs(want).max(axis=2, keepdims=True)
+    excess = np.abs(vals - want) / slack
+    worst = np.unravel_index(int(np.argmax(excess)), excess.shape)
+    assert excess.max() <= 1.0 + 1e-6, (f"{what}: act image beyond half a step of the oracle's act at {worst}: "
+                                        f"{vals[worst]} vs {want[worst]}, step {dstep[worst]}")
+
+
+@pytest.mark.parametrize("gu,dn,guard", [(orc.Q4_K, orc.Q4_K, False), (orc.Q3_K, orc.Q5_K, False),
+                                         (orc.Q4_K, orc.Q6_K, True)])
+def test_moe_prefill_vs_oracle(ops, gu, dn, guard):
+    """77 tokens: router logits against the float64 oracle; ids from the oracle's own logits (every token's top-k
+    margin clear of the logit difference); the x and act activation images byte-exact against the oracle's Q8_1 of
+    x and of the GPU's act (guard on: f32 act rows exposed, no row scaled, so every act image is the GEMM epilogue's);
+    the layer against the float64 chain."""
     from flintnsteel_amd import synth
     H, F, NE, K, T = 512, 256, 16, 4, 77
-    layer = synth.build_layer(H, F, NE, K, gu, dn, seed=11, layer=gu * 10 + dn)
+    layer0 = synth.build_layer(H, F, NE, K, gu, dn, seed=11, layer=gu * 10 + dn)
+    layer = ops.MoeLayer(layer0.router_w, layer0.slots, gu, dn, H, F, K, guard=guard) if guard else layer0
     pre = ops.MoePrefill(layer)
     x = synth.activations(T, H, seed=11, layer=3)
     ws = pre.workspace(T)
     out = host(pre(x, ws=ws))
     tr = {k: host(v) for k, v in pre.trace(ws, T).items()}
-    ids, w, _, _ = orc.route_topk(tr["logits"], K, 0, True)
-    assert np.array_equal(ids, tr["ids"]) and np.array_equal(w, tr["w"]), "routing differs from the oracle"
+    xh = host(x)
+    ref_logits = orc.router_f32(host(layer.router_w), xh)
+    assert_close(tr["logits"], ref_logits, "prefill logits", 1e-5, 1e-6)
+    check_routing(tr["logits"], ref_logits, tr["ids"], K, 0)
+    ids = tr["ids"]
+    ids_g, w_g, _, _ = orc.route_topk(tr["logits"], K, 0, True)
+    assert np.array_equal(ids_g, ids), "ids differ given the same logits"
+    assert np.array_equal(w_g.view(np.uint32), tr["w"].view(np.uint32)), "weights differ given the same logits"
+    assert np.array_equal(tr["xpack"], split_image(orc.quantize_q8_1(xh), H)), "x image differs from the oracle's Q8_1"
+    if guard:
+        assert (tr["escale"] == 1.0).all()
+        act = tr["act"]
+        want = split_image(orc.quantize_q8_1(act), F)
+        assert np.array_equal(tr["apack"], want), "act image differs from the oracle's Q8_1 of act"
     slots_np = {k: layer.slots.view(k).cpu().numpy() for k in ("gate", "up", "down")}
-    toks = list(range(T))
-    ref = _oracle_layer_tokens(layer, slots_np, host(x), toks, ids, w, gu, dn, H, F)
-    # act is re-quantised from fp32 values whose last bits depend on the summation order, so a Q8_1 code of act can
-    # differ by one step from the oracle's: the layer bound is the north_star's 1e-3 (the GEMMs alone are held to 1e-4)
-    assert_close(out, ref, f"prefill layer {orc.TYPE_NAMES[gu]}/{orc.TYPE_NAMES[dn]}", max_tol=1e-3, l2_tol=1e-4)
+    tr["out"] = out
+    check_prefill_chains(tr, layer, slots_np, xh, list(range(T)), ids, gu, dn, H, F,
+                         f"prefill layer {orc.TYPE_NAMES[gu]}/{orc.TYPE_NAMES[dn]}")
 
 
 def test_moe_prefill_config4_sample(ops):
     """Config 4 shapes (512 tokens, hidden 2048, 128 experts top-8, inter 768, Q4_K) with a Dirichlet-skewed router
-    bias: routing of every token bit-exact, 12 sampled tokens against the float64 chain, residual added."""
+    bias: logits against the oracle, ids against the oracle's routing of its own logits (tokens with a clear margin),
+    the x image of all 512 tokens byte-exact, 64 tokens (among them every token of the largest expert group up to 40)
+    against the float64 chain, residual added."""
     from flintnsteel_amd import synth
     H, F, NE, K, T = 2048, 768, 128, 8, 512
     layer = synth.build_layer(H, F, NE, K, orc.Q4_K, orc.Q4_K, seed=20261022, layer=400)
@@ -219,15 +311,20 @@ def test_moe_prefill_config4_sample(ops):
     tr = {k: host(v) for k, v in pre.trace(ws, T).items()}
     xh = host(x)
     logits_ref = orc.router_f32(layer.router_w.cpu().numpy(), xh) + bias
-    assert np.abs(tr["logits"] - logits_ref).max() <= 1e-4 * np.abs(logits_ref).max()
+    assert_close(tr["logits"], logits_ref, "config-4 logits", 1e-5, 1e-6)
+    check_routing(tr["logits"], logits_ref, tr["ids"], K, 0, min_clear=0.98)
     ids, w, _, _ = orc.route_topk(tr["logits"], K, 0, True)
     assert np.array_equal(ids, tr["ids"]) and np.array_equal(w, tr["w"])
+    assert np.array_equal(tr["xpack"], split_image(orc.quantize_q8_1(xh), H)), "x image differs from the oracle"
     counts = np.bincount(ids.ravel(), minlength=NE)
     assert counts.max() > 128, "the skewed bias should give at least one expert more than one tile group"
-    toks = sorted(set([0, 77, 511] + list(rng.choice(T, 9, replace=False))))
+    big = np.flatnonzero((ids == counts.argmax()).any(axis=1))
+    rest = rng.choice(np.setdiff1d(np.arange(T), big), 64 - min(40, len(big)) - 3, replace=False)
+    toks = sorted(set([0, 77, 511] + list(big[:40]) + list(rest)))
     slots_np = {k: layer.slots.view(k).cpu().numpy() for k in ("gate", "up", "down")}
-    ref = _oracle_layer_tokens(layer, slots_np, xh, toks, ids, w, orc.Q4_K, orc.Q4_K, H, F) + host(resid)[toks]
-    assert_close(out[toks], ref, "config-4 prefill sample", max_tol=1e-3, l2_tol=1e-4)
+    tr["out"] = out
+    check_prefill_chains(tr, layer, slots_np, xh, toks, ids, orc.Q4_K, orc.Q4_K, H, F, "config-4 prefill sample",
+                         resid=host(resid))
 
 
 def test_moe_prefill_guard_bf16_sigmoid_residual(ops):
@@ -253,21 +350,14 @@ def test_moe_prefill_guard_bf16_sigmoid_residual(ops):
     assert np.abs(tr["logits"] - logits_ref).max() <= 1e-4 * np.abs(logits_ref).max()
     ids, w, _, _ = orc.route_topk(tr["logits"], K, 1, True)
     assert np.array_equal(ids, tr["ids"]) and np.array_equal(w, tr["w"])
+    # (x is scaled by 40, so many sigmoid gates saturate and tie: a valid top-k check for every token)
+    check_routing(tr["logits"], logits_ref, tr["ids"], K, 1, min_clear=0.0)
+    # act images: every row here is guarded, so re-quantised from act / e (the GEMM epilogue's own images are checked
+    # in test_moe_prefill_vs_oracle), byte-exact
+    assert (tr["escale"] > 1.0).any()
+    want = split_image(orc.quantize_q8_1(tr["act"]), F)
+    assert np.array_equal(tr["apack"], want), "act image differs from the oracle's Q8_1 of act"
     slots = {k: base.slots.view(k).cpu().numpy() for k in ("gate", "up", "down")}
-    xq = orc.quantize_q8_1(xh)
-    ref = np.zeros((T, H))
-    guarded = 0
-    for t in range(T):
-        for j in range(K):
-            e = int(ids[t, j])
-            g = orc.mmvq_experts(orc.Q4_K, [slots["gate"][e].reshape(F, -1)], H, F, xq[t:t + 1], 1, 1, np.zeros(1, np.int32))
-            u = orc.mmvq_experts(orc.Q4_K, [slots["up"][e].reshape(F, -1)], H, F, xq[t:t + 1], 1, 1, np.zeros(1, np.int32))
-            act = orc.swiglu(g, u).astype(np.float32)[0]
-            esc = orc.amax_guard_scale(act)
-            guarded += esc > 1.0
-            aq = orc.quantize_q8_1((act / esc)[None].astype(np.float32))
-            d = orc.mmvq_experts(orc.Q6_K, [slots["down"][e].reshape(H, -1)], F, H, aq, 1, 1, np.zeros(1, np.int32))[0]
-            ref[t] += d * esc * float(w[t, j])
-    assert guarded > 0, "test needs act rows with amax > 1024"
-    ref += host(resid)
-    assert_close(out, ref, "guarded bf16 sigmoid prefill", max_tol=1e-3, l2_tol=1e-4)
+    tr["out"] = out
+    check_prefill_chains(tr, layer, slots, xh, list(range(T)), ids, orc.Q4_K, orc.Q6_K, H, F,
+                         "guarded bf16 sigmoid prefill", resid=host(resid))

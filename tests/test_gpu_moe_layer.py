@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.helpers import assert_close
+from tests.helpers import assert_close, assert_close_chain
 
 pytestmark = pytest.mark.gpu
 
@@ -107,7 +107,7 @@ def test_moe_layer_decode(ops, synth, case):
     assert_close(out, out_ref, "combined out")
     # fully independent oracle chain (its own fp32 act): the north_star's 1e-3 bound
     _, out_ind, _ = oracle_layer(layer, x, ids_o, w_l, None, guard=False)
-    assert_close(out, out_ind, "combined out (independent chain)", 1e-3, 1e-4)
+    assert_close_chain(out, out_ind, "combined out (independent chain)")
 
 
 @pytest.mark.parametrize("qtype", [12, 8])
@@ -155,3 +155,30 @@ def test_moe_layer_rejects_bad_shapes(ops, synth):
         layer(torch.zeros(5, 256, device="cuda"), ws=ws)
     with pytest.raises(FnsError, match="workspace"):
         layer(torch.zeros(1, 256, device="cuda"), ws=ws[:16])
+
+
+STATUS_EXCHANGE_TIMEOUT = 1
+
+
+def test_exchange_timeout_is_reported(ops, synth):
+    """A decode call whose act exchange never completes (forced from the host: every producer group withholds one
+    arrival, poll limit 64) ends normally with NaN outputs and FNS_STATUS_EXCHANGE_TIMEOUT in the workspace's sticky
+    status word; the word survives later good calls until cleared; with the hooks reset the layer is exact again."""
+    from flintnsteel_amd._lib import call
+    layer = synth.build_layer(H, F, NE, K, 12, 12, SEED, layer=21)
+    x_d = synth.activations(1, H, SEED, layer=22)
+    ws = layer.workspace(1)
+    good = host(layer(x_d, ws=ws))
+    assert layer.status(ws) == 0 and np.isfinite(good).all()
+    try:
+        call("fns_hip_moe_set_test_hooks", 64, 1)
+        bad = host(layer(x_d, ws=ws))
+    finally:
+        call("fns_hip_moe_set_test_hooks", 0, 0)
+    assert np.isnan(bad).all(), "every workgroup gave up, so every output row is NaN"
+    assert layer.status(ws) == STATUS_EXCHANGE_TIMEOUT
+    again = host(layer(x_d, ws=ws))
+    assert np.array_equal(again, good)
+    assert layer.status(ws, clear=True) == STATUS_EXCHANGE_TIMEOUT, "sticky until cleared"
+    assert layer.status(ws) == 0
+    assert np.array_equal(host(layer(x_d, ws=ws)), good)

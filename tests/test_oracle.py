@@ -340,3 +340,37 @@ def test_cpu_layer_matches_float64_chain():
     dexp = orc.mmvq_experts(orc.Q6_K, [m.reshape(H_, -1) for m in dn], F_, H_, aq, K_, 1, ids[0])
     ref = (dexp * w[0][:, None]).sum(0)
     assert np.abs(out - ref).max() / np.abs(ref).max() < 1e-3
+
+
+def test_split_image_helper_decodes_to_q8_1():
+    """The test helper that spells out the prefill GEMM's split activation image: hi + lo of every column is the
+    oracle's dequantised Q8_1 value (q * f16 d) exactly, and the sums are d * sum(q) per 32-column block."""
+    from tests.helpers import split_image
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((3, 512)) * 3).astype(np.float32)
+    x[1] = 0.0
+    xq = orc.quantize_q8_1(x)
+    img = split_image(xq, 512)
+    assert img.shape == (3, 2 * 1056)
+    deq = orc.dequantize_q8_1(xq, 512)
+    perm = np.array([0, 2, 1, 3, 4, 6, 5, 7])
+    for kb in range(2):
+        main = img[:, kb * 1024:(kb + 1) * 1024].view(np.float16).astype(np.float32).reshape(3, 2, 2, 16, 8)
+        val = (main[:, :, 0] + main[:, :, 1])[..., perm].reshape(3, 256)  # stored order is an involution
+        assert np.array_equal(val, deq[:, kb * 256:(kb + 1) * 256])
+        s = img[:, 2048 + 32 * kb: 2048 + 32 * (kb + 1)].view(np.float16).astype(np.float32).reshape(3, 2, 8)
+        sums = (s[:, 0] + s[:, 1])[:, perm]
+        assert np.array_equal(sums, deq[:, kb * 256:(kb + 1) * 256].reshape(3, 8, 32).sum(axis=2))
+    assert not img[1].any()
+
+
+def test_image_to_q8_1_inverts_split_image():
+    from tests.helpers import image_to_q8_1, split_image
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((4, 768)) * 2).astype(np.float32)
+    x[2, 64:96] = 0.0
+    xq = orc.quantize_q8_1(x)
+    back = image_to_q8_1(split_image(xq, 768), 768)
+    a = xq[:, : 24 * 36].reshape(4, 24, 36)
+    b = back[:, : 24 * 36].reshape(4, 24, 36)
+    assert np.array_equal(a[:, :, 0:2], b[:, :, 0:2]) and np.array_equal(a[:, :, 4:], b[:, :, 4:])
