@@ -33,20 +33,36 @@ __device__ __forceinline__ uint32_t ld32u(const uint8_t *p) {
     return __builtin_amdgcn_alignbit(w1, w0, sh);
 }
 
-// 64 activation bytes of quarter qt of block bb, as 16 dwords.
-__device__ __forceinline__ void act_quarter(const ActImg &x, int bb, int qt, int a[16]) {
+// The activation side of one quarter (64 consecutive columns of block bb, quarter qt) in registers: the 64 int8 values
+// as 16 dwords, the Q8_1 scales of its two 32-column blocks, d * (sum of the quantised values) of its four 16-column
+// groups and of its two 32-column blocks. Loaded once, it serves every weight row that has the same quarter.
+struct ActQ {
+    int a[16];
+    float d[2], s16[4], s32[2];
+};
+__device__ __forceinline__ ActQ act_q(const ActImg &x, int bb, int qt) {
+    ActQ r;
     const int8_t *p = x.q + bb * kImgQRow + 64 * qt;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int4 v = *(const int4 *) (p + 16 * i);
-        a[4 * i] = v.x;
-        a[4 * i + 1] = v.y;
-        a[4 * i + 2] = v.z;
-        a[4 * i + 3] = v.w;
+        r.a[4 * i] = v.x;
+        r.a[4 * i + 1] = v.y;
+        r.a[4 * i + 2] = v.z;
+        r.a[4 * i + 3] = v.w;
     }
+    const int b32 = bb * 8 + 2 * qt;
+    r.d[0] = x.d[b32];
+    r.d[1] = x.d[b32 + 1];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) r.s16[g] = x.s16[2 * b32 + g];
+    r.s32[0] = x.s32[b32];
+    r.s32[1] = x.s32[b32 + 1];
+    return r;
 }
 
-template <int T, class L> __device__ __forceinline__ float quarter_dot(const uint8_t *blk, const ActImg &x, int bb, int qt);
+// Quarter dot against an activation quarter in registers (qt: the quarter's index in its block).
+template <int T, class L> __device__ __forceinline__ float quarter_dot_r(const uint8_t *blk, const ActQ &x, int qt);
 
 // Q4_K / Q5_K share the header decoding: 6-bit scale and min of sub-blocks 2qt, 2qt+1 (bytes k0, k0+1 of the words).
 __device__ __forceinline__ void k4_scales(const uint4 &h, int qt, uint32_t &scw, uint32_t &mw) {
@@ -58,79 +74,62 @@ __device__ __forceinline__ void k4_scales(const uint4 &h, int qt, uint32_t &scw,
 }
 __device__ __forceinline__ float ubyte_dyn(uint32_t w, int k) { return (float) ((w >> (8 * k)) & 0xffu); }
 
-__device__ __forceinline__ float k4_finish(const uint4 &h, const ActImg &x, int bb, int qt, int dl, int dh) {
+__device__ __forceinline__ float k4_finish(const uint4 &h, const ActQ &x, int qt, int dl, int dh) {
     uint32_t scw, mw;
     k4_scales(h, qt, scw, mw);
     const int k0 = 2 * (qt & 1);
-    const int b32 = bb * 8 + 2 * qt;
-    float sumd = ubyte_dyn(scw, k0) * x.d[b32] * (float) dl;
-    sumd = fmaf_(ubyte_dyn(scw, k0 + 1) * x.d[b32 + 1], (float) dh, sumd);
-    float summ = ubyte_dyn(mw, k0) * x.s32[b32];
-    summ = fmaf_(ubyte_dyn(mw, k0 + 1), x.s32[b32 + 1], summ);
+    float sumd = ubyte_dyn(scw, k0) * x.d[0] * (float) dl;
+    sumd = fmaf_(ubyte_dyn(scw, k0 + 1) * x.d[1], (float) dh, sumd);
+    float summ = ubyte_dyn(mw, k0) * x.s32[0];
+    summ = fmaf_(ubyte_dyn(mw, k0 + 1), x.s32[1], summ);
     return half_to_float(h.x & 0xffffu) * sumd - half_to_float(h.x >> 16) * summ;
 }
 
-template <> __device__ __forceinline__ float quarter_dot<T_Q4_K, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                            int qt) {
-    const uint4 h = Aligned16::ld(blk);
-    const uint4 q0 = Aligned16::ld(blk + 16 + 32 * qt), q1 = Aligned16::ld(blk + 32 + 32 * qt);
+template <class L> __device__ __forceinline__ float q4k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+    const uint4 h = L::ld(blk);
+    const uint4 q0 = L::ld(blk + 16 + 32 * qt), q1 = L::ld(blk + 32 + 32 * qt);
     const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    int a[16];
-    act_quarter(x, bb, qt, a);
     int dl = 0, dh = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        dl = dot4((int) (q[i] & kLo4), a[i], dl);
-        dh = dot4((int) ((q[i] >> 4) & kLo4), a[8 + i], dh);
+        dl = dot4((int) (q[i] & kLo4), x.a[i], dl);
+        dh = dot4((int) ((q[i] >> 4) & kLo4), x.a[8 + i], dh);
     }
-    return k4_finish(h, x, bb, qt, dl, dh);
+    return k4_finish(h, x, qt, dl, dh);
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q4_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                       int qt) {
-    const uint4 h = Any2::ld(blk);
-    const uint4 q0 = Any2::ld(blk + 16 + 32 * qt), q1 = Any2::ld(blk + 32 + 32 * qt);
-    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    int a[16];
-    act_quarter(x, bb, qt, a);
-    int dl = 0, dh = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        dl = dot4((int) (q[i] & kLo4), a[i], dl);
-        dh = dot4((int) ((q[i] >> 4) & kLo4), a[8 + i], dh);
-    }
-    return k4_finish(h, x, bb, qt, dl, dh);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q4_K, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q4k_quarter<Aligned16>(blk, x, qt);
+}
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q4_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q4k_quarter<Any2>(blk, x, qt);
 }
 
-template <class L> __device__ __forceinline__ float q5k_quarter(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+template <class L> __device__ __forceinline__ float q5k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
     const uint4 h = L::ld(blk);
     const uint4 h0 = L::ld(blk + 16), h1 = L::ld(blk + 32);
     const uint4 q0 = L::ld(blk + 48 + 32 * qt), q1 = L::ld(blk + 64 + 32 * qt);
     const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
     const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    int a[16];
-    act_quarter(x, bb, qt, a);
     int dl = 0, dh = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         // fifth bit: qh bit 2qt (low values) and 2qt+1 (high values), moved to bit 4 of each byte
         const uint32_t bl = ((qh[i] >> (2 * qt)) & 0x01010101u) << 4;
         const uint32_t bh = ((qh[i] >> (2 * qt + 1)) & 0x01010101u) << 4;
-        dl = dot4((int) ((q[i] & kLo4) | bl), a[i], dl);
-        dh = dot4((int) (((q[i] >> 4) & kLo4) | bh), a[8 + i], dh);
+        dl = dot4((int) ((q[i] & kLo4) | bl), x.a[i], dl);
+        dh = dot4((int) (((q[i] >> 4) & kLo4) | bh), x.a[8 + i], dh);
     }
-    return k4_finish(h, x, bb, qt, dl, dh);
+    return k4_finish(h, x, qt, dl, dh);
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q5_K, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                            int qt) {
-    return q5k_quarter<Aligned16>(blk, x, bb, qt);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q5_K, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q5k_quarter<Aligned16>(blk, x, qt);
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q5_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                       int qt) {
-    return q5k_quarter<Any2>(blk, x, bb, qt);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q5_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q5k_quarter<Any2>(blk, x, qt);
 }
 
 // Q6_K and Q3_K blocks are only 2-byte aligned: both policies read through Any2.
-__device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+__device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
     const int n = qt >> 1, hh = qt & 1;
     const uint4 A0 = lds16u(blk + 64 * n), A1 = lds16u(blk + 64 * n + 16);       // ql[64n .. 64n+31]
     const uint4 B0 = lds16u(blk + 64 * n + 32), B1 = lds16u(blk + 64 * n + 48);  // ql[64n+32 .. 64n+63]
@@ -140,8 +139,6 @@ __device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActImg &x
     const uint32_t A[8] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w};
     const uint32_t B[8] = {B0.x, B0.y, B0.z, B0.w, B1.x, B1.y, B1.z, B1.w};
     const uint32_t Q[8] = {Q0.x, Q0.y, Q0.z, Q0.w, Q1.x, Q1.y, Q1.z, Q1.w};
-    int a[16];
-    act_quarter(x, bb, qt, a);
     const int sh = 4 * hh;
     int du[4] = {0, 0, 0, 0};  // groups: A half 0, A half 1, B half 0, B half 1
 #pragma unroll
@@ -149,28 +146,22 @@ __device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActImg &x
         const uint32_t qh = Q[i] >> sh;
         const uint32_t ua = ((A[i] >> sh) & kLo4) | ((qh << 4) & 0x30303030u);
         const uint32_t ub = ((B[i] >> sh) & kLo4) | ((qh << 2) & 0x30303030u);
-        du[i >> 2] = dot4((int) ua, a[i], du[i >> 2]);
-        du[2 + (i >> 2)] = dot4((int) ub, a[8 + i], du[2 + (i >> 2)]);
+        du[i >> 2] = dot4((int) ua, x.a[i], du[i >> 2]);
+        du[2 + (i >> 2)] = dot4((int) ub, x.a[8 + i], du[2 + (i >> 2)]);
     }
-    const int c0 = bb * 256 + 64 * qt;
     float sum = 0.0f;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const int c = c0 + 16 * g;
-        sum = fmaf_(sbyte_f(scw, g), group_term(du[g], x.d[c >> 5], x.s16[c >> 4], 32.0f), sum);
-    }
+    for (int g = 0; g < 4; ++g) sum = fmaf_(sbyte_f(scw, g), group_term(du[g], x.d[g >> 1], x.s16[g], 32.0f), sum);
     return half_to_float(dbits) * sum;
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q6_K, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                            int qt) {
-    return q6k_quarter(blk, x, bb, qt);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q6_K, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q6k_quarter(blk, x, qt);
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q6_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                       int qt) {
-    return q6k_quarter(blk, x, bb, qt);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q6_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q6k_quarter(blk, x, qt);
 }
 
-__device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+__device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
     const int n = qt >> 1, hh = qt & 1;
     const uint4 H0 = lds16u(blk), H1 = lds16u(blk + 16);                          // hmask[0 .. 31]
     const uint4 q0 = lds16u(blk + 32 + 32 * n), q1 = lds16u(blk + 48 + 32 * n);  // qs[32n .. 32n+31]
@@ -184,8 +175,6 @@ __device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActImg &x
     const uint32_t lo = ((hh ? S1 : S0) >> (4 * n)) & kLo4;
     const uint32_t hi = (uint32_t) ((((uint64_t) S2) << 4) >> (2 * qt)) & 0x30303030u;
     const uint32_t scw = lo | hi;
-    int a[16];
-    act_quarter(x, bb, qt, a);
     int du[4] = {0, 0, 0, 0};  // groups: j0 half 0, j0 half 1, j1 half 0, j1 half 1 (j0 = 2hh, j1 = 2hh + 1)
     const int j0 = 2 * hh;
 #pragma unroll
@@ -193,53 +182,48 @@ __device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActImg &x
         const uint32_t hm = HM[i] >> (4 * n + j0);
         const uint32_t u0 = ((q[i] >> (2 * j0)) & 0x03030303u) | ((hm << 2) & 0x04040404u);
         const uint32_t u1 = ((q[i] >> (2 * j0 + 2)) & 0x03030303u) | ((hm << 1) & 0x04040404u);
-        du[i >> 2] = dot4((int) u0, a[i], du[i >> 2]);
-        du[2 + (i >> 2)] = dot4((int) u1, a[8 + i], du[2 + (i >> 2)]);
+        du[i >> 2] = dot4((int) u0, x.a[i], du[i >> 2]);
+        du[2 + (i >> 2)] = dot4((int) u1, x.a[8 + i], du[2 + (i >> 2)]);
     }
-    const int c0 = bb * 256 + 64 * qt;
     float sum = 0.0f;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const int c = c0 + 16 * g;
-        sum = fmaf_(ubyte_dyn(scw, g) - 32.0f, group_term(du[g], x.d[c >> 5], x.s16[c >> 4], 4.0f), sum);
-    }
+    for (int g = 0; g < 4; ++g)
+        sum = fmaf_(ubyte_dyn(scw, g) - 32.0f, group_term(du[g], x.d[g >> 1], x.s16[g], 4.0f), sum);
     return half_to_float(t.w >> 16) * sum;
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q3_K, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                            int qt) {
-    return q3k_quarter(blk, x, bb, qt);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q3_K, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q3k_quarter(blk, x, qt);
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q3_K, Any2>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                       int qt) {
-    return q3k_quarter(blk, x, bb, qt);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q3_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q3k_quarter(blk, x, qt);
 }
 
 // Q8_0 quarter qt = blocks 2qt and 2qt+1 of the 8-block unit (68 bytes at offset 68 qt, 2-byte aligned at least):
 // sum over the two blocks of (d_w * d8) * (q_w . a), the block product of ggml vec_dot_q8_0_q8_1.
-__device__ __forceinline__ float q80_quarter(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+__device__ __forceinline__ float q80_quarter(const uint8_t *blk, const ActQ &x, int qt) {
     const uint8_t *p = blk + 68 * qt;
     const uint4 A0 = lds16u(p), A1 = lds16u(p + 16), A2 = lds16u(p + 32), A3 = lds16u(p + 48);
     const uint32_t W[17] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w, A2.x,
                             A2.y, A2.z, A2.w, A3.x, A3.y, A3.z, A3.w, ld32u(p + 64)};
-    int a[16];
-    act_quarter(x, bb, qt, a);
     int s0 = 0, s1 = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        s0 = dot4((int) __builtin_amdgcn_alignbit(W[i + 1], W[i], 16), a[i], s0);  // block 0 codes: bytes 2 .. 33
-        s1 = dot4((int) W[9 + i], a[8 + i], s1);                                    // block 1 codes: bytes 36 .. 67
+        s0 = dot4((int) __builtin_amdgcn_alignbit(W[i + 1], W[i], 16), x.a[i], s0);  // block 0 codes: bytes 2 .. 33
+        s1 = dot4((int) W[9 + i], x.a[8 + i], s1);                                    // block 1 codes: bytes 36 .. 67
     }
-    const int b32 = bb * 8 + 2 * qt;
-    const float d0 = half_to_float(W[0] & 0xffffu) * x.d[b32], d1 = half_to_float(W[8] >> 16) * x.d[b32 + 1];
+    const float d0 = half_to_float(W[0] & 0xffffu) * x.d[0], d1 = half_to_float(W[8] >> 16) * x.d[1];
     return fmaf_(d1, (float) s1, d0 * (float) s0);
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q8_0, Aligned16>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                            int qt) {
-    return q80_quarter(blk, x, bb, qt);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q80_quarter(blk, x, qt);
 }
-template <> __device__ __forceinline__ float quarter_dot<T_Q8_0, Any2>(const uint8_t *blk, const ActImg &x, int bb,
-                                                                       int qt) {
-    return q80_quarter(blk, x, bb, qt);
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q80_quarter(blk, x, qt);
+}
+
+// The quarter dot against an activation row image (the activation quarter read from LDS for this one product).
+template <int T, class L> __device__ __forceinline__ float quarter_dot(const uint8_t *blk, const ActImg &x, int bb, int qt) {
+    return quarter_dot_r<T, L>(blk, act_q(x, bb, qt), qt);
 }
 
 // The same dot for NC activation columns (n < ncol live; NC == 1 ignores ncol): acc[n] += quarter_dot(blk, x[n]).
@@ -261,15 +245,14 @@ __device__ __forceinline__ void quarter_dot_nc(const uint8_t *blk, const ActImg 
 #pragma unroll
         for (int n = 0; n < NC; ++n) {
             if (NC == 1 || n < ncol) {
-                int a[16];
-                act_quarter(x[n], bb, qt, a);
+                const ActQ a = act_q(x[n], bb, qt);
                 int dl = 0, dh = 0;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    dl = dot4(lo[i], a[i], dl);
-                    dh = dot4(hi[i], a[8 + i], dh);
+                    dl = dot4(lo[i], a.a[i], dl);
+                    dh = dot4(hi[i], a.a[8 + i], dh);
                 }
-                acc[n] += k4_finish(h, x[n], bb, qt, dl, dh);
+                acc[n] += k4_finish(h, a, qt, dl, dh);
             }
         }
     } else {

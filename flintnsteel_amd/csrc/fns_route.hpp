@@ -251,16 +251,18 @@ __device__ __forceinline__ void route_topk_pairs(const float *__restrict__ lg, i
         }
     }
     __syncthreads();
+    FNS_MARK(1, blockIdx.x, 6);
     const int part = tid % P;
     const int kpl = ((n_expert + 2 * P - 1) / (2 * P)) * 2;  // keys per thread, even (16-byte reads)
     for (int e0 = 0; e0 < n_expert; e0 += EPP) {
         const int e = e0 + tid / P;
         const uint64_t ke = s_key[e < 256 ? e : 255];
         int rank = 0;
-        const uint64_t *kp = s_key + part * kpl;
+        // the eight threads of an expert read 8 consecutive 16-byte pieces per step (no LDS bank conflicts between
+        // them); together they cover keys [0, kpl * P)
 #pragma unroll 4
         for (int i = 0; i < kpl; i += 2) {
-            const ulonglong2 kk = *(const ulonglong2 *) (kp + i);
+            const ulonglong2 kk = *(const ulonglong2 *) (s_key + i * P + 2 * part);
             rank += kk.x > ke ? 1 : 0;
             rank += kk.y > ke ? 1 : 0;
         }
@@ -271,6 +273,7 @@ __device__ __forceinline__ void route_topk_pairs(const float *__restrict__ lg, i
         }
     }
     __syncthreads();
+    FNS_MARK(1, blockIdx.x, 7);
 }
 
 // Gating + top-k + renormalisation for one token by a whole workgroup (n_expert <= 256): the all-pairs rank up to

@@ -114,12 +114,15 @@ __device__ __forceinline__ void pack_store(uint8_t *pack, int npad, int i, const
 __device__ void route_all(const LayerArgs &a);
 
 // ---- K1: router rows + Q8_1 of x ----------------------------------------------------------------------------------
-// 1024-thread workgroups: the first ceil(n_expert / 4) each compute four router rows (256 lanes per row), the rest
-// quantise 1024 columns of one token row. Few, wide workgroups start faster than one small workgroup per row.
-constexpr int kK1Threads = 1024, kK1Rows = kK1Threads / 256;
+// NT-thread workgroups: the first ceil(n_expert / (NT / 256)) each compute NT / 256 router rows (256 lanes per row),
+// the rest quantise NT columns of one token row. One token (NT = 256): one row per workgroup, so the router's bytes
+// are spread over as many CUs as there are rows; several tokens (NT = 1024): the last router workgroup to finish
+// routes every token with one group of 256 threads per token (route_all).
+constexpr int kK1Threads = 1024;
 
-template <bool NORM>
-__global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
+template <bool NORM, int NT>
+__global__ __launch_bounds__(NT) void k_route_quant(const LayerArgs a) {
+    constexpr int kK1Rows = NT / 256;
     __shared__ float red[kK1Rows][4][kMaxTok];
     __shared__ float s_nred[4], s_scale[kMaxTok], s_nq[kK1Rows][4][kMaxTok];
     const int H = a.H, T = a.T;
@@ -215,7 +218,7 @@ __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
             else a.logits[(size_t) t256 * a.NE + r] = v;
         }
         FNS_MARK(0, blockIdx.x, 3);
-        if (T > 1) {  // the last router workgroup to finish routes every token (it resets the arrival count)
+        if (NT == kK1Threads && T > 1) {  // the last router workgroup to finish routes every token (it resets the count)
             // the logits went out as device-coherent stores; the wait below makes them complete before the arrival
             __shared__ int s_last;
             __builtin_amdgcn_s_waitcnt(0);
@@ -233,9 +236,9 @@ __global__ __launch_bounds__(kK1Threads) void k_route_quant(const LayerArgs a) {
         return;
     }
     const int npad = (H + 511) / 512 * 512;
-    const int chunks = (npad + kK1Threads - 1) / kK1Threads;
+    const int chunks = (npad + NT - 1) / NT;
     const int chunk = blockIdx.x - n_router_wg;
-    const int t = chunk / chunks, i = (chunk % chunks) * kK1Threads + threadIdx.x;
+    const int t = chunk / chunks, i = (chunk % chunks) * NT + threadIdx.x;
     float v = i < H ? a.x[(size_t) t * H + i] : 0.0f;
     if (NORM && i < H) v = (s_scale[t] * v) * a.norm_w[i];
     const Q8Lane r = q8_1_lane(v);  // whole 32-lane blocks: the lanes past npad form whole blocks and store nothing
@@ -1087,12 +1090,13 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         for (int qi = lane; qi < 4 * nbg; qi += 32) {
             const int bb = qi >> 2, qt = qi & 3;
             const int off = rl * rbg + bb * BG;
+            const ActQ xq = act_q(img, bb, qt);  // shared by the gate and the up row
             if (staged) {
-                acc += quarter_dot<TGU, Aligned16>(s_gu + off, img, bb, qt);
-                accg += quarter_dot<TGU, Aligned16>(s_gu + gu_region + off, img, bb, qt);
+                acc += quarter_dot_r<TGU, Aligned16>(s_gu + off, xq, qt);
+                accg += quarter_dot_r<TGU, Aligned16>(s_gu + gu_region + off, xq, qt);
             } else {
-                acc += quarter_dot<TGU, Any2>(wa + off, img, bb, qt);
-                accg += quarter_dot<TGU, Any2>(wb + off, img, bb, qt);
+                acc += quarter_dot_r<TGU, Any2>(wa + off, xq, qt);
+                accg += quarter_dot_r<TGU, Any2>(wb + off, xq, qt);
             }
         }
         FNS_MARK(1, blockIdx.x, 5);
@@ -1689,14 +1693,16 @@ static int launch_shared(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t s
 
 static int launch_stage(const FnsMoeLayer *L, const LayerArgs &a, int stage, hipStream_t st) {
     if (stage == 0) {  // [RMSNorm +] router + Q8_1 of x, [shared expert]
-        const int chunks = (int) ((host::pad512(L->hidden) + kK1Threads - 1) / kK1Threads);
-        const int n_router_wg = (L->n_expert + kK1Rows - 1) / kK1Rows;
-        if (a.norm_w)
-            hipLaunchKernelGGL(k_route_quant<true>, dim3((unsigned) (n_router_wg + chunks * a.T)), dim3(kK1Threads), 0,
-                               st, a);
-        else
-            hipLaunchKernelGGL(k_route_quant<false>, dim3((unsigned) (n_router_wg + chunks * a.T)), dim3(kK1Threads), 0,
-                               st, a);
+        const int nt = a.T == 1 ? 256 : kK1Threads, rows = nt / 256;
+        const int chunks = (int) ((host::pad512(L->hidden) + nt - 1) / nt);
+        const dim3 grid((unsigned) ((L->n_expert + rows - 1) / rows + chunks * a.T));
+        if (a.T == 1) {
+            if (a.norm_w) hipLaunchKernelGGL((k_route_quant<true, 256>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_route_quant<false, 256>), grid, dim3(256), 0, st, a);
+        } else {
+            if (a.norm_w) hipLaunchKernelGGL((k_route_quant<true, kK1Threads>), grid, dim3(kK1Threads), 0, st, a);
+            else hipLaunchKernelGGL((k_route_quant<false, kK1Threads>), grid, dim3(kK1Threads), 0, st, a);
+        }
         FNS_TRY(host::check_launch("moe route_quant"));
         // (the shared expert runs inside the fused kernel when that takes the call)
         return L->shexp_inter > 0 && !(a.shd && use_fused(L, a)) ? launch_shared(L, a, st) : host::OK;
