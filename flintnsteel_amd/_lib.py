@@ -64,6 +64,17 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_fill_normal": [_P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F, _F, _P],
     "fns_hip_quantize_weights": [_I, _P, _P, _I64, _I64, _P],
     "fns_hip_selftest_lanes": [_P, _P],
+    "fns_hip_gguf_open": [ctypes.c_char_p, _P],
+    "fns_hip_gguf_close": [_P],
+    "fns_hip_gguf_info": [_P, _P, _P, _P, _P],
+    "fns_hip_gguf_tensor": [_P, ctypes.c_char_p, _P],
+    "fns_hip_gguf_tensor_at": [_P, _I64, _P, _P],
+    "fns_hip_gguf_get_u32": [_P, ctypes.c_char_p, _P],
+    "fns_hip_gguf_get_f32": [_P, ctypes.c_char_p, _P],
+    "fns_hip_gguf_get_bool": [_P, ctypes.c_char_p, _P],
+    "fns_hip_gguf_get_str": [_P, ctypes.c_char_p, _P],
+    "fns_hip_moe_layer_from_gguf": [_P, _I, _P, _P],
+    "fns_hip_moe_resident_free": [_P],
 }
 _RESTYPE = {
     "fns_hip_last_error": ctypes.c_char_p,
@@ -71,6 +82,8 @@ _RESTYPE = {
     "fns_hip_mmq_q8_1_bytes": _SZ,
     "fns_hip_mmq_bounds_bytes": _SZ,
     "fns_hip_moe_noalloc_max_bytes": _SZ,
+    "fns_hip_gguf_close": None,
+    "fns_hip_moe_resident_free": None,
 }
 
 _lib = None

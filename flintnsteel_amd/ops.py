@@ -273,6 +273,25 @@ class MoeLayer:
                                  sh["gate"].data_ptr() if sh else None, sh["up"].data_ptr() if sh else None,
                                  sh["down"].data_ptr() if sh else None)
 
+    @classmethod
+    def from_gguf(cls, file: "GgufFile", layer: int) -> "MoeLayer":
+        """MoE layer `layer` of a GGUF checkpoint made resident in HBM by fns_hip_moe_layer_from_gguf (expert slots,
+        table, router, norm and shared expert in library-owned device memory, freed with this object)."""
+        obj = cls.__new__(cls)
+        obj.desc = MoeLayerDesc()
+        obj.router_w = obj.slots = obj.router_bias = obj.ffn_norm = obj.shexp = None
+        obj._file = file  # the metadata stays readable while the layer lives
+        res = ctypes.c_void_p()
+        call("fns_hip_moe_layer_from_gguf", file.handle, layer, ctypes.byref(res), ctypes.byref(obj.desc))
+        obj._resident = res
+        return obj
+
+    def __del__(self):
+        res = getattr(self, "_resident", None)
+        if res:
+            lib().fns_hip_moe_resident_free(res)
+            self._resident = None
+
     def workspace_layout(self, n_tok: int):
         offs = (ctypes.c_size_t * 6)()
         total = ctypes.c_size_t()
@@ -439,3 +458,71 @@ def selftest_lanes() -> int:
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
     call("fns_hip_selftest_lanes", _p(bad), _s())
     return int(bad.item())
+
+
+class GgufTensorInfo(ctypes.Structure):
+    """Mirror of FnsGgufTensorInfo (include/fns_hip.h)."""
+    _fields_ = [("type", ctypes.c_int), ("n_dims", ctypes.c_int), ("ne", ctypes.c_int64 * 4),
+                ("nbytes", ctypes.c_size_t), ("offset", ctypes.c_size_t), ("data", ctypes.c_void_p)]
+
+
+class GgufFile:
+    """A GGUF checkpoint mapped by the library's reader (fns_hip_gguf_*; reference src/model.cpp:30-136)."""
+
+    def __init__(self, path: str):
+        self.handle = None
+        h = ctypes.c_void_p()
+        call("fns_hip_gguf_open", str(path).encode(), ctypes.byref(h))
+        self.handle = h
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().fns_hip_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def info(self) -> dict:
+        v, nt, nk, off = ctypes.c_uint32(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_size_t()
+        call("fns_hip_gguf_info", self.handle, ctypes.byref(v), ctypes.byref(nt), ctypes.byref(nk), ctypes.byref(off))
+        return {"version": v.value, "n_tensors": nt.value, "n_kv": nk.value, "data_offset": off.value}
+
+    def tensor(self, name: str) -> dict:
+        info = GgufTensorInfo()
+        call("fns_hip_gguf_tensor", self.handle, name.encode(), ctypes.byref(info))
+        return self._as_dict(info)
+
+    def tensors(self) -> list[tuple[str, dict]]:
+        out = []
+        for i in range(self.info()["n_tensors"]):
+            info, name = GgufTensorInfo(), ctypes.c_char_p()
+            call("fns_hip_gguf_tensor_at", self.handle, i, ctypes.byref(info), ctypes.byref(name))
+            out.append((name.value.decode(), self._as_dict(info)))
+        return out
+
+    @staticmethod
+    def _as_dict(info: GgufTensorInfo) -> dict:
+        raw = (ctypes.c_uint8 * info.nbytes).from_address(info.data) if info.nbytes else b""
+        return {"type": info.type, "ne": list(info.ne[: info.n_dims]), "nbytes": info.nbytes, "offset": info.offset,
+                "bytes": np.frombuffer(raw, dtype=np.uint8).copy() if info.nbytes else np.zeros(0, np.uint8)}
+
+    def u32(self, key: str) -> int:
+        v = ctypes.c_uint32()
+        call("fns_hip_gguf_get_u32", self.handle, key.encode(), ctypes.byref(v))
+        return v.value
+
+    def f32(self, key: str) -> float:
+        v = ctypes.c_float()
+        call("fns_hip_gguf_get_f32", self.handle, key.encode(), ctypes.byref(v))
+        return v.value
+
+    def bool(self, key: str) -> bool:
+        v = ctypes.c_int()
+        call("fns_hip_gguf_get_bool", self.handle, key.encode(), ctypes.byref(v))
+        return bool(v.value)
+
+    def str(self, key: str) -> str:
+        v = ctypes.c_char_p()
+        call("fns_hip_gguf_get_str", self.handle, key.encode(), ctypes.byref(v))
+        return v.value.decode()

@@ -23,6 +23,7 @@ extern "C" {
 #define FNS_ERR_SHAPE (-2)
 #define FNS_ERR_LAUNCH (-3)
 #define FNS_ERR_NOMEM (-4)
+#define FNS_ERR_IO (-5) /* a GGUF file that cannot be opened or is malformed */
 
 /* ggml type ids accepted by the quantized entry points (ggml.h numbering); router dtypes: 0 = f32, 30 = bf16. */
 #define FNS_TYPE_F32 0
@@ -210,6 +211,43 @@ int fns_hip_moe_prefill_workspace(const FnsMoeLayer *layer, int64_t n_tok, size_
 int fns_hip_moe_prefill_section(const FnsMoeLayer *layer, int64_t n_tok, int section, size_t *offset, size_t *bytes);
 int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int64_t n_tok,
                         void *workspace, size_t workspace_bytes, void *stream);
+
+/* --- GGUF checkpoints: reader and fully resident MoE layers ---
+ * Replaces the reference's loader (src/model.cpp:30-136: gguf header and tensor table, the file mapped without copying)
+ * and expert placement (src/engine.cu:375-471: slots [gate | up | down] 256-byte aligned with 4096 zero bytes after the
+ * last, a device table of slot pointers); every expert is resident in HBM. The reader is host code (no GPU needed);
+ * fns_hip_moe_layer_from_gguf copies with hipMemcpy on the current device. C++ interface: include/fns/gguf.h. */
+typedef struct FnsGguf FnsGguf;
+typedef struct FnsGgufTensorInfo {
+    int type;        /* ggml_type */
+    int n_dims;
+    int64_t ne[4];   /* ggml order: ne[0] contiguous */
+    size_t nbytes;
+    size_t offset;   /* from the start of the data section */
+    const void *data; /* host pointer into the mapping (valid until fns_hip_gguf_close) */
+} FnsGgufTensorInfo;
+/* Opens and maps `path`; FNS_ERR_IO (with the reason in fns_hip_last_error) on a missing or malformed file. */
+int fns_hip_gguf_open(const char *path, FnsGguf **out);
+void fns_hip_gguf_close(FnsGguf *file);
+int fns_hip_gguf_info(const FnsGguf *file, uint32_t *version, int64_t *n_tensors, int64_t *n_kv, size_t *data_offset);
+/* Tensor by name (FNS_ERR_SHAPE when absent) or by index; *name (optional) points into the reader. */
+int fns_hip_gguf_tensor(const FnsGguf *file, const char *name, FnsGgufTensorInfo *info);
+int fns_hip_gguf_tensor_at(const FnsGguf *file, int64_t index, FnsGgufTensorInfo *info, const char **name);
+/* gguf_get_val_u32 / f32 / bool / str of the reference's loader (src/model.cpp:19-26): FNS_ERR_SHAPE when the key is
+ * absent or of another type. *value of _str points into the reader. */
+int fns_hip_gguf_get_u32(const FnsGguf *file, const char *key, uint32_t *value);
+int fns_hip_gguf_get_f32(const FnsGguf *file, const char *key, float *value);
+int fns_hip_gguf_get_bool(const FnsGguf *file, const char *key, int *value);
+int fns_hip_gguf_get_str(const FnsGguf *file, const char *key, const char **value);
+/* MoE layer `layer` of the file made resident in HBM (blk.N.ffn_{gate,up,down}_exps.weight, ffn_gate_inp.weight,
+ * optional exp_probs_b.bias, ffn_norm.weight and ffn_{gate,up,down}_shexp.weight; metadata
+ * <arch>.expert_used_count, expert_weights_norm, expert_gating_func (1 softmax, 2 sigmoid; default sigmoid for
+ * "flint", the reference's gating), attention.layer_norm_rms_epsilon). Fills *desc for fns_hip_moe_layer /
+ * fns_hip_moe_prefill (guard = 1 for "flint", whose blocks apply the F16 guard, else 0); the device memory it points
+ * to is owned by *resident. */
+typedef struct FnsMoeResident FnsMoeResident;
+int fns_hip_moe_layer_from_gguf(const FnsGguf *file, int layer, FnsMoeResident **resident, FnsMoeLayer *desc);
+void fns_hip_moe_resident_free(FnsMoeResident *resident);
 
 /* --- seeded synthetic data on the device (benchmarks and large tests) ---
  * out[i] = mean + std * N(0,1), Philox-4x32-10 counter (offset + i) / 4 and Box-Muller; offset % 4 == 0. */

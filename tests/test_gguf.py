@@ -1,0 +1,174 @@
+"""GGUF checkpoints: the library's reader (fns_hip_gguf_*, include/fns/gguf.h) against files written by
+tests/gguf_writer.py, and MoE layers made resident from them (fns_hip_moe_layer_from_gguf).
+
+Reference: src/model.cpp:30-136 (gguf header and tensor table, tensors viewed in the mapped file),
+src/engine.cu:375-471 (expert slots [gate | up | down], the device table). The reader tests run on the CPU (no HIP
+call); the resident-layer tests run the GGUF-loaded layer and the same layer built directly from the generated
+arrays through the decode and prefill paths and require identical outputs, bit for bit: the loader must place every
+byte where the slot contract says (the directly built layers are pinned against the float64 oracle elsewhere)."""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.gguf_writer import (BF16, F32, GGUF_ARRAY, GGUF_BOOL, GGUF_F32, GGUF_I8, GGUF_STRING, GGUF_U32, bf16_bits,
+                               write_gguf)
+
+H, F, NE, K, FS = 512, 256, 16, 4, 512
+
+
+def _moe_file(path, arch="flint", gating=None, gu=orc.Q4_K, dn=orc.Q6_K, router_dtype=BF16, with_shexp=True,
+              with_bias=True, layer=1, seed=3, alignment=32):
+    """A checkpoint with one MoE block at blk.<layer> (Flint tensor names and metadata) and the arrays it holds."""
+    rng = np.random.default_rng(seed)
+    w = lambda *s: rng.normal(0, 0.02, s).astype(np.float32)  # noqa: E731
+    gate, up, down = orc.quantize(gu, w(NE, F, H)), orc.quantize(gu, w(NE, F, H)), orc.quantize(dn, w(NE, H, F))
+    router = w(NE, H) * 50
+    router_bits = bf16_bits(router) if router_dtype == BF16 else router
+    norm = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(NE)).astype(np.float32)
+    p = f"blk.{layer}."
+    tensors = [(p + "ffn_norm.weight", F32, [H], norm),
+               (p + "ffn_gate_inp.weight", router_dtype, [H, NE], router_bits),
+               (p + "ffn_gate_exps.weight", gu, [H, F, NE], gate),
+               (p + "ffn_up_exps.weight", gu, [H, F, NE], up),
+               (p + "ffn_down_exps.weight", dn, [F, H, NE], down)]
+    arrays = {"gate": gate, "up": up, "down": down, "router": router_bits, "norm": norm}
+    if with_bias:
+        tensors.append((p + "exp_probs_b.bias", F32, [NE], bias))
+        arrays["bias"] = bias
+    if with_shexp:
+        sg, su, sd = orc.quantize(gu, w(FS, H)), orc.quantize(gu, w(FS, H)), orc.quantize(dn, w(H, FS))
+        tensors += [(p + "ffn_gate_shexp.weight", gu, [H, FS], sg), (p + "ffn_up_shexp.weight", gu, [H, FS], su),
+                    (p + "ffn_down_shexp.weight", dn, [FS, H], sd)]
+        arrays.update(sg=sg, su=su, sd=sd)
+    kv = [("general.architecture", GGUF_STRING, arch), (f"{arch}.block_count", GGUF_U32, layer + 1),
+          (f"{arch}.expert_count", GGUF_U32, NE), (f"{arch}.expert_used_count", GGUF_U32, K),
+          (f"{arch}.expert_weights_norm", GGUF_BOOL, 1),
+          (f"{arch}.attention.layer_norm_rms_epsilon", GGUF_F32, 1e-6),
+          (f"{arch}.attention.sliding_window_pattern", GGUF_ARRAY, (GGUF_I8, [1, 0])),
+          ("tokenizer.ggml.tokens", GGUF_ARRAY, (GGUF_STRING, ["<s>", "a", "b"]))]
+    if gating is not None:
+        kv.append((f"{arch}.expert_gating_func", GGUF_U32, gating))
+    # a tensor of another kind first, so the MoE tensors sit at non-zero offsets
+    tensors.insert(0, ("token_embd.weight", 8, [H, 3], np.zeros(3 * H // 32 * 34, np.uint8) + 7))  # Q8_0
+    write_gguf(path, kv, tensors, alignment=alignment)
+    return arrays
+
+
+def test_reader_header_metadata_and_tensors(tmp_path):
+    from flintnsteel_amd import ops
+    path = tmp_path / "m.gguf"
+    arrays = _moe_file(path, alignment=64)
+    f = ops.GgufFile(path)
+    info = f.info()
+    assert info["version"] == 3 and info["n_tensors"] == 10 and info["n_kv"] == 9 and info["data_offset"] % 64 == 0
+    assert f.str("general.architecture") == "flint"
+    assert f.u32("flint.expert_used_count") == K and f.u32("flint.expert_count") == NE
+    assert f.bool("flint.expert_weights_norm") is True
+    assert abs(f.f32("flint.attention.layer_norm_rms_epsilon") - 1e-6) < 1e-12
+    t = f.tensor("blk.1.ffn_gate_exps.weight")
+    assert t["type"] == orc.Q4_K and t["ne"] == [H, F, NE] and t["offset"] % 64 == 0
+    assert np.array_equal(t["bytes"], arrays["gate"].reshape(-1))
+    assert np.array_equal(f.tensor("blk.1.ffn_down_exps.weight")["bytes"], arrays["down"].reshape(-1))
+    r = f.tensor("blk.1.ffn_gate_inp.weight")
+    assert r["type"] == BF16 and r["ne"] == [H, NE] and np.array_equal(r["bytes"].view(np.uint16), arrays["router"].reshape(-1))
+    names = [n for n, _ in f.tensors()]
+    assert names[0] == "token_embd.weight" and "blk.1.ffn_down_shexp.weight" in names
+    from flintnsteel_amd._lib import FnsError
+    with pytest.raises(FnsError, match="no tensor"):
+        f.tensor("blk.1.nope")
+    with pytest.raises(FnsError, match="missing"):
+        f.u32("flint.nope")
+    with pytest.raises(FnsError, match="not a u32"):
+        f.u32("general.architecture")
+
+
+def test_reader_rejects_malformed_files(tmp_path):
+    from flintnsteel_amd import ops
+    from flintnsteel_amd._lib import FnsError
+    good = tmp_path / "good.gguf"
+    _moe_file(good, with_shexp=False)
+    data = good.read_bytes()
+    cases = {"bad magic": b"GGUX" + data[4:], "truncated file|larger than the file": data[:600],
+             "truncated file|implausible": data[:300],
+             "unsupported version": data[:4] + struct.pack("<I", 9) + data[8:],
+             "tensor outside the file": data[:-4096]}
+    for what, blob in cases.items():
+        p = tmp_path / "bad.gguf"
+        p.write_bytes(blob)
+        with pytest.raises(FnsError, match=what):
+            ops.GgufFile(p)
+    with pytest.raises(FnsError, match="cannot open"):
+        ops.GgufFile(tmp_path / "missing.gguf")
+
+
+def test_layer_build_rejects_unsupported_checkpoints(tmp_path):
+    """Shape and type checks run before any device allocation (CPU): unsupported expert type, missing tensors."""
+    from flintnsteel_amd import ops
+    from flintnsteel_amd._lib import FnsError
+    p = tmp_path / "q2k.gguf"
+    rng = np.random.default_rng(0)
+    q2k = rng.integers(0, 255, NE * F * (H // 256) * 84, dtype=np.uint8)
+    write_gguf(p, [("general.architecture", GGUF_STRING, "flint"), ("flint.expert_used_count", GGUF_U32, K)],
+               [("blk.0.ffn_gate_exps.weight", 10, [H, F, NE], q2k), ("blk.0.ffn_up_exps.weight", 10, [H, F, NE], q2k),
+                ("blk.0.ffn_down_exps.weight", 10, [F, H, NE], q2k),
+                ("blk.0.ffn_gate_inp.weight", F32, [H, NE], np.zeros(H * NE, np.float32))])
+    f = ops.GgufFile(p)
+    with pytest.raises(FnsError, match="not supported by the GEMV kernels"):
+        ops.MoeLayer.from_gguf(f, 0)
+    with pytest.raises(FnsError, match="missing tensor"):
+        ops.MoeLayer.from_gguf(f, 3)
+
+
+def _direct_layer(ops, torch, arrays, gu, dn, router_dtype, gating, guard, with_shexp, with_bias):
+    """The same layer built from the arrays through ops.MoeLayer (ExpertSlots)."""
+    slots = ops.ExpertSlots.from_tensors(torch.from_numpy(arrays["gate"].reshape(NE, -1)),
+                                         torch.from_numpy(arrays["up"].reshape(NE, -1)),
+                                         torch.from_numpy(arrays["down"].reshape(NE, -1)))
+    if router_dtype == BF16:
+        router = torch.from_numpy(arrays["router"].astype(np.int16)).view(torch.bfloat16).cuda()
+    else:
+        router = torch.from_numpy(arrays["router"]).cuda()
+    shexp = None
+    if with_shexp:
+        shexp = {"gate": torch.from_numpy(arrays["sg"]).cuda(), "up": torch.from_numpy(arrays["su"]).cuda(),
+                 "down": torch.from_numpy(arrays["sd"]).cuda(), "inter": FS, "gu_type": gu, "down_type": dn}
+    return ops.MoeLayer(router, slots, gu, dn, H, F, K, gating=gating, guard=guard,
+                        router_bias=torch.from_numpy(arrays["bias"]).cuda() if with_bias else None,
+                        ffn_norm=torch.from_numpy(arrays["norm"]).cuda(), norm_eps=1e-6, shexp=shexp)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", ["flint", "softmax_f32"])
+def test_gguf_layer_equals_directly_built_layer(tmp_path, variant):
+    import torch
+    from flintnsteel_amd import ops, synth
+    flint = variant == "flint"
+    kw = dict(arch="flint" if flint else "testmoe", gating=None if flint else 1,
+              router_dtype=BF16 if flint else F32, with_shexp=flint, with_bias=flint)
+    print(f"gguf layer variant {variant}", flush=True)
+    path = tmp_path / "m.gguf"
+    arrays = _moe_file(path, **kw)
+    f = ops.GgufFile(path)
+    g = ops.MoeLayer.from_gguf(f, 1)
+    d = g.desc
+    assert (d.hidden, d.inter, d.n_expert, d.k) == (H, F, NE, K)
+    assert d.gating == (ops.GATING_SIGMOID if flint else ops.GATING_SOFTMAX) and d.norm_w == 1
+    assert d.guard == int(flint) and d.shexp_inter == (FS if flint else 0)
+    ref = _direct_layer(ops, torch, arrays, orc.Q4_K, orc.Q6_K, kw["router_dtype"], d.gating, bool(d.guard),
+                        kw["with_shexp"], kw["with_bias"])
+    for n_tok in (1, 4):
+        x = synth.activations(n_tok, H, 5, layer=n_tok)
+        a, b = g(x, x_resid=x), ref(x, x_resid=x)
+        torch.cuda.synchronize()
+        assert np.array_equal(a.cpu().numpy(), b.cpu().numpy()), f"decode/verify n_tok={n_tok} differs"
+    x = synth.activations(37, H, 5, layer=9)
+    a, b = ops.MoePrefill(g)(x, x_resid=x), ops.MoePrefill(ref)(x, x_resid=x)
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy(), b.cpu().numpy()), "prefill differs"
+    del g
+    f.close()
