@@ -35,6 +35,7 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_mmvq_experts_swiglu": [_I, _P, _SZ, _SZ, _I64, _I64, _P, _I64, _P, _I64, _P, _P],
     "fns_hip_mmvq_experts": [_I, _P, _SZ, _I64, _I64, _P, _I64, _P, _I64, _P, _P],
     "fns_hip_mmvq_supports": [_I],
+    "fns_hip_set_iq_grids": [_P, _P, _P],
     "fns_hip_rms_norm_q8_1": [_P, _P, _P, _P, _I, _F, _I, _P],
     "fns_hip_gemv_router": [_I, _P, _P, _P, _I, _I, _I, _P],
     "fns_hip_gemm_router": [_I, _P, _P, _P, _I, _I, _I, _P],

@@ -1,5 +1,8 @@
 // capi.cpp - extern "C" entry points of libfns_hip.so (include/fns_hip.h): thin forwards to fns::impl.
 #include "fns_hip.h"
+#include "fns/ggml_kernels.h"
+
+#include <cstring>
 
 #include "fns_host.hpp"
 #include "fns_internal.hpp"
@@ -55,6 +58,29 @@ int fns_hip_mmvq_experts(int type, const void *const *table, size_t off, int64_t
 }
 
 int fns_hip_mmvq_supports(int type) { return host::is_supported(type) ? 1 : 0; }
+
+int fns_hip_set_iq_grids(const uint32_t *iq3xxs, const uint32_t *iq3s, const uint64_t *iq2s) {
+    if (!iq3xxs || !iq3s || !iq2s) return host::set_error(host::ERR_SHAPE, "set_iq_grids: null table");
+    struct {
+        uint32_t a[256];
+        uint32_t b[512];
+        uint64_t c[1024];
+    } g;
+    static_assert(sizeof g == 256 * 4 + 512 * 4 + 1024 * 8, "packed like dev::IqGrids");
+    std::memcpy(g.a, iq3xxs, sizeof g.a);
+    std::memcpy(g.b, iq3s, sizeof g.b);
+    std::memcpy(g.c, iq2s, sizeof g.c);
+    // the decoders negate a codebook byte as (g ^ 0xff) + 1 within its byte: every value must be non-zero
+    const uint8_t *bytes = (const uint8_t *) &g;
+    for (size_t i = 0; i < sizeof g; ++i)
+        if (bytes[i] == 0 || bytes[i] > 127)
+            return host::set_error(host::ERR_SHAPE, "set_iq_grids: codebook byte %zu is %d (values must be 1..127)", i,
+                                   bytes[i]);
+    FNS_TRY(impl::iq_grids_upload_mmvq(&g));
+    FNS_TRY(impl::iq_grids_upload_layer(&g));
+    host::set_iq_grids_ready();
+    return host::OK;
+}
 
 int fns_hip_rms_norm_q8_1(const float *x, const float *w, float *out, void *xq, int n, float eps, int rows,
                           void *stream) {
@@ -181,3 +207,10 @@ int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x
     return impl::moe_prefill(layer, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream));
 }
 }  // extern "C"
+
+// C++ API form (include/fns/ggml_kernels.h): aborts on bad tables, as the reference's API aborts on errors.
+namespace fns {
+void set_iq_grids(const uint32_t *iq3xxs, const uint32_t *iq3s, const uint64_t *iq2s) {
+    host::abort_on_error(fns_hip_set_iq_grids(iq3xxs, iq3s, iq2s), "set_iq_grids");
+}
+}  // namespace fns

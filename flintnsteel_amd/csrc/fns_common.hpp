@@ -33,7 +33,10 @@ namespace fns::dev {
 
 constexpr int kWave = 64;
 
-enum : int { T_Q8_0 = 8, T_Q8_1 = 9, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30 };
+enum : int {
+    T_Q8_0 = 8, T_Q8_1 = 9, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
+    T_IQ3_XXS = 18, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23, T_BF16 = 30
+};
 
 template <int T> struct Traits;
 template <> struct Traits<T_Q3_K> { static constexpr int bytes = 110, slots = 4; };
@@ -42,9 +45,19 @@ template <> struct Traits<T_Q5_K> { static constexpr int bytes = 176, slots = 8;
 template <> struct Traits<T_Q6_K> { static constexpr int bytes = 210, slots = 8; };
 // Q8_0 (34 B per 32 values: half d | int8 qs[32]): the kernels' 256-value unit is 8 consecutive blocks (272 B).
 template <> struct Traits<T_Q8_0> { static constexpr int bytes = 272, slots = 4; };
+// IQ formats (256 values per block; decoded by the quarter kernels only):
+//   IQ4_XS 136 B: half d | u16 scales_h | scales_l[4] | qs[128] (4-bit indices into the IQ4_NL values)
+//   IQ3_XXS 98 B: half d | grid indices[64] | 8 x u32 (4 x 7 sign bits + 4-bit scale per 32 values)
+//   IQ3_S  110 B: half d | grid indices[64] | qh[8] (9th index bits) | signs[32] | scales[4] (4 bits per 32 values)
+//   IQ2_S   82 B: half d | grid indices[32] | signs[32] | qh[8] (2 high index bits per 8 values) | scales[8]
+template <> struct Traits<T_IQ4_XS> { static constexpr int bytes = 136, slots = 4; };
+template <> struct Traits<T_IQ3_XXS> { static constexpr int bytes = 98, slots = 4; };
+template <> struct Traits<T_IQ3_S> { static constexpr int bytes = 110, slots = 4; };
+template <> struct Traits<T_IQ2_S> { static constexpr int bytes = 82, slots = 4; };
 
 __host__ __device__ constexpr int block_bytes(int t) {
-    return t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 272 : 0;
+    return t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 272
+         : t == T_IQ4_XS ? 136 : t == T_IQ3_XXS ? 98 : t == T_IQ3_S ? 110 : t == T_IQ2_S ? 82 : 0;
 }
 
 __device__ __forceinline__ float half_to_float(uint32_t bits16) {

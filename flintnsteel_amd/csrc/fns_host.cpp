@@ -1,6 +1,7 @@
 // fns_host.cpp - error reporting shared by the C ABI and the C++ API.
 #include "fns_host.hpp"
 
+#include <atomic>
 #include <cstdarg>
 #include <cstring>
 
@@ -19,6 +20,12 @@ int set_error(int code, const char *fmt, ...) {
 }
 
 const char *last_error() { return g_msg; }
+
+namespace {
+std::atomic<bool> g_iq_ready{false};
+}
+bool iq_grids_ready() { return g_iq_ready.load(std::memory_order_acquire); }
+void set_iq_grids_ready() { g_iq_ready.store(true, std::memory_order_release); }
 
 int check_launch(const char *what) {
     const hipError_t e = hipGetLastError();

@@ -32,13 +32,22 @@ void abort_on_error(int rc, const char *what);
 
 inline int64_t pad512(int64_t n) { return (n + 511) / 512 * 512; }
 inline bool is_kquant(int t) { return t == 11 || t == 12 || t == 13 || t == 14; }
-// Types that only the quarter-block kernels decode (no K-quant sub-block machinery): Q8_0.
-inline bool is_quarter_only(int t) { return t == 8; }
+// IQ formats: IQ3_XXS (18), IQ3_S (21), IQ2_S (22), IQ4_XS (23); the first three decode through codebooks that the
+// engine registers (fns_hip_set_iq_grids).
+inline bool is_iq(int t) { return t == 18 || t == 21 || t == 22 || t == 23; }
+inline bool iq_needs_grid(int t) { return t == 18 || t == 21 || t == 22; }
+bool iq_grids_ready();
+void set_iq_grids_ready();
+// Types that only the quarter-block kernels decode (no K-quant sub-block machinery): Q8_0 and the IQ formats.
+inline bool is_quarter_only(int t) { return t == 8 || is_iq(t); }
 // Every weight type the GEMV paths accept (mmvq_supports).
-inline bool is_supported(int t) { return is_kquant(t) || is_quarter_only(t); }
-// Bytes of 256 consecutive values of a row (a K-quant block; 8 Q8_0 blocks).
+inline bool is_supported(int t) {
+    return is_kquant(t) || t == 8 || (is_iq(t) && (!iq_needs_grid(t) || iq_grids_ready()));
+}
+// Bytes of 256 consecutive values of a row (a K-quant or IQ block; 8 Q8_0 blocks).
 inline int64_t kquant_block_bytes(int t) {
-    return t == 11 ? 110 : t == 12 ? 144 : t == 13 ? 176 : t == 14 ? 210 : t == 8 ? 272 : 0;
+    return t == 11 ? 110 : t == 12 ? 144 : t == 13 ? 176 : t == 14 ? 210 : t == 8 ? 272 : t == 23 ? 136 : t == 18 ? 98
+         : t == 21 ? 110 : t == 22 ? 82 : 0;
 }
 inline int64_t q8_1_row_bytes(int64_t ncols) { return pad512(ncols) / 32 * 36; }
 

@@ -221,6 +221,152 @@ template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Any2>(const u
     return q80_quarter(blk, x, qt);
 }
 
+// ---- IQ formats: quarter qt = sub-blocks 2qt and 2qt+1 (32 values each). Per sub-block the integer arithmetic of
+// the reference's GPU products (src/ggml/ggml_mmvq.cu:101-157 for IQ3_XXS / IQ3_S; ggml vecdotq.cuh
+// vec_dot_iq4_xs_q8_1 / vec_dot_iq2_s_q8_1 for IQ4_XS / IQ2_S): an exact v_dot4 sum, the sub-block scale applied in
+// integers (C division truncating toward zero), then (d_w * d8) * sum in fp32; the quarter returns the two sub-block
+// terms added in order.
+
+// The IQ3_XXS / IQ3_S / IQ2_S codebooks (ggml's iq3xxs_grid, iq3s_grid, iq2s_grid). The library does not carry them:
+// the engine registers its copies once per device (fns_hip_set_iq_grids), which fills this array of every translation
+// unit that decodes IQ blocks. Codebook values are positive bytes (never 0), which the sign step below relies on.
+struct IqGrids {
+    uint32_t iq3xxs[256];
+    uint32_t iq3s[512];
+    uint64_t iq2s[1024];
+};
+static __device__ IqGrids g_iq_grids;
+
+// The IQ4_NL values {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113} as four byte tables.
+constexpr uint32_t kIq4T0 = 0xBFAD9881u, kIq4T1 = 0xF6EADDCFu, kIq4T2 = 0x26190D01u, kIq4T3 = 0x71594535u;
+// Four 4-bit indices (one per byte) -> their four int8 values: v_perm picks from entries 0-7 and 8-15, bit 3 chooses.
+__device__ __forceinline__ uint32_t iq4nl_values(uint32_t nib) {
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4T1, kIq4T0, sel), hi = __builtin_amdgcn_perm(kIq4T3, kIq4T2, sel);
+    const uint32_t e = (nib >> 3) & 0x01010101u;
+    const uint32_t m = (e << 8) - e;  // 0xff in the bytes whose index is >= 8
+    return (hi & m) | (lo & ~m);
+}
+// Four sign bits -> one bit per byte (bit j -> byte j, bit 0).
+__device__ __forceinline__ uint32_t spread4(uint32_t s4) { return (s4 * 0x00204081u) & 0x01010101u; }
+// Four positive codebook bytes with the signs of spread4 applied: per byte (g ^ 0xff) + 1 = -g, which cannot carry
+// into the next byte because g >= 1.
+__device__ __forceinline__ int signed_grid(uint32_t g, uint32_t e) { return (int) ((g ^ ((e << 8) - e)) + e); }
+// The 7 stored sign bits of an IQ3_XXS group plus the eighth that makes the count of negative signs even.
+__device__ __forceinline__ uint32_t ksigns(uint32_t v7) { return v7 | ((uint32_t) (__builtin_popcount(v7) & 1) << 7); }
+__device__ __forceinline__ uint32_t ld8u(const uint8_t *p) { return (uint32_t) *p; }
+
+__device__ __forceinline__ float iq4xs_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+    const uint32_t h0 = ld32u(blk), sl = ld32u(blk + 4);
+    const float d = half_to_float(h0 & 0xffffu);
+    const uint32_t sh = h0 >> 16;
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int ib = 2 * qt + h;
+        const uint4 q = lds16u(blk + 8 + 16 * ib);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s = dot4((int) iq4nl_values(w[i] & kLo4), x.a[8 * h + i], s);
+            s = dot4((int) iq4nl_values((w[i] >> 4) & kLo4), x.a[8 * h + 4 + i], s);
+        }
+        const int ls = (int) (((sl >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xfu) | (((sh >> (2 * ib)) & 3u) << 4));
+        s *= ls - 32;
+        acc += (d * x.d[h]) * (float) s;
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float iq3xxs_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+    const float d = half_to_float(ld32u(blk) & 0xffffu);
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int ib = 2 * qt + h;
+        const uint32_t i0 = ld32u(blk + 2 + 8 * ib), i1 = ld32u(blk + 6 + 8 * ib);
+        const uint32_t aux = ld32u(blk + 66 + 4 * ib);
+        int s = 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t idx = l < 2 ? i0 : i1, sh = 16 * (l & 1);
+            const uint32_t sg = ksigns((aux >> (7 * l)) & 127u);
+            const uint32_t g0 = g_iq_grids.iq3xxs[(idx >> sh) & 0xffu], g1 = g_iq_grids.iq3xxs[(idx >> (sh + 8)) & 0xffu];
+            s = dot4(signed_grid(g0, spread4(sg & 0xfu)), x.a[8 * h + 2 * l], s);
+            s = dot4(signed_grid(g1, spread4(sg >> 4)), x.a[8 * h + 2 * l + 1], s);
+        }
+        const int ls = (int) (aux >> 28);
+        s = (ls * s + s / 2) / 2;
+        acc += (d * x.d[h]) * (float) s;
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float iq3s_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+    const float d = half_to_float(ld32u(blk) & 0xffffu);
+    const uint32_t scw = ld32u(blk + 106);
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int ib = 2 * qt + h;
+        const uint32_t i0 = ld32u(blk + 2 + 8 * ib), i1 = ld32u(blk + 6 + 8 * ib);
+        const uint32_t qh = ld8u(blk + 66 + ib), sg = ld32u(blk + 74 + 4 * ib);
+        int s = 0;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const uint32_t gi = (((l < 4 ? i0 : i1) >> (8 * (l & 3))) & 0xffu) | (((qh >> l) & 1u) << 8);
+            const uint32_t sb = (sg >> (4 * l)) & 0xfu;  // byte l/2, nibble l%2
+            s = dot4(signed_grid(g_iq_grids.iq3s[gi], spread4(sb)), x.a[8 * h + l], s);
+        }
+        s *= 1 + 2 * (int) ((scw >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xfu);
+        acc += (d * x.d[h]) * (float) s;
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float iq2s_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+    const float d = half_to_float(ld32u(blk) & 0xffffu);
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int ib = 2 * qt + h;
+        const uint32_t idx = ld32u(blk + 2 + 4 * ib), sg = ld32u(blk + 34 + 4 * ib);
+        const uint32_t qh = ld8u(blk + 66 + ib), sc = ld8u(blk + 74 + ib);
+        int s2[2] = {0, 0};
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t gi = ((idx >> (8 * l)) & 0xffu) | (((qh >> (2 * l)) & 3u) << 8);
+            const uint64_t g = g_iq_grids.iq2s[gi];
+            const uint32_t sb = (sg >> (8 * l)) & 0xffu;
+            s2[l >> 1] = dot4(signed_grid((uint32_t) g, spread4(sb & 0xfu)), x.a[8 * h + 2 * l], s2[l >> 1]);
+            s2[l >> 1] = dot4(signed_grid((uint32_t) (g >> 32), spread4(sb >> 4)), x.a[8 * h + 2 * l + 1], s2[l >> 1]);
+        }
+        const int ls0 = (int) (sc & 0xfu), ls1 = (int) (sc >> 4);
+        const int s = (s2[0] * ls0 + s2[1] * ls1 + (s2[0] + s2[1]) / 2) / 4;
+        acc += (d * x.d[h]) * (float) s;
+    }
+    return acc;
+}
+
+#define FNS_IQ_QUARTER(T, F)                                                                                        \
+    template <> __device__ __forceinline__ float quarter_dot_r<T, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) { \
+        return F(blk, x, qt);                                                                                        \
+    }                                                                                                                \
+    template <> __device__ __forceinline__ float quarter_dot_r<T, Any2>(const uint8_t *blk, const ActQ &x, int qt) {     \
+        return F(blk, x, qt);                                                                                        \
+    }
+FNS_IQ_QUARTER(T_IQ4_XS, iq4xs_quarter)
+FNS_IQ_QUARTER(T_IQ3_XXS, iq3xxs_quarter)
+FNS_IQ_QUARTER(T_IQ3_S, iq3s_quarter)
+FNS_IQ_QUARTER(T_IQ2_S, iq2s_quarter)
+#undef FNS_IQ_QUARTER
+
+// Copies the codebooks into this translation unit's g_iq_grids on the current device.
+static inline hipError_t upload_iq_grids(const IqGrids *host) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_iq_grids), host, sizeof(IqGrids), 0, hipMemcpyHostToDevice);
+}
+
 // The quarter dot against an activation row image (the activation quarter read from LDS for this one product).
 template <int T, class L> __device__ __forceinline__ float quarter_dot(const uint8_t *blk, const ActImg &x, int bb, int qt) {
     return quarter_dot_r<T, L>(blk, act_q(x, bb, qt), qt);

@@ -309,6 +309,10 @@ template <int NC, bool GLU> int launch_type(int type, const MmvqParams &p, int n
         case T_Q5_K: return launch_nc<T_Q5_K, NC, GLU>(p, n_chan, st);
         case T_Q6_K: return launch_nc<T_Q6_K, NC, GLU>(p, n_chan, st);
         case T_Q8_0: return launch_q<T_Q8_0, NC, GLU>(p, n_chan, st);
+        case T_IQ4_XS: return launch_q<T_IQ4_XS, NC, GLU>(p, n_chan, st);
+        case T_IQ3_XXS: return launch_q<T_IQ3_XXS, NC, GLU>(p, n_chan, st);
+        case T_IQ3_S: return launch_q<T_IQ3_S, NC, GLU>(p, n_chan, st);
+        case T_IQ2_S: return launch_q<T_IQ2_S, NC, GLU>(p, n_chan, st);
         default: return host::set_error(host::ERR_TYPE, "mmvq: ggml type %d not supported", type);
     }
 }
@@ -498,5 +502,13 @@ void mmvq_experts(ggml_type type, const char *const *table, size_t off, int64_t 
                          "mmvq_experts");
 }
 bool mmvq_supports(ggml_type type) { return host::is_supported((int) type); }
+
+namespace impl {
+// This translation unit's copy of the IQ codebooks (fns_quarter.hpp g_iq_grids), on the current device.
+int iq_grids_upload_mmvq(const void *grids) {
+    const hipError_t e = dev::upload_iq_grids((const dev::IqGrids *) grids);
+    return e == hipSuccess ? host::OK : host::set_error(host::ERR_LAUNCH, "set_iq_grids: %s", hipGetErrorString(e));
+}
+}  // namespace impl
 
 }  // namespace fns

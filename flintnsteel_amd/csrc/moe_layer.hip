@@ -1317,7 +1317,8 @@ template <int TQ, int LPR> int launch_gate_up_lds(const LayerArgs &a, size_t lds
 }
 
 // Types that only the quarter kernels decode (the register- and LDS-staged whole-block forms are K-quant only).
-template <int T> constexpr bool kQuarterOnly = T == T_Q8_0;
+template <int T> constexpr bool kQuarterOnly = T == T_Q8_0 || T == T_IQ4_XS || T == T_IQ3_XXS || T == T_IQ3_S ||
+                                               T == T_IQ2_S;
 
 template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
     const int nblk = a.H / 256;
@@ -1413,6 +1414,18 @@ template <int TGU> const void *fused_fn_by_down(int tdn, bool sh) {
 }
 const void *fused_kernel(int tgu, int tdn, bool sh) {
     if (tgu == T_Q8_0 || tdn == T_Q8_0) return tgu == tdn ? fused_fn<T_Q8_0, T_Q8_0>(sh) : nullptr;
+    // IQ formats: the mixes of the reference's checkpoints (IQ3_XXS / IQ3_S / IQ2_S / IQ4_XS gate and up over an
+    // IQ4_XS down); other mixes that involve them take the three-kernel path
+    if (host::is_iq(tgu) || host::is_iq(tdn)) {
+        if (tdn != T_IQ4_XS) return nullptr;
+        switch (tgu) {
+            case T_IQ4_XS: return fused_fn<T_IQ4_XS, T_IQ4_XS>(sh);
+            case T_IQ3_XXS: return fused_fn<T_IQ3_XXS, T_IQ4_XS>(sh);
+            case T_IQ3_S: return fused_fn<T_IQ3_S, T_IQ4_XS>(sh);
+            case T_IQ2_S: return fused_fn<T_IQ2_S, T_IQ4_XS>(sh);
+        }
+        return nullptr;
+    }
     switch (tgu) {
         case T_Q3_K: return fused_fn_by_down<T_Q3_K>(tdn, sh);
         case T_Q4_K: return fused_fn_by_down<T_Q4_K>(tdn, sh);
@@ -1471,6 +1484,10 @@ int by_type_gate_up(int t, const LayerArgs &a, hipStream_t st) {
         case T_Q5_K: return dispatch_gate_up<T_Q5_K>(a, st);
         case T_Q6_K: return dispatch_gate_up<T_Q6_K>(a, st);
         case T_Q8_0: return dispatch_gate_up<T_Q8_0>(a, st);
+        case T_IQ4_XS: return dispatch_gate_up<T_IQ4_XS>(a, st);
+        case T_IQ3_XXS: return dispatch_gate_up<T_IQ3_XXS>(a, st);
+        case T_IQ3_S: return dispatch_gate_up<T_IQ3_S>(a, st);
+        case T_IQ2_S: return dispatch_gate_up<T_IQ2_S>(a, st);
     }
     return host::set_error(host::ERR_TYPE, "moe_layer: gate/up type %d not supported", t);
 }
@@ -1482,6 +1499,10 @@ int by_type_down(int t, const LayerArgs &a, hipStream_t st) {
         case T_Q5_K: return dispatch_down<T_Q5_K>(a, st);
         case T_Q6_K: return dispatch_down<T_Q6_K>(a, st);
         case T_Q8_0: return dispatch_down<T_Q8_0>(a, st);
+        case T_IQ4_XS: return dispatch_down<T_IQ4_XS>(a, st);
+        case T_IQ3_XXS: return dispatch_down<T_IQ3_XXS>(a, st);
+        case T_IQ3_S: return dispatch_down<T_IQ3_S>(a, st);
+        case T_IQ2_S: return dispatch_down<T_IQ2_S>(a, st);
     }
     return host::set_error(host::ERR_TYPE, "moe_layer: down type %d not supported", t);
 }
@@ -1781,6 +1802,12 @@ int moe_layer_noalloc(const FnsMoeLayer *L, const float *x, const float *x_resid
 }
 
 size_t moe_noalloc_max_bytes() { return kScratchBytes; }
+
+// This translation unit's copy of the IQ codebooks (fns_quarter.hpp g_iq_grids), on the current device.
+int iq_grids_upload_layer(const void *grids) {
+    const hipError_t e = dev::upload_iq_grids((const dev::IqGrids *) grids);
+    return e == hipSuccess ? host::OK : host::set_error(host::ERR_LAUNCH, "set_iq_grids: %s", hipGetErrorString(e));
+}
 
 // The sticky status word of a workspace (ws null: this device's no-allocation scratch), read after the stream's work
 // so far has completed; clear: zero it afterwards (a kernel on `st`).

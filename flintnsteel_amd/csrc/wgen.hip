@@ -427,7 +427,8 @@ int fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, float mea
 }
 
 int quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, hipStream_t st) {
-    if (!host::is_supported(type)) return host::set_error(host::ERR_TYPE, "quantize_weights: type %d not supported", type);
+    if (!host::is_kquant(type) && type != T_Q8_0)
+        return host::set_error(host::ERR_TYPE, "quantize_weights: type %d not supported", type);
     if (!x || !out || nrows < 0 || ncols <= 0 || ncols % 256)
         return host::set_error(host::ERR_SHAPE, "quantize_weights: ncols must be a positive multiple of 256");
     const int64_t nb = nrows * (ncols / 256);

@@ -26,6 +26,10 @@ enum ggml_type : int {
     GGML_TYPE_Q4_K = 12,
     GGML_TYPE_Q5_K = 13,
     GGML_TYPE_Q6_K = 14,
+    GGML_TYPE_IQ3_XXS = 18,
+    GGML_TYPE_IQ3_S = 21,
+    GGML_TYPE_IQ2_S = 22,
+    GGML_TYPE_IQ4_XS = 23,
     GGML_TYPE_BF16 = 30,
 };
 #endif
@@ -109,5 +113,10 @@ void flash_attn_prefill(const float *q, const void *kc, const void *vc, const vo
 // Quantized types this path accepts: Q8_0 and the K-quants (Q3_K added for the configs' UD-Q3_K_XL-like mix).
 // Reference: include/fns/ggml_kernels.h:79-80, src/ggml/ggml_mmvq.cu:403-411.
 bool mmvq_supports(ggml_type type);
+
+// No counterpart in the reference (its ggml build compiles the IQ codebooks in): registers ggml's iq3xxs_grid[256],
+// iq3s_grid[512] and iq2s_grid[1024] on the current device, once per device, before IQ3_XXS / IQ3_S / IQ2_S products;
+// mmvq_supports rejects those types until then. Aborts on bad tables (every byte must be 1..127).
+void set_iq_grids(const uint32_t *iq3xxs, const uint32_t *iq3s, const uint64_t *iq2s);
 
 }  // namespace fns

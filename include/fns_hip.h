@@ -32,6 +32,10 @@ extern "C" {
 #define FNS_TYPE_Q4_K 12
 #define FNS_TYPE_Q5_K 13
 #define FNS_TYPE_Q6_K 14
+#define FNS_TYPE_IQ3_XXS 18
+#define FNS_TYPE_IQ3_S 21
+#define FNS_TYPE_IQ2_S 22
+#define FNS_TYPE_IQ4_XS 23
 #define FNS_TYPE_BF16 30
 
 #define FNS_GATING_SOFTMAX 0
@@ -68,6 +72,11 @@ int fns_hip_mmvq_experts(int type, const void *const *table, size_t off, int64_t
                          int64_t n_xq, const int32_t *ids, int64_t n_ids, float *dst, void *stream);
 /* include/fns/ggml_kernels.h:79-80 mmvq_supports */
 int fns_hip_mmvq_supports(int type);
+/* No counterpart in the reference, whose ggml build compiles the IQ codebooks in: registers ggml's iq3xxs_grid[256],
+ * iq3s_grid[512] and iq2s_grid[1024] (the engine's own copies) on the current device; call once per device before
+ * any IQ3_XXS / IQ3_S / IQ2_S product. Until then mmvq_supports rejects those three types (IQ4_XS needs no table).
+ * Every codebook byte must be 1..127, as ggml's are. Synchronous (hipMemcpyToSymbol); not graph-capturable. */
+int fns_hip_set_iq_grids(const uint32_t *iq3xxs, const uint32_t *iq3s, const uint64_t *iq2s);
 
 /* --- kernels.cuh MoE subset (reference src/kernels.cuh, namespace fns::k) --- */
 

@@ -31,6 +31,36 @@ _Static_assert(sizeof(blk_q4_K) == 144, "q4_K block is 144 bytes");
 _Static_assert(sizeof(blk_q5_K) == 176, "q5_K block is 176 bytes");
 _Static_assert(sizeof(blk_q6_K) == 210, "q6_K block is 210 bytes");
 
+/* IQ formats (ggml-common.h block_iq4_xs / block_iq3_xxs / block_iq3_s / block_iq2_s). */
+typedef struct { uint16_t d; uint16_t scales_h; uint8_t scales_l[4]; uint8_t qs[128]; } blk_iq4_xs;
+typedef struct { uint16_t d; uint8_t qs[96]; } blk_iq3_xxs;  /* 64 grid indices, then 8 words of signs + scale */
+typedef struct { uint16_t d; uint8_t qs[64]; uint8_t qh[8]; uint8_t signs[32]; uint8_t scales[4]; } blk_iq3_s;
+typedef struct { uint16_t d; uint8_t qs[64]; uint8_t qh[8]; uint8_t scales[8]; } blk_iq2_s;  /* qs: 32 idx, 32 signs */
+_Static_assert(sizeof(blk_iq4_xs) == 136, "iq4_xs block is 136 bytes");
+_Static_assert(sizeof(blk_iq3_xxs) == 98, "iq3_xxs block is 98 bytes");
+_Static_assert(sizeof(blk_iq3_s) == 110, "iq3_s block is 110 bytes");
+_Static_assert(sizeof(blk_iq2_s) == 82, "iq2_s block is 82 bytes");
+
+/* ggml's non-linear 4-bit values of IQ4_NL / IQ4_XS (kvalues_iq4nl). */
+static const int8_t kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* The lattice codebooks of IQ3_XXS (256 x 4 bytes), IQ3_S (512 x 4) and IQ2_S (1024 x 8) are ggml's tables
+ * (iq3xxs_grid, iq3s_grid, iq2s_grid); they are not in this container, so the caller registers them here (the tests
+ * register seeded tables of the right size and value sets, and the HIP library gets the same ones). */
+static uint32_t g_iq3xxs_grid[256], g_iq3s_grid[512];
+static uint64_t g_iq2s_grid[1024];
+static int g_iq_grids_set;
+
+void or_set_iq_grids(const uint32_t *iq3xxs, const uint32_t *iq3s, const uint64_t *iq2s) {
+    memcpy(g_iq3xxs_grid, iq3xxs, sizeof g_iq3xxs_grid);
+    memcpy(g_iq3s_grid, iq3s, sizeof g_iq3s_grid);
+    memcpy(g_iq2s_grid, iq2s, sizeof g_iq2s_grid);
+    g_iq_grids_set = 1;
+}
+
+/* ksigns_iq2xs[v]: the 7 stored sign bits v plus an eighth that makes the count of negative signs even. */
+static int ksign_bits(uint32_t v7) { return (int) (v7 | ((uint32_t) (__builtin_popcount(v7) & 1) << 7)); }
+
 /* ---- half precision ---- */
 uint16_t or_f32_to_f16(float f) {
     uint32_t x;
@@ -108,6 +138,10 @@ size_t or_block_bytes(int type) {
         case OR_Q4_K: return sizeof(blk_q4_K);
         case OR_Q5_K: return sizeof(blk_q5_K);
         case OR_Q6_K: return sizeof(blk_q6_K);
+        case OR_IQ4_XS: return sizeof(blk_iq4_xs);
+        case OR_IQ3_XXS: return sizeof(blk_iq3_xxs);
+        case OR_IQ3_S: return sizeof(blk_iq3_s);
+        case OR_IQ2_S: return sizeof(blk_iq2_s);
         default: return 0;
     }
 }
@@ -116,8 +150,13 @@ int or_block_elems(int type) {
     switch (type) {
         case OR_Q8_0: case OR_Q8_1: return 32;
         case OR_Q3_K: case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: return QK_K;
+        case OR_IQ4_XS: case OR_IQ3_XXS: case OR_IQ3_S: case OR_IQ2_S: return QK_K;
         default: return 0;
     }
+}
+
+int or_is_iq(int type) {
+    return type == OR_IQ4_XS || type == OR_IQ3_XXS || type == OR_IQ3_S || type == OR_IQ2_S;
 }
 
 size_t or_row_bytes(int type, int64_t ncols) {
@@ -583,8 +622,137 @@ static void deq_q8_0(const blk_q8_0 *b, double *y) {
     for (int i = 0; i < 32; ++i) y[i] = d * b->qs[i];
 }
 
+/* IQ dequantisation (ggml-quants.c dequantize_row_iq4_xs / iq3_xxs / iq3_s / iq2_s): per 32-value sub-block a
+ * scale, then codebook values with signs. Sub-block scale formulas are the dequantiser's; the integer rounding of
+ * the GPU dot products is restated in or_iq_dot below. */
+static void deq_iq4_xs(const blk_iq4_xs *b, double *y) {
+    const double d = or_f16_to_f32(b->d);
+    for (int ib = 0; ib < 8; ++ib) {
+        const int ls = ((b->scales_l[ib / 2] >> (4 * (ib % 2))) & 0xf) | (((b->scales_h >> (2 * ib)) & 3) << 4);
+        const double dl = d * (ls - 32);
+        for (int j = 0; j < 16; ++j) {
+            y[32 * ib + j] = dl * kvalues_iq4nl[b->qs[16 * ib + j] & 0xf];
+            y[32 * ib + 16 + j] = dl * kvalues_iq4nl[b->qs[16 * ib + j] >> 4];
+        }
+    }
+}
+static void deq_iq3_xxs(const blk_iq3_xxs *b, double *y) {
+    const double d = or_f16_to_f32(b->d);
+    for (int ib = 0; ib < 8; ++ib) {
+        uint32_t aux;
+        memcpy(&aux, b->qs + 64 + 4 * ib, 4);
+        const double db = d * (0.5 + (aux >> 28)) * 0.5;
+        for (int l = 0; l < 4; ++l) {
+            const int s = ksign_bits((aux >> (7 * l)) & 127);
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t g = g_iq3xxs_grid[b->qs[8 * ib + 2 * l + h]];
+                for (int j = 0; j < 4; ++j)
+                    y[32 * ib + 8 * l + 4 * h + j] = db * (double) ((g >> (8 * j)) & 0xff) * ((s >> (4 * h + j)) & 1 ? -1 : 1);
+            }
+        }
+    }
+}
+static void deq_iq3_s(const blk_iq3_s *b, double *y) {
+    const double d = or_f16_to_f32(b->d);
+    for (int ib = 0; ib < 8; ++ib) {
+        const double db = d * (1 + 2 * ((b->scales[ib / 2] >> (4 * (ib % 2))) & 0xf));
+        for (int l = 0; l < 8; ++l) {
+            const uint32_t g = g_iq3s_grid[b->qs[8 * ib + l] | (((b->qh[ib] >> l) & 1) << 8)];
+            const int s = b->signs[4 * ib + l / 2] >> (4 * (l % 2));
+            for (int j = 0; j < 4; ++j)
+                y[32 * ib + 4 * l + j] = db * (double) ((g >> (8 * j)) & 0xff) * ((s >> j) & 1 ? -1 : 1);
+        }
+    }
+}
+static void deq_iq2_s(const blk_iq2_s *b, double *y) {
+    const double d = or_f16_to_f32(b->d);
+    for (int ib = 0; ib < 8; ++ib) {
+        for (int l = 0; l < 4; ++l) {
+            const double dl = d * (0.5 + ((b->scales[ib] >> (4 * (l / 2))) & 0xf)) * 0.25;
+            const uint64_t g = g_iq2s_grid[b->qs[4 * ib + l] | (((b->qh[ib] >> (2 * l)) & 3) << 8)];
+            const int s = b->qs[32 + 4 * ib + l];
+            for (int j = 0; j < 8; ++j)
+                y[32 * ib + 8 * l + j] = dl * (double) ((g >> (8 * j)) & 0xff) * ((s >> j) & 1 ? -1 : 1);
+        }
+    }
+}
+
+/* One 32-value sub-block dot of an IQ block with a Q8_1 block, in the integer arithmetic of the reference's GPU
+ * products (src/ggml/ggml_mmvq.cu:101-157 for IQ3_XXS / IQ3_S; ggml vecdotq.cuh vec_dot_iq4_xs_q8_1 /
+ * vec_dot_iq2_s_q8_1 for the others): an exact integer sum, the sub-block scale applied in integers (C division
+ * truncating toward zero), then d_w * d8 in fp32 times the integer. */
+static double iq_sub_dot(int type, const void *blk, int ib, const int8_t *q8, float d8) {
+    long sumi = 0;
+    float dw = 0.0f;
+    switch (type) {
+        case OR_IQ4_XS: {
+            const blk_iq4_xs *b = (const blk_iq4_xs *) blk;
+            for (int j = 0; j < 16; ++j)
+                sumi += kvalues_iq4nl[b->qs[16 * ib + j] & 0xf] * q8[j] + kvalues_iq4nl[b->qs[16 * ib + j] >> 4] * q8[16 + j];
+            const int ls = ((b->scales_l[ib / 2] >> (4 * (ib % 2))) & 0xf) | (((b->scales_h >> (2 * ib)) & 3) << 4);
+            sumi *= ls - 32;
+            dw = or_f16_to_f32(b->d);
+            break;
+        }
+        case OR_IQ3_XXS: {
+            const blk_iq3_xxs *b = (const blk_iq3_xxs *) blk;
+            uint32_t aux;
+            memcpy(&aux, b->qs + 64 + 4 * ib, 4);
+            for (int l = 0; l < 4; ++l) {
+                const int s = ksign_bits((aux >> (7 * l)) & 127);
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t g = g_iq3xxs_grid[b->qs[8 * ib + 2 * l + h]];
+                    for (int j = 0; j < 4; ++j) {
+                        const int v = (int) ((g >> (8 * j)) & 0xff);
+                        sumi += ((s >> (4 * h + j)) & 1 ? -v : v) * q8[8 * l + 4 * h + j];
+                    }
+                }
+            }
+            const long ls = aux >> 28;
+            sumi = (ls * sumi + sumi / 2) / 2;
+            dw = or_f16_to_f32(b->d);
+            break;
+        }
+        case OR_IQ3_S: {
+            const blk_iq3_s *b = (const blk_iq3_s *) blk;
+            for (int l = 0; l < 8; ++l) {
+                const uint32_t g = g_iq3s_grid[b->qs[8 * ib + l] | (((b->qh[ib] >> l) & 1) << 8)];
+                const int s = b->signs[4 * ib + l / 2] >> (4 * (l % 2));
+                for (int j = 0; j < 4; ++j) {
+                    const int v = (int) ((g >> (8 * j)) & 0xff);
+                    sumi += ((s >> j) & 1 ? -v : v) * q8[4 * l + j];
+                }
+            }
+            sumi *= 1 + 2 * ((b->scales[ib / 2] >> (4 * (ib % 2))) & 0xf);
+            dw = or_f16_to_f32(b->d);
+            break;
+        }
+        case OR_IQ2_S: {
+            const blk_iq2_s *b = (const blk_iq2_s *) blk;
+            long s2[2] = {0, 0};
+            for (int l = 0; l < 4; ++l) {
+                const uint64_t g = g_iq2s_grid[b->qs[4 * ib + l] | (((b->qh[ib] >> (2 * l)) & 3) << 8)];
+                const int s = b->qs[32 + 4 * ib + l];
+                for (int j = 0; j < 8; ++j) {
+                    const int v = (int) ((g >> (8 * j)) & 0xff);
+                    s2[l / 2] += ((s >> j) & 1 ? -v : v) * q8[8 * l + j];
+                }
+            }
+            const long ls0 = b->scales[ib] & 0xf, ls1 = b->scales[ib] >> 4;
+            sumi = (s2[0] * ls0 + s2[1] * ls1 + (s2[0] + s2[1]) / 2) / 4;
+            dw = or_f16_to_f32(b->d);
+            break;
+        }
+    }
+    return (double) (dw * d8) * (double) sumi;
+}
+
 static void deq_block(int type, const void *blk, double *y) {
     switch (type) {
+        case OR_IQ4_XS: deq_iq4_xs((const blk_iq4_xs *) blk, y); break;
+        case OR_IQ3_XXS: deq_iq3_xxs((const blk_iq3_xxs *) blk, y); break;
+        case OR_IQ3_S: deq_iq3_s((const blk_iq3_s *) blk, y); break;
+        case OR_IQ2_S: deq_iq2_s((const blk_iq2_s *) blk, y); break;
         case OR_Q8_0: deq_q8_0((const blk_q8_0 *) blk, y); break;
         case OR_Q3_K: deq_q3_K((const blk_q3_K *) blk, y); break;
         case OR_Q4_K: deq_q4_K((const blk_q4_K *) blk, y); break;
@@ -715,6 +883,22 @@ int or_mmvq_experts(int type, const void *const *table, int64_t ncols, int64_t n
     const int be = or_block_elems(type);
     if (!be || type == OR_Q8_1 || ncols % be || n_xq < 1 || x_div < 1) return -1;
     const size_t rb = or_row_bytes(type, ncols);
+    if (or_is_iq(type)) {  /* the reference's integer sub-block products, float64 across sub-blocks */
+        for (int64_t c = 0; c < n_ids; ++c) {
+            const blk_q8_1 *xb = (const blk_q8_1 *) ((const char *) xq + (size_t) ((c / x_div) % n_xq) *
+                                                                             or_q8_1_row_bytes(ncols));
+            const char *base = (const char *) table[ids[c]];
+            for (int64_t r = 0; r < nrows; ++r) {
+                double s = 0;
+                for (int64_t b = 0; b < ncols / QK_K; ++b)
+                    for (int ib = 0; ib < 8; ++ib)
+                        s += iq_sub_dot(type, base + (size_t) r * rb + (size_t) b * or_block_bytes(type), ib,
+                                        xb[b * 8 + ib].qs, or_f16_to_f32(xb[b * 8 + ib].d));
+                dst[c * nrows + r] = s;
+            }
+        }
+        return 0;
+    }
     double *xd = (double *) malloc(sizeof(double) * (size_t) ncols);
     double *wr = (double *) malloc(sizeof(double) * (size_t) ncols);
     if (!xd || !wr) { free(xd); free(wr); return -1; }

@@ -31,7 +31,12 @@ extern "C" {
 #endif
 
 /* ggml type ids (public ggml.h numbering). */
-enum { OR_Q8_0 = 8, OR_Q8_1 = 9, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14 };
+enum { OR_Q8_0 = 8, OR_Q8_1 = 9, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14,
+       OR_IQ3_XXS = 18, OR_IQ3_S = 21, OR_IQ2_S = 22, OR_IQ4_XS = 23 };
+int or_is_iq(int type);
+/* The IQ3_XXS / IQ3_S / IQ2_S codebooks (ggml's iq3xxs_grid[256], iq3s_grid[512], iq2s_grid[1024]; not in this
+ * container): registered by the caller before any IQ call. */
+void or_set_iq_grids(const uint32_t *iq3xxs, const uint32_t *iq3s, const uint64_t *iq2s);
 
 uint16_t or_f32_to_f16(float f);   /* IEEE binary16, round to nearest even */
 float or_f16_to_f32(uint16_t h);

@@ -19,9 +19,13 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libfns_oracle.so"
 
 Q8_0, Q8_1, Q3_K, Q4_K, Q5_K, Q6_K = 8, 9, 11, 12, 13, 14
-TYPE_NAMES = {Q8_0: "Q8_0", Q8_1: "Q8_1", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
-BLOCK_BYTES = {Q8_0: 34, Q8_1: 36, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
-BLOCK_ELEMS = {Q8_0: 32, Q8_1: 32, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS = 18, 21, 22, 23
+TYPE_NAMES = {Q8_0: "Q8_0", Q8_1: "Q8_1", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
+              IQ3_XXS: "IQ3_XXS", IQ3_S: "IQ3_S", IQ2_S: "IQ2_S", IQ4_XS: "IQ4_XS"}
+BLOCK_BYTES = {Q8_0: 34, Q8_1: 36, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210,
+               IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ4_XS: 136}
+BLOCK_ELEMS = {Q8_0: 32, Q8_1: 32, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256,
+               IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256, IQ4_XS: 256}
 
 
 def build() -> None:
@@ -57,6 +61,8 @@ def lib() -> ctypes.CDLL:
             "or_moe_combine": (None, [P, P, P, P, P, P, I64, I, I64]),
             "or_compact_ids": (I, [P, I64, I, I, I, P, P, P]),
             "or_cpu_moe_layer": (I, [I, I, P, P, SZ, SZ, SZ, P, P, I64, I64, I, I, I]),
+            "or_set_iq_grids": (None, [P, P, P]),
+            "or_is_iq": (I, [I]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -64,6 +70,14 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def set_iq_grids(iq3xxs: np.ndarray, iq3s: np.ndarray, iq2s: np.ndarray) -> None:
+    """Registers the IQ3_XXS / IQ3_S / IQ2_S codebooks (uint32 [256], uint32 [512], uint64 [1024])."""
+    a, b, c = (np.ascontiguousarray(iq3xxs, np.uint32), np.ascontiguousarray(iq3s, np.uint32),
+               np.ascontiguousarray(iq2s, np.uint64))
+    assert a.shape == (256,) and b.shape == (512,) and c.shape == (1024,)
+    lib().or_set_iq_grids(_p(a), _p(b), _p(c))
 
 
 def _p(a: np.ndarray | None):

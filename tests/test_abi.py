@@ -30,7 +30,9 @@ def test_q8_1_row_bytes_padding():
 
 def test_supported_types():
     L = _lib.lib()
-    assert [t for t in range(40) if L.fns_hip_mmvq_supports(t)] == [8, 11, 12, 13, 14]
+    got = {t for t in range(40) if L.fns_hip_mmvq_supports(t)}
+    # Q8_0, the K-quants and IQ4_XS always; IQ3_XXS / IQ3_S / IQ2_S once their codebooks are registered
+    assert {8, 11, 12, 13, 14, 23} <= got <= {8, 11, 12, 13, 14, 18, 21, 22, 23}
 
 
 def _buf():

@@ -374,3 +374,96 @@ def test_image_to_q8_1_inverts_split_image():
     a = xq[:, : 24 * 36].reshape(4, 24, 36)
     b = back[:, : 24 * 36].reshape(4, 24, 36)
     assert np.array_equal(a[:, :, 0:2], b[:, :, 0:2]) and np.array_equal(a[:, :, 4:], b[:, :, 4:])
+
+
+# ---- IQ formats (restated from ggml-common.h / ggml-quants.c at the pinned commit; codebooks registered) ----------
+
+def _f16(x: float) -> bytes:
+    return np.array([x], np.float16).tobytes()
+
+
+def test_iq4_xs_layout_closed_form():
+    """d = 1, every sub-block scale 33 (dl = 1): the values are the IQ4_NL table read through the nibble order (low
+    nibbles = values 0..15 of a sub-block, high = 16..31) and the 6-bit scale split (scales_l nibbles, scales_h
+    2-bit fields)."""
+    kv = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    qs = bytes(((j & 15) | ((15 - j) << 4)) for _ in range(8) for j in range(16))
+    blk = _f16(1.0) + (0xAAAA).to_bytes(2, "little") + bytes([0x11] * 4) + qs
+    y = orc.dequantize(orc.IQ4_XS, np.frombuffer(blk, np.uint8)[None], 256)[0]
+    for ib in range(8):
+        assert list(y[32 * ib:32 * ib + 16]) == kv
+        assert list(y[32 * ib + 16:32 * ib + 32]) == kv[::-1]
+    # scale field of sub-block 5 = 40 (low nibble 8, high bits 2): dl = 8 for that sub-block only
+    sl = bytearray([0x11] * 4)
+    sl[2] = 0x81
+    y2 = orc.dequantize(orc.IQ4_XS, np.frombuffer(_f16(1.0) + (0xAAAA).to_bytes(2, "little") + bytes(sl) + qs,
+                                                  np.uint8)[None], 256)[0]
+    assert np.array_equal(y2[160:192], 8 * y[160:192]) and np.array_equal(y2[:160], y[:160])
+
+
+def test_iq_codebook_formats_closed_form():
+    """One block of each codebook format with hand-chosen indices, signs and scales: values = scale * codebook byte *
+    sign, with the sign rules of each format (IQ3_XXS: 7 stored bits + even parity)."""
+    from tests.iq_data import register_grids
+    g3x, g3s, g2s = register_grids(5)
+    byte = lambda g, i, j: int((int(g[i]) >> (8 * j)) & 0xFF)  # noqa: E731
+    # IQ3_XXS: sub-block 0: indices 0..7, sign field 0b0000011 for pair 0 (bits 0,1 negative), scale 1 -> db = 0.75
+    qs = bytearray(96)
+    qs[0:8] = bytes(range(8))
+    aux = 0b0000011 | (1 << 28)
+    qs[64:68] = aux.to_bytes(4, "little")
+    y = orc.dequantize(orc.IQ3_XXS, np.frombuffer(_f16(1.0) + bytes(qs), np.uint8)[None], 256)[0]
+    exp = [0.75 * byte(g3x, l // 4, l % 4) * (-1 if l < 2 else 1) for l in range(32)]
+    assert np.allclose(y[:32], exp, rtol=0, atol=0)
+    # parity: a single stored negative sign turns on the eighth sign (bit 7 -> value 7 of the group)
+    qs[64:68] = (0b0000001 | (1 << 28)).to_bytes(4, "little")
+    y = orc.dequantize(orc.IQ3_XXS, np.frombuffer(_f16(1.0) + bytes(qs), np.uint8)[None], 256)[0]
+    assert y[0] < 0 and y[7] < 0 and all(v > 0 for v in y[1:7])
+    # IQ3_S: sub-block 1, index 3 with its 9th bit set (entry 256 + 3), sign nibble 0b0101, scale 2 -> db = 5
+    qs = bytearray(64)
+    qs[8 + 3] = 3
+    qh = bytearray(8)
+    qh[1] = 1 << 3
+    signs = bytearray(32)
+    signs[4 + 1] = 0b0101 << 4   # byte l/2 = 1, nibble l%2 = 1
+    scales = bytearray(4)
+    scales[0] = 2 << 4           # sub-block 1: high nibble of byte 0
+    blk = _f16(1.0) + bytes(qs) + bytes(qh) + bytes(signs) + bytes(scales)
+    y = orc.dequantize(orc.IQ3_S, np.frombuffer(blk, np.uint8)[None], 256)[0]
+    got = y[32 + 12:32 + 16]
+    want = [5 * byte(g3s, 259, j) * (-1 if (0b0101 >> j) & 1 else 1) for j in range(4)]
+    assert np.array_equal(got, want)
+    # IQ2_S: sub-block 2, group 3: index 7 + high bits 2 (entry 519), sign byte 0x81, scales low 1 / high 3
+    qs = bytearray(64)
+    qs[4 * 2 + 3] = 7
+    qs[32 + 4 * 2 + 3] = 0x81
+    qh = bytearray(8)
+    qh[2] = 2 << 6
+    sc = bytearray(8)
+    sc[2] = 1 | (3 << 4)
+    y = orc.dequantize(orc.IQ2_S, np.frombuffer(_f16(1.0) + bytes(qs) + bytes(qh) + bytes(sc), np.uint8)[None], 256)[0]
+    dl = (0.5 + 3) * 0.25  # group 3 uses the high nibble
+    want = [dl * byte(g2s, 519, j) * (-1 if j in (0, 7) else 1) for j in range(8)]
+    assert np.array_equal(y[64 + 24:64 + 32], want)
+
+
+@pytest.mark.parametrize("qtype", [23, 18, 21, 22])
+def test_iq_integer_products_match_dequantised_dot(qtype):
+    """The oracle's GEMV for IQ types restates the reference's integer sub-block products (scale applied in integers,
+    C division truncating); it must equal the independent float64 dequant . dequant dot up to that truncation:
+    exact for IQ4_XS and IQ3_S, at most one unit of d_w * d8 per sub-block for IQ3_XXS and IQ2_S."""
+    from tests.iq_data import random_blocks, register_grids
+    register_grids(5)
+    ncols, nrows = 1024, 16
+    w = random_blocks(qtype, nrows, ncols, seed=qtype)
+    x = np.random.default_rng(qtype).standard_normal((1, ncols)).astype(np.float32)
+    xq = orc.quantize_q8_1(x)
+    got = orc.mmvq_experts(qtype, [w], ncols, nrows, xq, 1, 1, np.zeros(1, np.int32))[0]
+    ref = orc.dequantize(qtype, w, ncols) @ orc.dequantize_q8_1(xq, ncols)[0]
+    d_w = w.reshape(nrows, -1, orc.BLOCK_BYTES[qtype])[:, :, :2].copy().view(np.float16).astype(np.float64)[..., 0]
+    d8 = xq[0].reshape(-1, 36)[:, :2].copy().view(np.float16).astype(np.float64)[:ncols // 32, 0]
+    bound = np.abs(d_w).repeat(8, axis=1) @ np.abs(d8)  # one unit per sub-block
+    if qtype in (orc.IQ4_XS, orc.IQ3_S):
+        assert np.allclose(got, ref, rtol=1e-12, atol=1e-15)
+    else:
+        assert np.all(np.abs(got - ref) <= bound * (1.0 + 1e-9)) and not np.array_equal(got, ref)
