@@ -62,6 +62,7 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_moe_prefill_workspace": [_P, _I64, _P, _P],
     "fns_hip_moe_prefill_section": [_P, _I64, _I, _P, _P],
     "fns_hip_moe_prefill": [_P, _P, _P, _P, _I64, _P, _SZ, _P],
+    "fns_hip_moe_prefill_status": [_P, _I64, _P, _I, _P, _P],
     "fns_hip_fill_normal": [_P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F, _F, _P],
     "fns_hip_quantize_weights": [_I, _P, _P, _I64, _I64, _P],
     "fns_hip_selftest_lanes": [_P, _P],

@@ -202,6 +202,11 @@ int fns_hip_moe_prefill_section(const FnsMoeLayer *layer, int64_t n_tok, int sec
     return impl::moe_prefill_section(layer, n_tok, section, offset, bytes);
 }
 
+int fns_hip_moe_prefill_status(const FnsMoeLayer *layer, int64_t n_tok, void *workspace, int clear, uint32_t *status,
+                               void *stream) {
+    return impl::moe_prefill_status(layer, n_tok, workspace, clear, status, S(stream));
+}
+
 int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int64_t n_tok,
                         void *workspace, size_t workspace_bytes, void *stream) {
     return impl::moe_prefill(layer, x, x_resid, out, n_tok, workspace, workspace_bytes, S(stream));

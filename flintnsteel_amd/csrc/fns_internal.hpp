@@ -59,9 +59,11 @@ size_t mmq_image_bytes(int64_t ncols);
 size_t mmq_q8_1_bytes(int64_t ncols, int64_t nrows);
 size_t mmq_bounds_bytes(int64_t n_expert);
 int mmq_quant_image(const float *x, int64_t ncols, int64_t rows, void *xpack, hipStream_t st);
-int mmq_quant_image_scaled(const float *x, const float *escale, int64_t ncols, int64_t rows, void *xpack, hipStream_t st);
+int mmq_quant_image_scaled(const float *x, const float *escale, int64_t ncols, int64_t rows, void *xpack, int64_t stride,
+                           hipStream_t st);
 int mmq_compact(const int32_t *ids, int64_t n_tok, int64_t k, int64_t n_expert, int64_t x_rows_per_tok,
-                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, int32_t *gprefix, hipStream_t st);
+                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, int32_t *gprefix, hipStream_t st,
+                int32_t *gdone = nullptr, int n_gdone = 0);
 int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t off_b, bool glu, int64_t ncols,
                      int64_t nrows, int64_t n_expert, const void *xpack, int64_t n_pairs, const int32_t *ids_src1,
                      const int32_t *ids_dst, const int32_t *bounds, const int32_t *gprefix, float *dst, void *out_pack,
@@ -72,9 +74,11 @@ int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, i
                 const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
                 int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, void *xq, float *dst, hipStream_t st);
 int moe_set_test_hooks(int spin_limit, int withhold);
+void moe_test_hooks(int *spin_limit, int *withhold);  // the values set by moe_set_test_hooks
 int moe_layer_status(const FnsMoeLayer *L, int n_tok, void *ws, int clear, uint32_t *status, hipStream_t st);
 int moe_prefill_workspace(const FnsMoeLayer *L, int64_t n_tok, size_t *offsets, size_t *total);
 int moe_prefill_section(const FnsMoeLayer *L, int64_t n_tok, int section, size_t *offset, size_t *bytes);
+int moe_prefill_status(const FnsMoeLayer *L, int64_t n_tok, void *ws, int clear, uint32_t *status, hipStream_t st);
 int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int64_t n_tok, void *ws,
                 size_t ws_bytes, hipStream_t st);
 

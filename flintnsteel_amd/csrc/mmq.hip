@@ -63,12 +63,13 @@ inline size_t gprefix_bytes(int64_t n_expert) { return (size_t) 2 * (n_expert + 
 __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *__restrict__ ids, int n, int k, int ne,
                                                                  int x_rows_per_tok, int32_t *__restrict__ ids_src1,
                                                                  int32_t *__restrict__ ids_dst, int32_t *bounds,
-                                                                 int32_t *gprefix) {
+                                                                 int32_t *gprefix, int32_t *gdone, int n_gdone) {
     constexpr int NW = kCompactThreads / kWave;
     __shared__ int cnt[256];
     __shared__ int wpos[NW][256];  // per-wave counts, then each wave's next sorted position per expert
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     for (int i = tid; i < NW * 256; i += kCompactThreads) (&wpos[0][0])[i] = 0;
+    for (int i = tid; i < n_gdone; i += kCompactThreads) gdone[i] = 0;  // the next fused GEMM launch's arrivals
     __syncthreads();
     const int chunk = (n + NW * kWave - 1) / (NW * kWave) * kWave;  // pairs per wave, a multiple of 64
     const int p0 = wave * chunk, p1 = min(n, p0 + chunk);
@@ -195,8 +196,13 @@ __device__ __forceinline__ int perm8(int k) { return (k & ~3) | ((k & 1) << 1) |
 // the split image row `row` at column col (a multiple of 8): d = amax / 127, q = roundf(v / d) - with an IEEE
 // division per value (EXACT: the reference's arithmetic, bit for bit) or v * (1 / d). The max and the integer sum are
 // exact in any order. Returns nothing; lane q = 0 of the block also stores its min-term sums.
+struct Q8Split {
+    _Float16 hi[8], lo[8];  // in the stored order
+    _Float16 shi, slo;      // the block's min-term sum (lane q = 0 of the block stores it)
+};
 template <bool EXACT>
-__device__ __forceinline__ void q8_split8(const float (&v)[8], uint8_t *row, int ncols, int col, bool store) {
+__device__ __forceinline__ Q8Split q8_split8_vals(const float (&v)[8]) {
+    Q8Split r;
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
@@ -205,28 +211,40 @@ __device__ __forceinline__ void q8_split8(const float (&v)[8], uint8_t *row, int
     const float dh = half_to_float(float_to_half(d));
     const float id = amax == 0.0f ? 0.0f : 1.0f / d;
     int qsum = 0;
-    _Float16 hi[8], lo[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int qk = amax == 0.0f ? 0 : (int) (int8_t) roundf(EXACT ? v[k] / d : v[k] * id);
         qsum += qk;
         const float x = (float) qk * dh;  // exact
         const _Float16 h = (_Float16) x;
-        hi[perm8(k)] = h;
-        lo[perm8(k)] = (_Float16) (x - (float) h);
+        r.hi[perm8(k)] = h;
+        r.lo[perm8(k)] = (_Float16) (x - (float) h);
     }
     qsum = lanes_sum_i<4>(qsum);
+    const float sv = dh * (float) qsum;  // exact in fp32
+    r.shi = (_Float16) sv;
+    r.slo = (_Float16) (sv - (float) r.shi);
+    return r;
+}
+// byte offsets within an image row of the 8 columns at col (hi; lo at + 256) and of the block's min-term sums (hi;
+// lo at + 16)
+__device__ __forceinline__ uint32_t img_col_off(int col) {
+    return (uint32_t) ((col >> 8) * kSbMain + ((col >> 7) & 1) * 512 + ((col & 127) >> 3) * 16);
+}
+__device__ __forceinline__ uint32_t img_sum_off(int ncols, int col) {
+    return (uint32_t) ((ncols >> 8) * kSbMain + (col >> 8) * kSbMin + 2 * perm8((col >> 5) & 7));
+}
+template <bool EXACT>
+__device__ __forceinline__ void q8_split8(const float (&v)[8], uint8_t *row, int ncols, int col, bool store) {
+    const Q8Split r = q8_split8_vals<EXACT>(v);
     if (!store) return;
-    uint8_t *o = row + (size_t) (col >> 8) * kSbMain + ((col >> 7) & 1) * 512 + ((col & 127) >> 3) * 16;
-    *(uint4 *) o = __builtin_bit_cast(uint4, hi);
-    *(uint4 *) (o + 256) = __builtin_bit_cast(uint4, lo);
+    uint8_t *o = row + img_col_off(col);
+    *(uint4 *) o = __builtin_bit_cast(uint4, r.hi);
+    *(uint4 *) (o + 256) = __builtin_bit_cast(uint4, r.lo);
     if ((col & 31) == 0) {
-        const float sv = dh * (float) qsum;  // exact in fp32
-        const _Float16 shi = (_Float16) sv, slo = (_Float16) (sv - (float) shi);
-        _Float16 *m = (_Float16 *) (row + (size_t) (ncols >> 8) * kSbMain + (size_t) (col >> 8) * kSbMin);
-        const int si = perm8((col >> 5) & 7);
-        m[si] = shi;
-        m[8 + si] = slo;
+        _Float16 *m = (_Float16 *) (row + img_sum_off(ncols, col));
+        m[0] = r.shi;
+        m[8] = r.slo;
     }
 }
 
@@ -297,6 +315,10 @@ struct MmqArgs {
     uint8_t *out_pack;         // GLU: act split image rows (by output row)
     int64_t out_img;
     float *act_out;            // GLU: optional f32 act [out row][nrows]
+    int *gdone;                // fused launch: per-group arrival counts (zeroed by the compaction kernel)
+    int gwait;                 // fused launch: arrivals a down item waits for (its group's gate/up items)
+    int spin_limit;            // fused launch: polls before a down item gives up (its outputs are then NaN)
+    uint32_t *status;          // fused launch: sticky status word, kStatusTimeout once a wait gave up
 };
 
 // Weight fragments of one 256-value block for one lane: the header (scales, d) and the codes of column groups
@@ -495,9 +517,51 @@ __device__ __forceinline__ v16f mfma32(v8h a, v8h b, v16f c) {
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 typedef __attribute__((address_space(3))) void *LdsPtr;
-// 16 bytes per lane from r at (vo + so) into LDS at dst + 16 lane (dst wave-uniform)
+// 16 bytes per lane from r at (vo + so) into LDS at dst + 16 lane (dst wave-uniform); CPOL: cache-policy bits
+template <int CPOL = 0>
 __device__ __forceinline__ void dma16(Rsrc r, void *dst, uint32_t vo, uint32_t so) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr) dst, 16, vo, so, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr) dst, 16, vo, so, 0, CPOL);
+}
+
+// ---- the fused gate/up + down launch: per-group arrivals --------------------------------------------------------
+// A gate/up item stores its act image rows device-coherent (sc1: written through to memory, so no other XCD's L2 can
+// serve an older copy), waits for the stores to complete and then counts its arrival on the group's counter; a down
+// item of the group polls the counter (device-scope loads) until every gate/up item of the group has arrived and then
+// reads the act rows with device-scope (sc1) loads. No fence is involved: the order comes from the completed stores
+// before the arrival, as in the decode layer's exchange.
+constexpr int kCpolDevice = 16;           // sc1
+constexpr uint32_t kStatusTimeout = 1u;   // FNS_STATUS_EXCHANGE_TIMEOUT
+__device__ __forceinline__ void q8_split8_dev(const float (&v)[8], Rsrc r, uint32_t row_off, int ncols, int col,
+                                              bool store) {
+    const Q8Split q = q8_split8_vals<true>(v);
+    if (!store) return;
+    const uint32_t o = row_off + img_col_off(col);
+    const uint4 hi = __builtin_bit_cast(uint4, q.hi), lo = __builtin_bit_cast(uint4, q.lo);
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(v4u{hi.x, hi.y, hi.z, hi.w}, r, o, 0, kCpolDevice);
+    __builtin_amdgcn_raw_buffer_store_b128(v4u{lo.x, lo.y, lo.z, lo.w}, r, o + 256, 0, kCpolDevice);
+    if ((col & 31) == 0) {
+        const uint32_t m = row_off + img_sum_off(ncols, col);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, q.shi), r, m, 0, kCpolDevice);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, q.slo), r, m + 16, 0, kCpolDevice);
+    }
+}
+// thread 0 polls the group's arrival count (bounded); true for every thread when the wait gave up
+__device__ __forceinline__ bool wait_group(const MmqArgs &a, int slot, int *flag) {
+    if (threadIdx.x == 0) {
+        int spins = 0, fail = 0;
+        while (__hip_atomic_load(a.gdone + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a.gwait) {
+            if (++spins > a.spin_limit) {
+                fail = 1;
+                __hip_atomic_fetch_or(a.status, kStatusTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        *flag = fail;
+    }
+    __syncthreads();
+    return __builtin_amdgcn_readfirstlane(*flag) != 0;
 }
 
 // One workgroup = 4 waves x two 32-row weight streams x up to 32 NT routed activation rows of one expert (NT = 2: the
@@ -517,8 +581,9 @@ struct MmqLds {
 };
 
 // Group g of the launch's list (NT = 2: the 64-row groups and remainders > 32 rows; NT = 1: the expert's <= 32-row
-// remainder), weight row block wb.
-template <int T, bool GLU, int NT>
+// remainder), weight row block wb. DEV: an item of the fused launch (gate/up items count their arrival, down items
+// wait for their group's).
+template <int T, bool GLU, int NT, bool DEV>
 __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const MmqLds &L) {
     constexpr int ROWS = 32 * NT;  // activation rows of the workgroup
     constexpr int WROWS = GLU ? 128 : 256;  // weight rows of the workgroup
@@ -603,20 +668,30 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
     const uint32_t so = (uint32_t) ((size_t) sh_src[srow + lane / 2] * a.x_img + (size_t) nb * kSbMain + 16 * (lane & 1));
     // (unconditional: a fixed number of loads in flight keeps the compiler's wait counts exact; rows past cnt read
     // the last routed row again)
+    constexpr int CPOL = DEV && !GLU ? kCpolDevice : 0;  // the fused down items read this launch's act rows
     auto dma_chunk = [&](uint8_t *buf, int kb, int h) __attribute__((always_inline)) {
         const uint32_t soff = (uint32_t) (kb * kSbMain + h * 512);
 #pragma unroll
-        for (int u = 0; u < NU; ++u) dma16(rx, buf + (8 * u + 2 * wave) * kRowA, qo[u], soff);
+        for (int u = 0; u < NU; ++u) dma16<CPOL>(rx, buf + (8 * u + 2 * wave) * kRowA, qo[u], soff);
     };
     auto dma_sums = [&](int kb) __attribute__((always_inline)) {  // the waves past ROWS / 32 repeat the first ones
-        if constexpr (MIN) dma16(rx, sh_s + srow * kRowS, so, (uint32_t) (kb * kSbMin));
+        if constexpr (MIN) dma16<CPOL>(rx, sh_s + srow * kRowS, so, (uint32_t) (kb * kSbMin));
     };
 
     WFrag<T> f0, f1, n0, n1;
-    dma_chunk(sh_a0, 0, 0);
-    dma_sums(0);
-    wfrag_load<T, 0>(r0, v0, c0, 0, f0);
-    wfrag_load<T, 0>(r1, v1, c1, 0, f1);
+    bool failed = false;
+    if constexpr (DEV && !GLU) {  // the first weights in flight, then the wait for the group's act rows
+        wfrag_load<T, 0>(r0, v0, c0, 0, f0);
+        wfrag_load<T, 0>(r1, v1, c1, 0, f1);
+        failed = wait_group(a, NT == 2 ? g : a.n_main + g, &L.grp[3]);
+        dma_chunk(sh_a0, 0, 0);
+        dma_sums(0);
+    } else {
+        dma_chunk(sh_a0, 0, 0);
+        dma_sums(0);
+        wfrag_load<T, 0>(r0, v0, c0, 0, f0);
+        wfrag_load<T, 0>(r1, v1, c1, 0, f1);
+    }
     dma_wait();
     lds_barrier();
     MMQ_MARK(1);
@@ -827,8 +902,8 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
                 const int i = t * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
                 if (i < cnt) {
                     float *o = a.dst + (size_t) sh_dst[i] * a.nrows;
-                    if (row0 < a.nrows) o[row0] = acc[t][0][r];
-                    if (row0 + 128 < a.nrows) o[row0 + 128] = acc[t][1][r];
+                    if (row0 < a.nrows) o[row0] = failed ? __builtin_nanf("") : acc[t][0][r];
+                    if (row0 + 128 < a.nrows) o[row0 + 128] = failed ? __builtin_nanf("") : acc[t][1][r];
                 }
             }
     } else {
@@ -858,12 +933,22 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
             const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             // the reference's Q8_1 arithmetic (q = roundf(v / d), IEEE division): the same codes as the quantiser of
             // the f32 act rows would give
-            q8_split8<true>(v, a.out_pack + (size_t) sh_dst[i] * a.out_img, a.nrows, col, live);
+            if constexpr (DEV)
+                q8_split8_dev(v, rsrc_of(a.out_pack), (uint32_t) ((size_t) sh_dst[i] * a.out_img), a.nrows, col, live);
+            else
+                q8_split8<true>(v, a.out_pack + (size_t) sh_dst[i] * a.out_img, a.nrows, col, live);
             if (live && a.act_out) {
                 float *ao = a.act_out + (size_t) sh_dst[i] * a.nrows + col;
                 *(float4 *) ao = x0;
                 *(float4 *) (ao + 4) = x1;
             }
+        }
+        if constexpr (DEV) {  // every act store of the workgroup has completed: count the arrival
+            dma_wait();
+            __syncthreads();
+            if (tid == 0)
+                __hip_atomic_fetch_add(a.gdone + (NT == 2 ? g : a.n_main + g), 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     MMQ_MARK(12);
@@ -885,8 +970,79 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const int lid = blockIdx.x, r = lid / kXcds;
     const int g = (r / a.n_cb) * kXcds + lid % kXcds, wb = r % a.n_cb;
     if (g >= a.n_groups) return;
-    if (g < a.n_main) mmq_group<T, GLU, 2>(a, g, wb, L);
-    else mmq_group<T, GLU, 1>(a, g - a.n_main, wb, L);
+    if (g < a.n_main) mmq_group<T, GLU, 2, false>(a, g, wb, L);
+    else mmq_group<T, GLU, 1, false>(a, g - a.n_main, wb, L);
+}
+
+// Gate/up (with SwiGLU and the Q8_1 of act) and down of the expert path in one launch. The gate/up items come first,
+// in the order and XCD mapping of k_mmq (group g's weight row blocks on XCD g % 8), then the down items with the same
+// mapping; a down item first waits for its group's gate/up items (arrival counts, see above). Workgroups are
+// dispatched in index order on each XCD and every gate/up item precedes every down item, so a waiting down item never
+// holds a slot that a gate/up item it waits for still needs: the wait always ends. The gate/up tail and the first
+// down items overlap instead of being separated by a launch. (A persistent variant that takes items from per-XCD
+// queues measured no faster.)
+struct MoeArgs {
+    const char *const *table;
+    int64_t gate_off, up_off, down_off;
+    int hidden, inter, n_expert, n_main;  // n_main: the 64-row list's upper bound
+    int n_cb_gu, n_cb_dn, gwait, spin_limit;
+    const uint8_t *ximg;                  // x split images [n_tok][x_img]
+    uint8_t *aimg;                        // act split images [n_tok * k][a_img]
+    int64_t x_img, a_img;
+    const int32_t *bounds, *gprefix, *src1, *dstr;
+    float *dexp;
+    int *gdone;
+    uint32_t *status;
+};
+template <int TGU, int TDN>
+__global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 4))) void k_mmq_moe(const MoeArgs m) {
+    constexpr bool MIN = TGU == T_Q4_K || TGU == T_Q5_K || TDN == T_Q4_K || TDN == T_Q5_K;
+    __shared__ __align__(16) uint8_t sh_a0[kMmqTok * kRowA];
+    __shared__ __align__(16) uint8_t sh_a1[kMmqTok * kRowA];
+    __shared__ __align__(16) uint8_t sh_s[MIN ? kMmqTok * kRowS : 16];
+    __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok], sh_grp[4];
+    const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp};
+    const int total = m.n_main + m.n_expert;
+    const int items_gu = m.n_cb_gu * kXcds * ((total + kXcds - 1) / kXcds);  // a multiple of kXcds
+    const bool is_gu = (int) blockIdx.x < items_gu;
+    const int cb = is_gu ? m.n_cb_gu : m.n_cb_dn;
+    const int lid = is_gu ? (int) blockIdx.x : (int) blockIdx.x - items_gu, r = lid / kXcds;
+    const int g = (r / cb) * kXcds + lid % kXcds, wb = r % cb;
+    if (g >= total) return;
+    MmqArgs a{};
+    a.table = m.table;
+    a.n_expert = m.n_expert;
+    a.bounds = m.bounds;
+    a.gprefix = m.gprefix;
+    a.n_main = m.n_main;
+    a.dst_rows = m.dstr;
+    a.gdone = m.gdone;
+    if (is_gu) {
+        a.off_a = m.gate_off;
+        a.off_b = m.up_off;
+        a.ncols = m.hidden;
+        a.nrows = m.inter;
+        a.xpack = m.ximg;
+        a.x_img = m.x_img;
+        a.src = m.src1;
+        a.out_pack = m.aimg;
+        a.out_img = m.a_img;
+        if (g < m.n_main) mmq_group<TGU, true, 2, true>(a, g, wb, L);
+        else mmq_group<TGU, true, 1, true>(a, g - m.n_main, wb, L);
+    } else {
+        a.off_a = m.down_off;
+        a.ncols = m.inter;
+        a.nrows = m.hidden;
+        a.xpack = m.aimg;
+        a.x_img = m.a_img;
+        a.src = m.dstr;
+        a.dst = m.dexp;
+        a.gwait = m.gwait;
+        a.spin_limit = m.spin_limit;
+        a.status = m.status;
+        if (g < m.n_main) mmq_group<TDN, false, 2, true>(a, g, wb, L);
+        else mmq_group<TDN, false, 1, true>(a, g - m.n_main, wb, L);
+    }
 }
 
 template <bool GLU> const void *mmq_kernel(int type) {
@@ -919,6 +1075,40 @@ int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st)
     return host::check_launch("mmq");
 }
 
+// The fused kernel for the type pairs whose register allocation does not spill (the Q5_K and Q6_K decoders push the
+// combined kernel past 256 registers); the other pairs take two launches.
+template <int TGU> const void *mmq_moe_kernel_dn(int tdn) {
+    switch (tdn) {
+        case T_Q3_K: return (const void *) k_mmq_moe<TGU, T_Q3_K>;
+        case T_Q4_K: return (const void *) k_mmq_moe<TGU, T_Q4_K>;
+    }
+    return nullptr;
+}
+const void *mmq_moe_kernel(int tgu, int tdn) {
+    switch (tgu) {
+        case T_Q3_K: return mmq_moe_kernel_dn<T_Q3_K>(tdn);
+        case T_Q4_K: return mmq_moe_kernel_dn<T_Q4_K>(tdn);
+    }
+    return nullptr;
+}
+
+// The fused launch (the arrival counters zero: the compaction kernel clears them).
+int launch_mmq_moe(int tgu, int tdn, MoeArgs m, hipStream_t st) {
+    const void *fn = mmq_moe_kernel(tgu, tdn);
+    if (!fn) return host::set_error(host::ERR_TYPE, "mmq: types %d / %d not supported", tgu, tdn);
+    if (m.n_main <= 0) return host::OK;
+    m.n_cb_gu = (m.inter + 127) / 128;
+    m.n_cb_dn = (m.hidden + 255) / 256;
+    m.gwait += m.n_cb_gu;
+    const int64_t total = m.n_main + m.n_expert;
+    const int64_t items = (int64_t) (m.n_cb_gu + m.n_cb_dn) * kXcds * ((total + kXcds - 1) / kXcds);
+    if (items > INT32_MAX) return host::set_error(host::ERR_SHAPE, "mmq: grid too large");
+    void *args[] = {&m};
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) items), dim3(kMmqThreads), args, 0, st);
+    if (e != hipSuccess) return host::set_error(host::ERR_LAUNCH, "mmq: %s", hipGetErrorString(e));
+    return host::check_launch("mmq (gate/up + down)");
+}
+
 int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
     if (!host::is_kquant(type)) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
     if (ncols <= 0 || ncols % 256 || nrows <= 0 || nrows % kMmqRows || ncols > 65536)
@@ -943,33 +1133,43 @@ int mmq_quant_image(const float *x, int64_t ncols, int64_t rows, void *xpack, hi
 }
 
 int mmq_quant_image_scaled(const float *x, const float *escale, int64_t ncols, int64_t rows, void *xpack,
-                           hipStream_t st) {
+                           int64_t stride, hipStream_t st) {
     if (!x || !escale || !xpack || ncols <= 0 || ncols % 256 || ncols > 65536 || rows < 0 || rows > 65535)
         return host::set_error(host::ERR_SHAPE, "mmq quantize: bad arguments");
     if (rows == 0) return host::OK;
     hipLaunchKernelGGL(k_quant_image_scaled, dim3((unsigned) ((ncols + 2047) / 2048), (unsigned) rows), dim3(256), 0, st,
-                       x, escale, (int) ncols, (uint8_t *) xpack, (int64_t) mmq_image_bytes(ncols));
+                       x, escale, (int) ncols, (uint8_t *) xpack, stride);
     return host::check_launch("mmq quantize (guarded rows)");
 }
 
 int mmq_compact(const int32_t *ids, int64_t n_tok, int64_t k, int64_t n_expert, int64_t x_rows_per_tok,
-                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, int32_t *gprefix, hipStream_t st) {
+                int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, int32_t *gprefix, hipStream_t st, int32_t *gdone,
+                int n_gdone) {
     if (!ids || !ids_src1 || !ids_dst || !bounds || !gprefix || n_tok < 0 || k < 1 || n_expert < 1 || n_expert > 256 ||
         n_tok * k > (1 << 20) || (x_rows_per_tok != 1 && x_rows_per_tok != k))
         return host::set_error(host::ERR_SHAPE, "mmq compaction: bad arguments");
     hipLaunchKernelGGL(k_mmq_compact, dim3(1), dim3(kCompactThreads), 0, st, ids, (int) (n_tok * k), (int) k,
-                       (int) n_expert, (int) x_rows_per_tok, ids_src1, ids_dst, bounds, gprefix);
+                       (int) n_expert, (int) x_rows_per_tok, ids_src1, ids_dst, bounds, gprefix, gdone, gdone ? n_gdone : 0);
     return host::check_launch("mmq compaction");
 }
 
-int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t off_b, bool glu, int64_t ncols,
-                     int64_t nrows, int64_t n_expert, const void *xpack, int64_t n_pairs, const int32_t *ids_src1,
-                     const int32_t *ids_dst, const int32_t *bounds, const int32_t *gprefix, float *dst, void *out_pack,
-                     float *act_out, hipStream_t st) {
+// Bytes per act image row in the prefill workspace: the image rounded up to whole 128-byte lines, so that no cache
+// line holds parts of two rows. The fused launch depends on it: rows of different groups are written and read by
+// different workgroups at different times, and a line read for one row must never carry another row's older bytes.
+int64_t act_stride(int64_t ncols) { return ((int64_t) mmq_image_bytes(ncols) + 127) / 128 * 128; }
+
+// the 64-row list's upper bound for n_pairs sorted rows over n_expert experts: sum_e (n_e / 64 + (n_e % 64 > 32))
+int64_t main_groups(int64_t n_expert, int64_t n_pairs) { return n_expert + (n_pairs + kMmqTok - 1) / kMmqTok; }
+
+// x_stride / out_stride: bytes per activation / act image row (0: the image's own size)
+int expert_args(int type, const char *const *table, size_t off_a, size_t off_b, bool glu, int64_t ncols,
+                int64_t nrows, int64_t n_expert, const void *xpack, const int32_t *ids_src1, const int32_t *ids_dst,
+                const int32_t *bounds, const int32_t *gprefix, float *dst, void *out_pack, float *act_out, MmqArgs &a,
+                int64_t x_stride = 0, int64_t out_stride = 0) {
     FNS_TRY(check_mmq_shape(type, ncols, nrows));
     if (!table || !xpack || !bounds || !gprefix || (!glu && !dst) || (glu && !out_pack) || n_expert < 1 || n_expert > 256)
         return host::set_error(host::ERR_SHAPE, "mmq_experts: bad arguments");
-    MmqArgs a{};
+    a = MmqArgs{};
     a.table = table;
     a.off_a = (int64_t) off_a;
     a.off_b = (int64_t) off_b;
@@ -977,17 +1177,26 @@ int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t of
     a.nrows = (int) nrows;
     a.n_expert = (int) n_expert;
     a.xpack = (const uint8_t *) xpack;
-    a.x_img = (int64_t) mmq_image_bytes(ncols);
+    a.x_img = x_stride ? x_stride : (int64_t) mmq_image_bytes(ncols);
     a.bounds = bounds;
     a.gprefix = gprefix;
     a.src = ids_src1;
     a.dst_rows = ids_dst;
     a.dst = dst;
     a.out_pack = (uint8_t *) out_pack;
-    a.out_img = (int64_t) mmq_image_bytes(nrows);
+    a.out_img = out_stride ? out_stride : (int64_t) mmq_image_bytes(nrows);
     a.act_out = act_out;
-    const int groups = (int) (n_expert + (n_pairs + kMmqTok - 1) / kMmqTok);  // >= sum_e ceil(n_e / 128)
-    return launch_mmq(type, glu, a, groups, st);
+    return host::OK;
+}
+
+int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t off_b, bool glu, int64_t ncols,
+                     int64_t nrows, int64_t n_expert, const void *xpack, int64_t n_pairs, const int32_t *ids_src1,
+                     const int32_t *ids_dst, const int32_t *bounds, const int32_t *gprefix, float *dst, void *out_pack,
+                     float *act_out, hipStream_t st) {
+    MmqArgs a;
+    FNS_TRY(expert_args(type, table, off_a, off_b, glu, ncols, nrows, n_expert, xpack, ids_src1, ids_dst, bounds,
+                        gprefix, dst, out_pack, act_out, a));
+    return launch_mmq(type, glu, a, (int) main_groups(n_expert, n_pairs), st);
 }
 
 int mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq, float *dst,
@@ -1036,11 +1245,12 @@ void prefill_sizes(const FnsMoeLayer *L, int64_t T, size_t *sz) {
     sz[1] = (size_t) P * 4;                               // ids
     sz[2] = (size_t) P * 4;                               // w
     sz[3] = (size_t) T * mmq_image_bytes(L->hidden);      // x images
-    sz[4] = (size_t) P * mmq_image_bytes(L->inter);       // act images
+    sz[4] = (size_t) P * act_stride(L->inter);            // act images
     sz[5] = (size_t) P * L->hidden * 4;                   // per-(token, slot) down outputs
     sz[6] = (size_t) P * 4;                               // ids_src1
     sz[7] = (size_t) P * 4;                               // ids_dst
-    sz[8] = bounds_bytes(L->n_expert);                    // bounds + group prefix
+    // bounds + group prefix, arrival counters, status word
+    sz[8] = bounds_bytes(L->n_expert) + 4 * (size_t) (main_groups(L->n_expert, P) + L->n_expert) + 4;
     sz[9] = L->guard ? (size_t) P * L->inter * 4 : 0;     // f32 act (F16 guard only)
     sz[10] = (size_t) P * 4;                              // escale
     const int64_t fs = L->shexp_inter > 0 ? L->shexp_inter : 0;
@@ -1106,6 +1316,27 @@ int mmq_dense_shared(const FnsMoeLayer *L, const void *ximg, int64_t n_tok, void
     return launch_mmq(dt, false, d, groups, st);
 }
 
+namespace {
+__global__ void k_zero_word(uint32_t *w) { *w = 0; }
+}  // namespace
+
+// The sticky status word of a prefill workspace (after the fused launch's arrival counters in section 8), read after
+// the stream's work so far has completed; clear: zero it afterwards (a kernel on `st`).
+int moe_prefill_status(const FnsMoeLayer *L, int64_t n_tok, void *ws, int clear, uint32_t *status, hipStream_t st) {
+    if (!ws || !status) return host::set_error(host::ERR_SHAPE, "moe_prefill_status: null argument");
+    size_t off;
+    FNS_TRY(moe_prefill_section(L, n_tok, 8, &off, nullptr));
+    const int64_t words = 3 * (L->n_expert + 1) + main_groups(L->n_expert, n_tok * L->k) + L->n_expert;
+    uint32_t *word = (uint32_t *) ((uint8_t *) ws + off) + words;
+    if (hipMemcpyAsync(status, word, 4, hipMemcpyDeviceToHost, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+        return host::set_error(host::ERR_LAUNCH, "moe_prefill_status: reading the status word failed");
+    if (clear) {
+        hipLaunchKernelGGL(k_zero_word, dim3(1), dim3(1), 0, st, word);
+        FNS_TRY(host::check_launch("moe_prefill_status: clearing"));
+    }
+    return host::OK;
+}
+
 int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int64_t n_tok, void *ws,
                 size_t ws_bytes, hipStream_t st) {
     if (!L || !x || !out || !ws || !L->router_w || !L->table) return host::set_error(host::ERR_SHAPE, "moe_prefill: null argument");
@@ -1162,18 +1393,54 @@ int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, floa
         FNS_TRY(mmq_quant_image(x, L->hidden, n_tok, sec[3], st));
     }
     FNS_TRY(route_topk(logits, ids, w, L->n_expert, L->k, (int) n_tok, L->gating, L->norm_w, st));
-    FNS_TRY(mmq_compact(ids, n_tok, L->k, L->n_expert, 1, src1, dstr, bounds, bounds + L->n_expert + 1, st));
-    FNS_TRY(mmq_gemm_experts(L->gu_type, table, L->gate_off, L->up_off, true, L->hidden, L->inter, L->n_expert, sec[3],
-                             P, src1, dstr, bounds, bounds + L->n_expert + 1, nullptr, sec[4], L->guard ? act : nullptr,
-                             st));
-    if (L->guard) {  // whole-row amax: a second pass over the f32 act rows (reference src/kernels.cu:534-552)
-        FNS_TRY(amax_guard(act, escale, L->inter, (int) P, st));
-        FNS_TRY(mmq_quant_image_scaled(act, escale, L->inter, P, sec[4], st));
-    }
+    // gate/up (SwiGLU and the Q8_1 of act fused) and down: act image rows padded to whole cache lines; one launch
+    // unless the F16 guard's whole-row amax has to sit between them (or the type pair has no fused kernel)
+    const int groups = (int) main_groups(L->n_expert, P);
+    const int64_t astride = act_stride(L->inter);
+    int32_t *gdone = bounds + 3 * (L->n_expert + 1);
+    uint32_t *status = (uint32_t *) (gdone + groups + L->n_expert);
+    const bool fused = !L->guard && mmq_moe_kernel(L->gu_type, L->down_type) && P * astride < INT32_MAX;
+    FNS_TRY(mmq_compact(ids, n_tok, L->k, L->n_expert, 1, src1, dstr, bounds, bounds + L->n_expert + 1, st,
+                        fused ? gdone : nullptr, groups + (int) L->n_expert));
     // down: one act row per (token, slot), in the same expert order as gate/up: the sorted rows are the pairs
     // themselves (activation row = output row = p), so the gate/up sort is reused with ids_dst as the source list
-    FNS_TRY(mmq_gemm_experts(L->down_type, table, L->down_off, 0, false, L->inter, L->hidden, L->n_expert, sec[4], P,
-                             dstr, dstr, bounds, bounds + L->n_expert + 1, dexp, nullptr, nullptr, st));
+    MmqArgs gu, dn;
+    FNS_TRY(expert_args(L->gu_type, table, L->gate_off, L->up_off, true, L->hidden, L->inter, L->n_expert, sec[3], src1,
+                        dstr, bounds, bounds + L->n_expert + 1, nullptr, sec[4], L->guard ? act : nullptr, gu, 0,
+                        astride));
+    FNS_TRY(expert_args(L->down_type, table, L->down_off, 0, false, L->inter, L->hidden, L->n_expert, sec[4], dstr,
+                        dstr, bounds, bounds + L->n_expert + 1, dexp, nullptr, nullptr, dn, astride));
+    if (fused) {
+        MoeArgs m{};
+        m.table = table;
+        m.gate_off = (int64_t) L->gate_off;
+        m.up_off = (int64_t) L->up_off;
+        m.down_off = (int64_t) L->down_off;
+        m.hidden = (int) L->hidden;
+        m.inter = (int) L->inter;
+        m.n_expert = (int) L->n_expert;
+        m.n_main = groups;
+        m.ximg = sec[3];
+        m.x_img = (int64_t) mmq_image_bytes(L->hidden);
+        m.aimg = sec[4];
+        m.a_img = astride;
+        m.bounds = bounds;
+        m.gprefix = bounds + L->n_expert + 1;
+        m.src1 = src1;
+        m.dstr = dstr;
+        m.dexp = dexp;
+        m.gdone = gdone;
+        m.status = status;
+        moe_test_hooks(&m.spin_limit, &m.gwait);  // withheld arrivals; + the gate/up row blocks per group
+        FNS_TRY(launch_mmq_moe(L->gu_type, L->down_type, m, st));
+    } else {
+        FNS_TRY(launch_mmq(L->gu_type, true, gu, groups, st));
+        if (L->guard) {  // whole-row amax: a second pass over the f32 act rows (reference src/kernels.cu:534-552)
+            FNS_TRY(amax_guard(act, escale, L->inter, (int) P, st));
+            FNS_TRY(mmq_quant_image_scaled(act, escale, L->inter, P, sec[4], astride, st));
+        }
+        FNS_TRY(launch_mmq(L->down_type, false, dn, groups, st));
+    }
     float *sh = nullptr;
     if (L->shexp_inter > 0) {  // shared expert (reference src/engine.cu:351-355): dense gate/up + SwiGLU, then down
         sh = (float *) sec[14];

@@ -1569,6 +1569,10 @@ int moe_set_test_hooks(int spin_limit, int withhold) {
     g_withhold = withhold;
     return host::OK;
 }
+void moe_test_hooks(int *spin_limit, int *withhold) {
+    *spin_limit = g_spin_limit;
+    *withhold = g_withhold;
+}
 
 // Validates and fills the kernel arguments of one call.
 static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int n_tok, void *ws,

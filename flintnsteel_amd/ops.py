@@ -15,6 +15,7 @@ from ._lib import call, lib
 Q8_0, Q8_1, Q3_K, Q4_K, Q5_K, Q6_K = 8, 9, 11, 12, 13, 14
 F32, BF16 = 0, 30
 GATING_SOFTMAX, GATING_SIGMOID = 0, 1
+STATUS_EXCHANGE_TIMEOUT = 1  # FNS_STATUS_EXCHANGE_TIMEOUT
 # bytes per 256 values of a row (a K-quant block; 8 Q8_0 blocks)
 BLOCK_BYTES = {Q8_0: 272, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 TYPE_NAMES = {Q8_0: "Q8_0", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
@@ -374,6 +375,13 @@ class MoePrefill:
              ws.numel(), _s())
         return out
 
+    def status(self, ws: torch.Tensor, n_tok: int, clear: bool = False) -> int:
+        """The workspace's sticky status word (FNS_STATUS_* bits; 0: every fused gate/up + down wait so far completed)."""
+        st = ctypes.c_uint32()
+        call("fns_hip_moe_prefill_status", ctypes.byref(self.layer.desc), n_tok, _p(ws), int(clear), ctypes.byref(st),
+             _s())
+        return st.value
+
     def section(self, n_tok: int, index: int) -> tuple[int, int]:
         """(byte offset, bytes) of workspace section `index` (fns_hip_moe_prefill_section)."""
         off, size = ctypes.c_size_t(), ctypes.c_size_t()
@@ -396,6 +404,9 @@ class MoePrefill:
             off, n = self.section(n_tok, idx)
             if n:
                 out[name] = ws[off: off + n].view(dt).view(*shape)
+        # image rows may be padded to whole cache lines: the views hold each row's image bytes only
+        out["xpack"] = out["xpack"][:, : d.hidden // 256 * 1056]
+        out["apack"] = out["apack"][:, : d.inter // 256 * 1056]
         return out
 
 

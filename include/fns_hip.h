@@ -214,12 +214,21 @@ int fns_hip_mmq_compact(const int32_t *ids, int64_t n_tok, int64_t n_used, int64
  * 1 ids i32 [n_tok][k], 2 w f32 [n_tok][k], 3 x images, 4 act images [n_tok * k], 5 down outputs f32 [n_tok][k][hidden]. */
 int fns_hip_moe_prefill_workspace(const FnsMoeLayer *layer, int64_t n_tok, size_t *offsets, size_t *total_bytes);
 /* Byte offset and size of any workspace section of fns_hip_moe_prefill (the six above, then 6 ids_src1, 7 ids_dst,
- * 8 expert bounds, 9 f32 act [n_tok * k][inter] (F16 guard only, after the division), 10 guard scales [n_tok * k],
+ * 8 expert bounds, group prefix, arrival counters and the status word, 9 f32 act [n_tok * k][inter] (F16 guard
+ * only, after the division), 10 guard scales [n_tok * k],
  * 11 RMSNorm output, 12 its Q8_1 blocks, 13 shared-expert act images, 14 shared-expert output). Inspection and tests;
  * the image layouts are internal. */
 int fns_hip_moe_prefill_section(const FnsMoeLayer *layer, int64_t n_tok, int section, size_t *offset, size_t *bytes);
 int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int64_t n_tok,
                         void *workspace, size_t workspace_bytes, void *stream);
+/* No counterpart in the reference. Without the F16 guard and for gate/up and down types from {Q3_K, Q4_K}, gate/up
+ * and down run as one launch whose down workgroups wait (bounded) for their row group's gate/up
+ * workgroups; one that gives up writes NaN to its output rows and sets FNS_STATUS_EXCHANGE_TIMEOUT in the workspace's
+ * status word (section 8, which the workspace must hold zeroed when first used). As fns_hip_moe_layer_status: waits
+ * for the stream's work so far, stores the word in *status and, with clear = 1, zeroes it. The poll limit and
+ * withheld arrivals of fns_hip_moe_set_test_hooks apply to this wait too. Not graph-capturable (it synchronises). */
+int fns_hip_moe_prefill_status(const FnsMoeLayer *layer, int64_t n_tok, void *workspace, int clear, uint32_t *status,
+                               void *stream);
 
 /* --- GGUF checkpoints: reader and fully resident MoE layers ---
  * Replaces the reference's loader (src/model.cpp:30-136: gguf header and tensor table, the file mapped without copying)

@@ -361,3 +361,62 @@ def test_moe_prefill_guard_bf16_sigmoid_residual(ops):
     tr["out"] = out
     check_prefill_chains(tr, layer, slots, xh, list(range(T)), ids, orc.Q4_K, orc.Q6_K, H, F,
                          "guarded bf16 sigmoid prefill", resid=host(resid))
+
+
+def _skewed_q4k_layer(ops, guard):
+    from flintnsteel_amd import synth
+    H, F, NE, K = 2048, 768, 128, 8
+    base = synth.build_layer(H, F, NE, K, orc.Q4_K, orc.Q4_K, seed=20261022, layer=400)
+    rng = np.random.default_rng(20261022)
+    bias = dev(np.log(rng.dirichlet(np.full(NE, 0.3)) + 1e-6).astype(np.float32) * 0.5)
+    return ops.MoeLayer(base.router_w, base.slots, orc.Q4_K, orc.Q4_K, H, F, K, router_bias=bias, guard=guard)
+
+
+def test_moe_prefill_fused_launch_equals_two_launches(ops):
+    """Without the F16 guard, gate/up and down run as one launch (down workgroups wait for their row group's gate/up
+    workgroups); with the guard on and no row scaled, as two launches with the guard pass between them. Every per-item
+    computation is the same, so the outputs agree bit for bit - over three calls in a row (the arrival counters are
+    re-armed by each call's compaction) and a smaller batch on the same workspace."""
+    from flintnsteel_amd import synth
+    fused, two = ops.MoePrefill(_skewed_q4k_layer(ops, False)), ops.MoePrefill(_skewed_q4k_layer(ops, True))
+    ws_f = fused.workspace(512)
+    for T in (512, 512, 77):
+        print(f"fused vs two launches, T={T}", flush=True)
+        x = synth.activations(T, 2048, seed=20261022, layer=401 + T)
+        ws_t = two.workspace(T)
+        if T != 512:  # the status word sits elsewhere in another batch size's layout: clear it there first
+            fused.status(ws_f, T, clear=True)
+        a = host(fused(x, ws=ws_f))
+        b = host(two(x, ws=ws_t))
+        assert (host(two.trace(ws_t, T)["escale"]) == 1.0).all()
+        st = fused.status(ws_f, T)
+        rows = np.flatnonzero((a != b).any(axis=1))
+        assert np.isfinite(a).all() and rows.size == 0, (f"T={T}: fused launch differs from two launches: status {st}, "
+                                                         f"{int(np.isnan(a).sum())} NaN, rows {rows[:16].tolist()} "
+                                                         f"of {rows.size}")
+        assert st == 0
+
+
+def test_moe_prefill_fused_wait_timeout_is_reported(ops):
+    """Host-forced failure of the fused launch's wait (test hooks: one arrival withheld per group, a short poll
+    limit): every down workgroup gives up, writes NaN rows and sets the sticky status bit; every kernel exits. After
+    the hooks are reset and the word cleared, the same call is clean and matches its earlier result."""
+    from flintnsteel_amd import synth
+    from flintnsteel_amd._lib import call
+    pre = ops.MoePrefill(_skewed_q4k_layer(ops, False))
+    T = 96
+    x = synth.activations(T, 2048, seed=3, layer=5)
+    ws = pre.workspace(T)
+    good = host(pre(x, ws=ws))
+    assert pre.status(ws, T) == 0
+    print("forced wait timeout (withheld arrivals, poll limit 200)", flush=True)
+    call("fns_hip_moe_set_test_hooks", 200, 1)
+    try:
+        bad = host(pre(x, ws=ws))
+    finally:
+        call("fns_hip_moe_set_test_hooks", 0, 0)
+    assert pre.status(ws, T, clear=True) == ops.STATUS_EXCHANGE_TIMEOUT
+    assert np.isnan(bad).any()
+    assert pre.status(ws, T) == 0
+    again = host(pre(x, ws=ws))
+    assert np.array_equal(again, good) and pre.status(ws, T) == 0
