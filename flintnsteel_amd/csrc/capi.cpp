@@ -78,6 +78,7 @@ int fns_hip_set_iq_grids(const uint32_t *iq3xxs, const uint32_t *iq3s, const uin
                                    bytes[i]);
     FNS_TRY(impl::iq_grids_upload_mmvq(&g));
     FNS_TRY(impl::iq_grids_upload_layer(&g));
+    FNS_TRY(impl::iq_grids_upload_mmq(&g));
     host::set_iq_grids_ready();
     return host::OK;
 }

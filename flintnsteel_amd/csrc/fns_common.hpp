@@ -27,6 +27,7 @@
 #define FNS_MARK(k, wg, i) ((void) (wg))
 #define MMQ_MARK(i) ((void) 0)
 #define MMQ_NOTE(v) ((void) 0)
+#define PF_MARK(k, i) ((void) 0)
 #endif
 
 namespace fns::dev {

@@ -52,6 +52,7 @@ size_t moe_noalloc_max_bytes();
 // Each translation unit that decodes IQ blocks keeps its own device copy of the codebooks.
 int iq_grids_upload_mmvq(const void *grids);
 int iq_grids_upload_layer(const void *grids);
+int iq_grids_upload_mmq(const void *grids);
 int moe_layer_stage(const FnsMoeLayer *L, int stage, const float *x, const float *x_resid, float *out, int n_tok,
                     void *ws, size_t ws_bytes, hipStream_t st);
 

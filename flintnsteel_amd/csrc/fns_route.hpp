@@ -251,7 +251,6 @@ __device__ __forceinline__ void route_topk_pairs(const float *__restrict__ lg, i
         }
     }
     __syncthreads();
-    FNS_MARK(1, blockIdx.x, 6);
     const int part = tid % P;
     const int kpl = ((n_expert + 2 * P - 1) / (2 * P)) * 2;  // keys per thread, even (16-byte reads)
     for (int e0 = 0; e0 < n_expert; e0 += EPP) {
@@ -273,7 +272,6 @@ __device__ __forceinline__ void route_topk_pairs(const float *__restrict__ lg, i
         }
     }
     __syncthreads();
-    FNS_MARK(1, blockIdx.x, 7);
 }
 
 // Gating + top-k + renormalisation for one token by a whole workgroup (n_expert <= 256): the all-pairs rank up to

@@ -30,6 +30,7 @@
 #include "fns_host.hpp"
 #include "fns_internal.hpp"
 #include "fns_lanes.hpp"
+#include "fns_quarter.hpp"
 #include "fns_router_gemm.hpp"
 
 #include "fns/ggml_kernels.h"
@@ -67,10 +68,12 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
     constexpr int NW = kCompactThreads / kWave;
     __shared__ int cnt[256];
     __shared__ int wpos[NW][256];  // per-wave counts, then each wave's next sorted position per expert
+    PF_MARK(2, 0);
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     for (int i = tid; i < NW * 256; i += kCompactThreads) (&wpos[0][0])[i] = 0;
     for (int i = tid; i < n_gdone; i += kCompactThreads) gdone[i] = 0;  // the next fused GEMM launch's arrivals
     __syncthreads();
+    PF_MARK(2, 2);
     const int chunk = (n + NW * kWave - 1) / (NW * kWave) * kWave;  // pairs per wave, a multiple of 64
     const int p0 = wave * chunk, p1 = min(n, p0 + chunk);
     // the first kCache ids of each lane stay in registers for the second pass; their loads are clamped into the
@@ -95,6 +98,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         if (e >= 0 && e < ne) atomicAdd(&wpos[wave][e], 1);
     }
     __syncthreads();
+    PF_MARK(2, 3);
     if (tid < ne) {
         int c = 0;
 #pragma unroll
@@ -102,6 +106,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         cnt[tid] = c;
     }
     __syncthreads();
+    PF_MARK(2, 4);
     if (wave == 0) {  // exclusive prefix over <= 256 experts: 4 per lane, then a lane scan
         int v[4], g[4], g2[4], s = 0, sg = 0, sg2 = 0;
 #pragma unroll
@@ -145,6 +150,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         }
     }
     __syncthreads();
+    PF_MARK(2, 5);
     if (tid < ne) {  // the expert's sorted positions, split over the waves in wave order
         int pos = cnt[tid];
 #pragma unroll
@@ -155,6 +161,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         }
     }
     __syncthreads();
+    PF_MARK(2, 6);
     for (int it = 0, p = p0 + lane; p < p0 + chunk; ++it, p += kWave) {
         int e = -1;
 #pragma unroll
@@ -179,6 +186,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         // (this wave's reads above complete before its write below: one wave, LDS accesses in order)
         if (live && rank == 0) wpos[wave][e] += __popcll(same);
     }
+    PF_MARK(2, 1);
 }
 
 // ---- split activation images --------------------------------------------------------------------------------------
@@ -280,19 +288,22 @@ __global__ __launch_bounds__(512) void k_router_image(const void *__restrict__ w
                                                       const float *__restrict__ x, float *__restrict__ y, int ncols,
                                                       int nrows, int n_tok, int tiles_x, int n_rt,
                                                       uint8_t *__restrict__ img, int64_t img_row_bytes, int nxb) {
+    PF_MARK(0, 0);
     const int id = blockIdx.x;
     if (id < n_rt) {
         router_gemm_tile<BF16, true>(w, bias, x, y, ncols, nrows, n_tok, id % tiles_x, id / tiles_x);
+        PF_MARK(0, 1);
         return;
     }
     const int item = 2 * (id - n_rt) + (int) threadIdx.x / 256;
-    if (item >= nxb * n_tok) return;
     const int row = item / nxb, col = ((item % nxb) * 256 + (int) threadIdx.x % 256) * 8;
-    if (col >= ncols) return;
-    const float *src = x + (size_t) row * ncols + col;
-    const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
-    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-    q8_split8<true>(v, img + (size_t) row * img_row_bytes, ncols, col, true);
+    if (item < nxb * n_tok && col < ncols) {
+        const float *src = x + (size_t) row * ncols + col;
+        const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+        const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        q8_split8<true>(v, img + (size_t) row * img_row_bytes, ncols, col, true);
+    }
+    PF_MARK(0, 1);
 }
 
 // ---- grouped GEMM -------------------------------------------------------------------------------------------------
@@ -328,6 +339,15 @@ template <> struct WFrag<T_Q4_K> { uint4 h; uint4 q[4]; };
 template <> struct WFrag<T_Q5_K> { uint4 h; uint4 q[4]; uint4 qh; };
 template <> struct WFrag<T_Q6_K> { uint4 ql[4]; uint4 qh[2]; uint4 sc; uint32_t d; };
 template <> struct WFrag<T_Q3_K> { uint4 qs[2]; uint4 hm; uint4 tail; };
+// IQ formats (lane half h, its two column groups of every 32-value sub-block; see decode):
+//   IQ4_XS : header (d, scales_h, scales_l) and qs bytes 8 h .. 8 h + 7 of each sub-block
+//   IQ3_XXS: d, index bytes 4 h .. 4 h + 3 of each sub-block, the sub-block's aux word (signs, scale)
+//   IQ3_S  : d, qh (8 bytes), scales (4 bytes), index bytes 4 h .. 4 h + 3 and sign bytes 2 h, 2 h + 1 per sub-block
+//   IQ2_S  : d, qh, scales, the 16 index bytes and 16 sign bytes of each half block (lanes use 2 of every 4)
+template <> struct WFrag<T_IQ4_XS> { uint2 h; uint2 q[8]; };
+template <> struct WFrag<T_IQ3_XXS> { uint32_t d; uint32_t idx[8]; uint4 aux[2]; };
+template <> struct WFrag<T_IQ3_S> { uint32_t d, sc; uint2 qh; uint32_t idx[8], sg[8]; };
+template <> struct WFrag<T_IQ2_S> { uint32_t d; uint2 qh, sc; uint4 idx[2], sg[2]; };
 
 // Buffer loads: a uniform base in a resource (SGPRs), a 32-bit per-lane offset and a uniform offset - no 64-bit
 // address arithmetic per load. (Unaligned dword access is enabled on the platform, as for the plain global loads.)
@@ -338,6 +358,16 @@ __device__ __forceinline__ Rsrc rsrc_of(const void *base) {
 __device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t vo, uint32_t so) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bload8(Rsrc r, uint32_t vo, uint32_t so) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t bload4(Rsrc r, uint32_t vo, uint32_t so) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0);
+}
+__device__ __forceinline__ uint32_t bload2(Rsrc r, uint32_t vo, uint32_t so) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0);
 }
 
 // Part P (compile time) of the fragment of the block at (vo + so) from r; vc = vo + 16 h selects the lane's code
@@ -360,17 +390,55 @@ __device__ __forceinline__ void wfrag_load(Rsrc r, uint32_t vo, uint32_t vc, uin
             f.sc = bload16(r, vo, so + 192);
             f.d = __builtin_amdgcn_raw_buffer_load_b16(r, vo, so + 208, 0);
         }
-    } else {
+    } else if constexpr (T == T_Q3_K) {
         if constexpr (P == 0) {
             f.hm = bload16(r, vc, so);
             f.tail = bload16(r, vo, so + 94);  // scales[12] at +2, d at +14
         }
         f.qs[P] = bload16(r, vc, so + 32 + 32 * P);
+    } else if constexpr (T == T_IQ4_XS) {  // d @0, scales_h @2, scales_l @4, qs @8 (16 per sub-block)
+        const uint32_t vq = vo + ((vc - vo) >> 1);  // + 8 h
+        if constexpr (P == 0) f.h = bload8(r, vo, so);
+#pragma unroll
+        for (int ib = 4 * P; ib < 4 * P + 4; ++ib) f.q[ib] = bload8(r, vq, so + 8 + 16 * ib);
+    } else if constexpr (T == T_IQ3_XXS) {  // d @0, index bytes @2 (8 per sub-block), aux words @66
+        const uint32_t vq = vo + ((vc - vo) >> 2);  // + 4 h
+        if constexpr (P == 0) f.d = bload2(r, vo, so);
+#pragma unroll
+        for (int ib = 4 * P; ib < 4 * P + 4; ++ib) f.idx[ib] = bload4(r, vq, so + 2 + 8 * ib);
+        f.aux[P] = bload16(r, vo, so + 66 + 16 * P);
+    } else if constexpr (T == T_IQ3_S) {  // d @0, qs @2 (8 per sub-block), qh @66, signs @74 (4 per sub-block), scales @106
+        const uint32_t vq = vo + ((vc - vo) >> 2), vs = vo + ((vc - vo) >> 3);  // + 4 h, + 2 h
+        if constexpr (P == 0) {
+            f.d = bload2(r, vo, so);
+            f.qh = bload8(r, vo, so + 66);
+            f.sc = bload4(r, vo, so + 106);
+        }
+#pragma unroll
+        for (int ib = 4 * P; ib < 4 * P + 4; ++ib) {
+            f.idx[ib] = bload4(r, vq, so + 2 + 8 * ib);
+            f.sg[ib] = bload2(r, vs, so + 74 + 4 * ib);
+        }
+    } else {  // IQ2_S: d @0, index bytes @2 (4 per sub-block), sign bytes @34 (4 per sub-block), qh @66, scales @74
+        if constexpr (P == 0) {
+            f.d = bload2(r, vo, so);
+            f.qh = bload8(r, vo, so + 66);
+            f.sc = bload8(r, vo, so + 74);
+        }
+        f.idx[P] = bload16(r, vo, so + 2 + 16 * P);
+        f.sg[P] = bload16(r, vo, so + 34 + 16 * P);
     }
 }
 // vector loads issued by part P of wfrag_load for one stream
 template <int T, int P> constexpr int wfrag_loads() {
-    return T == T_Q4_K ? (P ? 2 : 3) : T == T_Q5_K ? (P ? 2 : 4) : T == T_Q6_K ? (P ? 3 : 5) : (P ? 1 : 3);
+    return T == T_Q4_K    ? (P ? 2 : 3)
+           : T == T_Q5_K  ? (P ? 2 : 4)
+           : T == T_Q6_K  ? (P ? 3 : 5)
+           : T == T_Q3_K  ? (P ? 1 : 3)
+           : T == T_IQ4_XS ? (P ? 4 : 5)
+           : T == T_IQ3_XXS ? (P ? 5 : 6)
+           : T == T_IQ3_S ? (P ? 8 : 11)
+                          : (P ? 2 : 5);  // IQ2_S
 }
 // the 8 code bytes of column group 2 h + p (p compile time) from a 16-byte code array
 __device__ __forceinline__ uint2 half8(const uint4 &v, int p) { return p ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y); }
@@ -405,8 +473,10 @@ __device__ __forceinline__ v8h centred8(uint32_t x, uint32_t y, h2 off, h2 sc) {
 // integer scale as f16 (Q6_K: two operands, scale split as 16 (sc >> 4) + (sc & 15), each product exact). The block's
 // float scale d (and dmin) are applied per superblock. on = (d != 0): a block with d = 0 contributes d * (...) = 0
 // whatever its codes.
-template <int T> struct BOp { v8h b[T == T_Q6_K ? 2 : 1]; };
-template <int T> __device__ __forceinline__ BOp<T> decode(const WFrag<T> &f, int s, int p, int h, bool on);
+template <int T> constexpr int kNumB = T == T_Q6_K || T == T_IQ4_XS ? 2 : 1;
+template <int T> struct BOp { v8h b[kNumB<T>]; };
+template <int T>
+__device__ __forceinline__ BOp<T> decode(const WFrag<T> &f, int s, int p, int h, bool on, const uint32_t *grid);
 
 // (sc_s, sc_s) as f16 and its bias -1024 sc_s for sub-block s (compile time) of a Q4_K / Q5_K block; on = 0: zeros.
 // The 6-bit scales are unpacked four at a time (ggml get_scale_min_k4), byte s placed twice next to 0x64 (1024.0).
@@ -416,7 +486,7 @@ __device__ __forceinline__ void k4_scale2(const uint4 &h, int s, bool on, h2 &s2
     s2 = as_h2(__builtin_amdgcn_perm(0x64646464u, on ? w : 0u, 0x04000400u | (i << 16) | i)) - splat((_Float16) 1024.0f);
     bias = s2 * splat((_Float16) -1024.0f);
 }
-template <> __device__ __forceinline__ BOp<T_Q4_K> decode<T_Q4_K>(const WFrag<T_Q4_K> &f, int s, int p, int, bool on) {
+template <> __device__ __forceinline__ BOp<T_Q4_K> decode<T_Q4_K>(const WFrag<T_Q4_K> &f, int s, int p, int, bool on, const uint32_t *) {
     const uint2 q = half8(f.q[s >> 1], p);
     const int sh = 4 * (s & 1);
     h2 s2, bias;
@@ -425,7 +495,7 @@ template <> __device__ __forceinline__ BOp<T_Q4_K> decode<T_Q4_K>(const WFrag<T_
     r.b[0] = scaled8((q.x >> sh) & kLo4, (q.y >> sh) & kLo4, s2, bias);
     return r;
 }
-template <> __device__ __forceinline__ BOp<T_Q5_K> decode<T_Q5_K>(const WFrag<T_Q5_K> &f, int s, int p, int, bool on) {
+template <> __device__ __forceinline__ BOp<T_Q5_K> decode<T_Q5_K>(const WFrag<T_Q5_K> &f, int s, int p, int, bool on, const uint32_t *) {
     const uint2 q = half8(f.q[s >> 1], p), qh = half8(f.qh, p);
     const int sh = 4 * (s & 1);
     h2 s2, bias;
@@ -437,7 +507,7 @@ template <> __device__ __forceinline__ BOp<T_Q5_K> decode<T_Q5_K>(const WFrag<T_
 }
 // Q6_K sub-block s: n = s / 4, qq = s % 4: ql[64 n + 32 (qq & 1) + l] nibble qq >> 1, qh[32 n + l] bits 2 qq,
 // value - 32; int8 scale of group 8 n + 2 qq + (l >= 16), i.e. + h for column groups 2 h, 2 h + 1.
-template <> __device__ __forceinline__ BOp<T_Q6_K> decode<T_Q6_K>(const WFrag<T_Q6_K> &f, int s, int p, int h, bool on) {
+template <> __device__ __forceinline__ BOp<T_Q6_K> decode<T_Q6_K>(const WFrag<T_Q6_K> &f, int s, int p, int h, bool on, const uint32_t *) {
     const int n = s >> 2, qq = s & 3;
     const uint2 ql = half8(f.ql[2 * n + (qq & 1)], p), qh = half8(f.qh[n], p);
     const int shl = 4 * (qq >> 1), shh = 2 * qq;
@@ -454,7 +524,7 @@ template <> __device__ __forceinline__ BOp<T_Q6_K> decode<T_Q6_K>(const WFrag<T_
 }
 // Q3_K sub-block s: n = s / 4, j = s % 4: qs[32 n + l] bits 2 j, hmask[l] bit 4 n + j (clear: -4); scale groups
 // 8 n + 2 j + (l >= 16), 6-bit value - 32 (low nibbles in scales[0..7], high bit pairs in scales[8..11]).
-template <> __device__ __forceinline__ BOp<T_Q3_K> decode<T_Q3_K>(const WFrag<T_Q3_K> &f, int s, int p, int h, bool on) {
+template <> __device__ __forceinline__ BOp<T_Q3_K> decode<T_Q3_K>(const WFrag<T_Q3_K> &f, int s, int p, int h, bool on, const uint32_t *) {
     const int n = s >> 2, j = s & 3;
     const uint2 q = half8(f.qs[n], p), hm = half8(f.hm, p);
     const int hs = 4 * n + j;
@@ -479,12 +549,79 @@ template <> __device__ __forceinline__ BOp<T_Q3_K> decode<T_Q3_K>(const WFrag<T_
     return r;
 }
 
+// IQ formats: B = signed codebook value x integer sub-block scale, exact in f16 (|B| <= 2048, or split in two
+// operands), the rest of the float scale in blk_d: IQ4_XS kv * (ls - 32) (split as 4 (s >> 2) + (s & 3)) with d;
+// IQ3_XXS g * (2 ls + 1) with d / 4; IQ3_S g * (2 sc + 1) with d; IQ2_S g * (2 ls + 1) with d / 8 - the products of
+// the dequantisers' scales (ggml-quants.c dequantize_row_iq*). Codebook entries come from the LDS copy `grid` of the
+// format's table. Signed values are biased by 128 (byte ^ 0x80) for the 1024 + byte conversion.
+__device__ __forceinline__ v8h signed_scaled8(uint32_t x, uint32_t y, int sc, bool on) {  // x, y: 4 int8 each
+    const _Float16 s = (_Float16) (on ? sc : 0);
+    return scaled8(x ^ 0x80808080u, y ^ 0x80808080u, splat(s), splat((_Float16) -1152.0f * s));
+}
+template <> __device__ __forceinline__ BOp<T_IQ4_XS> decode<T_IQ4_XS>(const WFrag<T_IQ4_XS> &f, int s, int p, int,
+                                                                      bool on, const uint32_t *) {
+    // column group p: the low (p = 0) or high (p = 1) nibbles of the lane's 8 bytes, values 8 h .. 8 h + 7 (+ 16 p)
+    const uint32_t x = iq4nl_values((f.q[s].x >> (4 * p)) & kLo4), y = iq4nl_values((f.q[s].y >> (4 * p)) & kLo4);
+    const int ls = (int) (((f.h.y >> (4 * s)) & 0xfu) | (((f.h.x >> (16 + 2 * s)) & 3u) << 4)) - 32;
+    BOp<T_IQ4_XS> r;
+    r.b[0] = signed_scaled8(x, y, 4 * (ls >> 2), on);
+    r.b[1] = signed_scaled8(x, y, ls & 3, on);
+    return r;
+}
+template <> __device__ __forceinline__ BOp<T_IQ3_XXS> decode<T_IQ3_XXS>(const WFrag<T_IQ3_XXS> &f, int s, int p, int h,
+                                                                        bool on, const uint32_t *grid) {
+    const int g = 2 * h + p;  // column group: index bytes 2 g, 2 g + 1; signs (aux >> 7 g) & 127
+    const uint32_t aux = word(f.aux[s >> 2], s & 3), idx = f.idx[s] >> (16 * p);
+    const uint32_t sg = ksigns((aux >> (7 * g)) & 127u);
+    const int x = signed_grid(grid[idx & 0xffu], spread4(sg & 0xfu));
+    const int y = signed_grid(grid[(idx >> 8) & 0xffu], spread4(sg >> 4));
+    BOp<T_IQ3_XXS> r;
+    r.b[0] = signed_scaled8((uint32_t) x, (uint32_t) y, 2 * (int) (aux >> 28) + 1, on);
+    return r;
+}
+template <> __device__ __forceinline__ BOp<T_IQ3_S> decode<T_IQ3_S>(const WFrag<T_IQ3_S> &f, int s, int p, int h,
+                                                                    bool on, const uint32_t *grid) {
+    const int g = 2 * h + p;  // codebook entries 2 g, 2 g + 1 of the sub-block (9-bit indices), sign byte g
+    const uint32_t qh = (s < 4 ? f.qh.x : f.qh.y) >> (8 * (s & 3)), idx = f.idx[s] >> (16 * p);
+    const uint32_t i0 = (idx & 0xffu) | (((qh >> (2 * g)) & 1u) << 8);
+    const uint32_t i1 = ((idx >> 8) & 0xffu) | (((qh >> (2 * g + 1)) & 1u) << 8);
+    const uint32_t sb = (f.sg[s] >> (8 * p)) & 0xffu;
+    const int x = signed_grid(grid[i0], spread4(sb & 0xfu)), y = signed_grid(grid[i1], spread4(sb >> 4));
+    BOp<T_IQ3_S> r;
+    r.b[0] = signed_scaled8((uint32_t) x, (uint32_t) y, 2 * (int) ((f.sc >> (4 * s)) & 0xfu) + 1, on);
+    return r;
+}
+template <> __device__ __forceinline__ BOp<T_IQ2_S> decode<T_IQ2_S>(const WFrag<T_IQ2_S> &f, int s, int p, int h,
+                                                                    bool on, const uint32_t *grid) {
+    const int g = 2 * h + p;  // codebook entry g of the sub-block (10-bit index, 8 values), sign byte g
+    const uint32_t idx = word(f.idx[s >> 2], s & 3), sgw = word(f.sg[s >> 2], s & 3);
+    const uint32_t qh = (s < 4 ? f.qh.x : f.qh.y) >> (8 * (s & 3)), sc = (s < 4 ? f.sc.x : f.sc.y) >> (8 * (s & 3));
+    const uint32_t gi = ((idx >> (8 * g)) & 0xffu) | (((qh >> (2 * g)) & 3u) << 8);
+    const uint32_t sb = (sgw >> (8 * g)) & 0xffu;
+    const int x = signed_grid(grid[2 * gi], spread4(sb & 0xfu)), y = signed_grid(grid[2 * gi + 1], spread4(sb >> 4));
+    BOp<T_IQ2_S> r;
+    r.b[0] = signed_scaled8((uint32_t) x, (uint32_t) y, 2 * (int) ((sc >> (4 * h)) & 0xfu) + 1, on);
+    return r;
+}
+
 // Per-superblock float scales of this lane's row: d, and dmin for Q4_K / Q5_K.
 template <int T> __device__ __forceinline__ float blk_d(const WFrag<T> &f) {
     if constexpr (T == T_Q4_K || T == T_Q5_K) return half_to_float(f.h.x & 0xffffu);
     else if constexpr (T == T_Q6_K) return half_to_float(f.d);
-    else return half_to_float(f.tail.w >> 16);
+    else if constexpr (T == T_Q3_K) return half_to_float(f.tail.w >> 16);
+    else if constexpr (T == T_IQ4_XS) return half_to_float(f.h.x & 0xffffu);
+    else if constexpr (T == T_IQ3_XXS) return 0.25f * half_to_float(f.d & 0xffffu);
+    else if constexpr (T == T_IQ3_S) return half_to_float(f.d & 0xffffu);
+    else return 0.125f * half_to_float(f.d & 0xffffu);  // IQ2_S
 }
+// The A piece (8 columns, 16 bytes of a half-superblock chunk row) of step i for lane half hh: sub-block i / 2,
+// column group 2 hh + i % 2 (the decoders above emit those), or for IQ4_XS group 2 (i % 2) + hh (its lane half reads
+// 8 bytes of both nibbles: values 8 hh .. 8 hh + 7 and 16 + 8 hh ..).
+template <int T> __device__ __forceinline__ int a_piece(int i, int hh) {
+    return T == T_IQ4_XS ? 4 * (i >> 1) + 2 * (i & 1) + hh : 4 * (i >> 1) + 2 * hh + (i & 1);
+}
+// LDS words of the format's codebook (IQ2_S: two words per entry)
+template <int T> constexpr int kGridWords = T == T_IQ3_XXS ? 256 : T == T_IQ3_S ? 512 : T == T_IQ2_S ? 2048 : 0;
 // Q4_K / Q5_K min term operand: B[k][row] = m_s against the A operand [S_hi 8 | S_lo 8] (lane half h holds k = 8 h ..
 // 8 h + 7), both halves the 8 mins in the stored sum order 0 2 1 3 4 6 5 7.
 template <int T> __device__ __forceinline__ v8h min_b(const WFrag<T> &f) {
@@ -578,6 +715,7 @@ struct MmqLds {
     int (&src)[kMmqTok];
     int (&dst)[kMmqTok];
     int (&grp)[4];  // the group's expert, first sorted row and row count
+    uint32_t *grid;  // IQ3_XXS / IQ3_S / IQ2_S: the codebook (kGridWords words)
 };
 
 // Group g of the launch's list (NT = 2: the 64-row groups and remainders > 32 rows; NT = 1: the expert's <= 32-row
@@ -592,12 +730,18 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
     auto &sh_s = L.s;
     auto &sh_src = L.src;
     auto &sh_dst = L.dst;
-    constexpr int BB = Traits<T>::bytes, NB = T == T_Q6_K ? 2 : 1;
+    constexpr int BB = Traits<T>::bytes, NB = kNumB<T>;
     constexpr bool MIN = T == T_Q4_K || T == T_Q5_K;
     // (the wave index as a scalar: the LDS-DMA destinations derived from it are wave-uniform M0 values)
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
     const int hh = lane / 32, jl = lane % 32;
 
+    if constexpr (kGridWords<T> > 0) {  // the codebook into LDS (visible after the barriers below)
+        const uint4 *src = (const uint4 *) (T == T_IQ3_XXS ? (const void *) g_iq_grids.iq3xxs
+                                            : T == T_IQ3_S ? (const void *) g_iq_grids.iq3s
+                                                           : (const void *) g_iq_grids.iq2s);
+        for (int i = tid; i < kGridWords<T> / 4; i += kMmqThreads) ((uint4 *) L.grid)[i] = src[i];
+    }
     // which expert / rows of activations: thread t < n_expert tests whether group g is expert t's (gp[t] <= g <
     // gp[t + 1]); all the prefix loads are independent, one round trip, and the one match publishes through LDS
     int e = 0, seg = 0, cnt = 0;
@@ -713,7 +857,7 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
     // acc[t][m] += A (hi, lo) x B (integer-scaled codes). Software-pipelined: while the MFMAs of step i issue, the A
     // fragments of step i + 1 are read from LDS and its B operands decoded (VALU), interleaved one MFMA / a few VALU.
     auto load_a = [&](const uint8_t *buf, int i, v8h (&av)[2][NT]) __attribute__((always_inline)) {
-        const int piece = 4 * (i >> 1) + 2 * hh + (i & 1);
+        const int piece = a_piece<T>(i, hh);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const uint8_t *ap = buf + (t * 32 + jl) * kRowA;
@@ -722,14 +866,15 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
         }
     };
     auto load_a1 = [&](const uint8_t *buf, int i, int x, v8h (&av)[NT]) __attribute__((always_inline)) {
-        const int piece = 16 * x + 4 * (i >> 1) + 2 * hh + (i & 1);
+        const int piece = 16 * x + a_piece<T>(i, hh);
 #pragma unroll
         for (int t = 0; t < NT; ++t) av[t] = *(const v8h *) (buf + (t * 32 + jl) * kRowA + 16 * (piece ^ (jl & 15)));
     };
     auto half_pass = [&](const uint8_t *buf, auto hc, const WFrag<T> &f0, const WFrag<T> &f1) __attribute__((always_inline)) {
         constexpr int h = decltype(hc)::value;
         v8h av[2][NT];
-        BOp<T> b0 = decode<T>(f0, 4 * h, 0, hh, on0), b1 = decode<T>(f1, 4 * h, 0, hh, on1), d0, d1;
+        const uint32_t *grid = L.grid;
+        BOp<T> b0 = decode<T>(f0, 4 * h, 0, hh, on0, grid), b1 = decode<T>(f1, 4 * h, 0, hh, on1, grid), d0, d1;
         load_a(buf, 0, av);
         if constexpr (NB == 1) {
             // One B operand per stream: the hi fragments of step i + 1 are read into the registers of step i's as soon
@@ -738,8 +883,8 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
             for (int i = 0; i < 8; ++i) {
                 __builtin_amdgcn_sched_barrier(0);
                 if (i < 7) {
-                    d0 = decode<T>(f0, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on0);
-                    d1 = decode<T>(f1, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on1);
+                    d0 = decode<T>(f0, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on0, grid);
+                    d1 = decode<T>(f1, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on1, grid);
                 }
 #pragma unroll
                 for (int x = 0; x < 2; ++x) {
@@ -772,8 +917,8 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
                 __builtin_amdgcn_sched_barrier(0);
                 if (i < 7) {
                     load_a(buf, i + 1, an);
-                    d0 = decode<T>(f0, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on0);
-                    d1 = decode<T>(f1, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on1);
+                    d0 = decode<T>(f0, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on0, grid);
+                    d1 = decode<T>(f1, 4 * h + (i + 1) / 2, (i + 1) & 1, hh, on1, grid);
                 }
                 // hi for every (tile, stream), then lo: dependent MFMAs 2 NT issues apart
 #pragma unroll
@@ -965,8 +1110,9 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     __shared__ __align__(16) uint8_t sh_a0[kMmqTok * kRowA];
     __shared__ __align__(16) uint8_t sh_a1[kMmqTok * kRowA];
     __shared__ __align__(16) uint8_t sh_s[(T == T_Q4_K || T == T_Q5_K) ? kMmqTok * kRowS : 16];
+    __shared__ __align__(16) uint32_t sh_grid[kGridWords<T> > 0 ? kGridWords<T> : 4];
     __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok], sh_grp[4];
-    const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp};
+    const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp, sh_grid};
     const int lid = blockIdx.x, r = lid / kXcds;
     const int g = (r / a.n_cb) * kXcds + lid % kXcds, wb = r % a.n_cb;
     if (g >= a.n_groups) return;
@@ -1001,7 +1147,8 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     __shared__ __align__(16) uint8_t sh_a1[kMmqTok * kRowA];
     __shared__ __align__(16) uint8_t sh_s[MIN ? kMmqTok * kRowS : 16];
     __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok], sh_grp[4];
-    const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp};
+    const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp, nullptr};
+    PF_MARK(3, 0);
     const int total = m.n_main + m.n_expert;
     const int items_gu = m.n_cb_gu * kXcds * ((total + kXcds - 1) / kXcds);  // a multiple of kXcds
     const bool is_gu = (int) blockIdx.x < items_gu;
@@ -1043,6 +1190,7 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
         if (g < m.n_main) mmq_group<TDN, false, 2, true>(a, g, wb, L);
         else mmq_group<TDN, false, 1, true>(a, g - m.n_main, wb, L);
     }
+    PF_MARK(3, 1);
 }
 
 template <bool GLU> const void *mmq_kernel(int type) {
@@ -1051,6 +1199,10 @@ template <bool GLU> const void *mmq_kernel(int type) {
         case T_Q4_K: return (const void *) k_mmq<T_Q4_K, GLU>;
         case T_Q5_K: return (const void *) k_mmq<T_Q5_K, GLU>;
         case T_Q6_K: return (const void *) k_mmq<T_Q6_K, GLU>;
+        case T_IQ4_XS: return (const void *) k_mmq<T_IQ4_XS, GLU>;
+        case T_IQ3_XXS: return (const void *) k_mmq<T_IQ3_XXS, GLU>;
+        case T_IQ3_S: return (const void *) k_mmq<T_IQ3_S, GLU>;
+        case T_IQ2_S: return (const void *) k_mmq<T_IQ2_S, GLU>;
     }
     return nullptr;
 }
@@ -1110,7 +1262,10 @@ int launch_mmq_moe(int tgu, int tdn, MoeArgs m, hipStream_t st) {
 }
 
 int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
-    if (!host::is_kquant(type)) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
+    if (!host::is_kquant(type) && !host::is_iq(type))
+        return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
+    if (host::iq_needs_grid(type) && !host::iq_grids_ready())
+        return host::set_error(host::ERR_TYPE, "mmq: type %d needs the IQ codebooks (fns_hip_set_iq_grids)", type);
     if (ncols <= 0 || ncols % 256 || nrows <= 0 || nrows % kMmqRows || ncols > 65536)
         return host::set_error(host::ERR_SHAPE, "mmq: ncols must be a positive multiple of 256, nrows of 64");
     return host::OK;
@@ -1118,6 +1273,12 @@ int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
 }  // namespace
 
 namespace impl {
+
+// This translation unit's copy of the IQ codebooks (fns_quarter.hpp g_iq_grids), on the current device.
+int iq_grids_upload_mmq(const void *grids) {
+    const hipError_t e = dev::upload_iq_grids((const dev::IqGrids *) grids);
+    return e == hipSuccess ? host::OK : host::set_error(host::ERR_LAUNCH, "set_iq_grids: %s", hipGetErrorString(e));
+}
 
 size_t mmq_image_bytes(int64_t ncols) { return (size_t) split_row_bytes(ncols); }
 size_t mmq_q8_1_bytes(int64_t ncols, int64_t nrows) { return (size_t) nrows * mmq_image_bytes(ncols) + 4096; }

@@ -83,12 +83,14 @@ __global__ __launch_bounds__(kRouteThreads) void k_route_topk(const float *__res
     __shared__ __align__(16) uint64_t s_key[kTopkScratch];
     __shared__ int s_sel[16];
     __shared__ float s_pv[16];
+    PF_MARK(1, 0);
     const int t = blockIdx.x;
     route_topk_block<kRouteThreads>(logits + (size_t) t * n_expert, n_expert, k, gating, s_key, s_sel, s_pv);
     if ((int) threadIdx.x < k) {
         ids[(size_t) t * k + threadIdx.x] = s_sel[threadIdx.x];
         w[(size_t) t * k + threadIdx.x] = route_weight(s_pv, k, norm, threadIdx.x);
     }
+    PF_MARK(1, 1);
 }
 
 __global__ void k_moe_combine(const float *__restrict__ dexp, const float *__restrict__ escale,
@@ -112,6 +114,7 @@ template <int K>
 __global__ void k_moe_combine4(const float *__restrict__ dexp, const float *__restrict__ escale,
                                const float *__restrict__ w, const float *__restrict__ sh, const float *x_in, float *out,
                                int n) {
+    PF_MARK(4, 0);
     const int t = blockIdx.y;
     const int i = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= n) return;
@@ -139,6 +142,7 @@ __global__ void k_moe_combine4(const float *__restrict__ dexp, const float *__re
     o.z = (col([](float4 v) { return v.z; }) + s.z) + xv.z;
     o.w = (col([](float4 v) { return v.w; }) + s.w) + xv.w;
     *(float4 *) (out + (size_t) t * n + i) = o;
+    PF_MARK(4, 1);
 }
 
 __global__ void k_count_routes(const int32_t *ids, uint32_t *counts, int k) {

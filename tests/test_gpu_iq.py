@@ -1,7 +1,8 @@
-"""IQ formats on the GPU (IQ4_XS, IQ3_XXS, IQ3_S, IQ2_S; reference src/ggml/ggml_mmvq.cu:101-157,378-385,403-411):
-the dense and expert-table GEMVs and the whole decode / verify layer against the CPU oracle, which restates the
-reference's integer sub-block products with the same codebooks (tests/iq_data.py registers identical seeded tables in
-both; ggml's own tables are not in this container, so agreement with them is not pinned).
+"""IQ formats on the GPU (IQ4_XS, IQ3_XXS, IQ3_S, IQ2_S; reference src/ggml/ggml_mmvq.cu:101-157,378-385,403-411,
+src/ggml/ggml_mmq.cu:59-66): the dense and expert-table GEMVs, the whole decode / verify layer, the prefill GEMM and
+the prefill layer against the CPU oracle, which restates the reference's integer sub-block products (GEMV) and the
+dequantisers' float sub-block scales (GEMM) with the same codebooks (tests/iq_data.py registers identical seeded
+tables in both; ggml's own tables are not in this container, so agreement with them is not pinned).
 
 Bars: GEMV outputs within 1e-5 relative L2 / 1e-4 normalised max of the oracle (fp32 accumulation against float64);
 the layer within the north_star's 1e-3 with ids and weights bit-exact; a verify column equal to its batch-1 result.
@@ -151,14 +152,73 @@ def test_moe_layer_decode_and_verify(ops, case):
         assert np.array_equal(out4[t], outs1[t]), f"verify column {t} differs from its batch-1 result"
 
 
-def test_prefill_rejects_iq_experts(ops):
-    """The prefill GEMM (MMQ) takes the K-quants only; an IQ layer's prefill is refused with FNS_ERR_TYPE before any
-    launch (the decode and verify paths above take IQ)."""
-    from flintnsteel_amd._lib import FnsError
-    H, F, NE, K = 1024, 512, 8, 2
-    slots = ops.ExpertSlots.from_tensors(*(torch.from_numpy(random_blocks(orc.IQ4_XS, NE * r, c, s).reshape(NE, -1))
-                                           for r, c, s in ((F, H, 1), (F, H, 2), (H, F, 3))))
-    layer = ops.MoeLayer(ops.fill_normal(torch.empty(NE, H, device="cuda"), 3, std=0.02), slots, orc.IQ4_XS,
-                         orc.IQ4_XS, H, F, K)
-    with pytest.raises(FnsError, match="not supported"):
-        ops.MoePrefill(layer)(torch.zeros(8, H, device="cuda"))
+def _dq(qtype, blocks, ncols):
+    """float64 [rows][ncols] of IQ blocks (the oracle's dequantiser: the products of ggml's MMQ scales)."""
+    return orc.dequantize(qtype, np.ascontiguousarray(blocks), ncols).reshape(blocks.shape[0], ncols)
+
+
+def _table(slots_dev):
+    return torch.tensor([slots_dev.data_ptr() + e * slots_dev.stride(0) for e in range(slots_dev.shape[0])],
+                        dtype=torch.int64, device="cuda")
+
+
+@pytest.mark.parametrize("qtype", IQ_TYPES, ids=lambda t: orc.TYPE_NAMES[t])
+def test_mmq_iq_dense_and_experts(ops, qtype):
+    """The prefill GEMM (MMQ) on IQ weights (reference src/ggml/ggml_mmq.cu:59-66 accepts all four): the dense form
+    and the expert form over every group shape, against the float64 dot of the oracle's dequantised weights with the
+    Q8_1 activations (ggml's MMQ applies each sub-block's scale as the dequantiser's float product, which the f16 split
+    GEMM reproduces exactly before its fp32 accumulation)."""
+    print(f"IQ mmq {orc.TYPE_NAMES[qtype]}", flush=True)
+    rng = np.random.default_rng(qtype)
+    T, ncols, nrows = 77, 768, 192
+    w = random_blocks(qtype, nrows, ncols, seed=300 + qtype)
+    x = rng.standard_normal((T, ncols)).astype(np.float32)
+    got = host(ops.mmq(qtype, torch.from_numpy(w).cuda(), ncols, nrows, torch.from_numpy(x).cuda()))
+    xdq = orc.dequantize_q8_1(orc.quantize_q8_1(x), ncols).reshape(T, ncols)
+    assert_close(got, xdq @ _dq(qtype, w, ncols).T, f"mmq dense {orc.TYPE_NAMES[qtype]}")
+    loads = [0, 1, 16, 17, 32, 33, 63, 64, 65, 129]
+    NE, ncols, nrows = len(loads), 512, 128
+    pairs = np.concatenate([np.full(n, e, np.int32) for e, n in enumerate(loads)])
+    ids = pairs[rng.permutation(len(pairs))].reshape(-1, 1)
+    mats = np.stack([random_blocks(qtype, nrows, ncols, seed=400 + 10 * qtype + e) for e in range(NE)])
+    md = torch.from_numpy(mats.reshape(NE, -1)).cuda()
+    x = rng.standard_normal((len(ids), ncols)).astype(np.float32)
+    got = host(ops.mmq_experts(qtype, _table(md), 0, ncols, nrows, NE, torch.from_numpy(x).cuda(), 1,
+                               torch.from_numpy(ids).cuda())).reshape(len(ids), nrows)
+    xdq = orc.dequantize_q8_1(orc.quantize_q8_1(x), ncols).reshape(len(ids), ncols)
+    ref = np.stack([xdq[i] @ _dq(qtype, mats[ids[i, 0]], ncols).T for i in range(len(ids))])
+    assert_close(got, ref, f"mmq_experts group shapes {orc.TYPE_NAMES[qtype]}")
+
+
+@pytest.mark.parametrize("gu,dn", [(orc.IQ3_XXS, orc.IQ4_XS), (orc.IQ2_S, orc.IQ3_S)], ids=["iq3xxs_iq4xs", "iq2s_iq3s"])
+def test_moe_prefill_iq(ops, gu, dn):
+    """The prefill layer with IQ experts (two-launch MMQ path): routing bit-exact against the oracle from the layer's
+    logits; the act image within half a Q8_1 step of the float64 SwiGLU of the dequantised gate / up products; the
+    output against the float64 chain fed with the GPU's act codes (tight bounds)."""
+    from tests.helpers import image_to_q8_1
+    from flintnsteel_amd import synth
+    H, F, NE, K, T = 512, 256, 8, 2, 77
+    print(f"IQ prefill {orc.TYPE_NAMES[gu]}/{orc.TYPE_NAMES[dn]}", flush=True)
+    g_, u_, d_ = (random_blocks(gu, NE * F, H, 21), random_blocks(gu, NE * F, H, 22), random_blocks(dn, NE * H, F, 23))
+    slots = ops.ExpertSlots.from_tensors(*(torch.from_numpy(a.reshape(NE, -1)) for a in (g_, u_, d_)))
+    layer = ops.MoeLayer(ops.fill_normal(torch.empty(NE, H, device="cuda"), 5, std=0.05), slots, gu, dn, H, F, K)
+    pre = ops.MoePrefill(layer)
+    x = synth.activations(T, H, 7, layer=2)
+    ws = pre.workspace(T)
+    out = host(pre(x, ws=ws))
+    tr = {k: host(v) for k, v in pre.trace(ws, T).items()}
+    ids, w, _, _ = orc.route_topk(tr["logits"], K, 0)
+    assert np.array_equal(ids, tr["ids"]) and np.array_equal(w, tr["w"])
+    xdq = orc.dequantize_q8_1(orc.quantize_q8_1(host(x)), H).reshape(T, H)
+    G, U, D = (_dq(gu, g_, H).reshape(NE, F, H), _dq(gu, u_, H).reshape(NE, F, H), _dq(dn, d_, F).reshape(NE, H, F))
+    aq = image_to_q8_1(tr["apack"], F)
+    adq = orc.dequantize_q8_1(aq, F).reshape(T, K, F)
+    ref = np.zeros((T, H))
+    for t in range(T):
+        for j in range(K):
+            e = int(ids[t, j])
+            act = orc.swiglu((G[e] @ xdq[t])[None], (U[e] @ xdq[t])[None])[0]
+            step = np.repeat(np.abs(adq[t, j]).reshape(-1, 32).max(axis=1) / 127.0, 32)
+            assert (np.abs(adq[t, j] - act) <= 0.5 * step + 1e-3 * np.abs(act).max()).all(), f"act image t={t} j={j}"
+            ref[t] += (D[e] @ adq[t, j]) * float(w[t, j])
+    assert_close(out, ref, f"IQ prefill {orc.TYPE_NAMES[gu]}/{orc.TYPE_NAMES[dn]} (GPU act codes)")
