@@ -33,6 +33,9 @@ int mmvq_experts_swiglu(int type, const char *const *table, size_t gate_off, siz
                         hipStream_t st);
 int mmvq_experts(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, const void *xq,
                  int64_t n_xq, const int32_t *ids, int64_t n_ids, float *dst, hipStream_t st);
+// as mmvq_experts, id i reading activation row (i / x_div) % n_xq
+int mmvq_experts_div(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, const void *xq,
+                     int64_t n_xq, int64_t x_div, const int32_t *ids, int64_t n_ids, float *dst, hipStream_t st);
 
 int gemv_router(int dtype, const void *w, const float *x, float *y, int ncols, int nrows, int cols, hipStream_t st);
 int gemm_router_bias(int dtype, const void *w, const float *bias, const float *x, float *y, int ncols, int nrows,

@@ -1360,8 +1360,19 @@ int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t of
     return launch_mmq(type, glu, a, (int) main_groups(n_expert, n_pairs), st);
 }
 
+// Q8_0 (the reference's dense and output-head type, src/ggml/ggml_mmq.cu:59) takes the GEMV kernels, a few token
+// columns per weight pass: each 32-value block is d_w * d8 * (integer dot) in both, so the results are those of a
+// GEMM over the same Q8_1 activations; the bytes are re-read per column group (the tiled GEMM covers the expert
+// K-quant and IQ formats, whose sub-block scales fold into exact f16 operands; Q8_0's float block scale does not).
 int mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq, float *dst,
         hipStream_t st) {
+    if (type == T_Q8_0) {
+        if (!w || !x || !xq || !dst || n_tok < 0 || ncols <= 0 || ncols % 256 || nrows <= 0)
+            return host::set_error(host::ERR_SHAPE, "mmq: bad arguments");
+        if (n_tok == 0) return host::OK;
+        FNS_TRY(quantize_q8_1(x, xq, ncols, n_tok, st));
+        return mmvq(type, w, ncols, nrows, xq, dst, n_tok, st);
+    }
     FNS_TRY(check_mmq_shape(type, ncols, nrows));
     if (!w || !x || !xq || !dst || n_tok < 0) return host::set_error(host::ERR_SHAPE, "mmq: bad arguments");
     if (n_tok == 0) return host::OK;
@@ -1380,6 +1391,18 @@ int mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, i
 int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, int64_t n_expert,
                 const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
                 int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, void *xq, float *dst, hipStream_t st) {
+    if (type == T_Q8_0) {  // the GEMV over every (token, slot), as mmq above; the expert sort is still written
+        if (!x || !xq || !table || !ids || !dst || n_used < 1 || n_tok < 0 || ncols <= 0 || ncols % 256 ||
+            (x_rows_per_tok != 1 && x_rows_per_tok != n_used))
+            return host::set_error(host::ERR_SHAPE, "mmq_experts: bad arguments");
+        if (n_tok == 0) return host::OK;
+        const int64_t rows = n_tok * x_rows_per_tok;
+        int32_t *gprefix = (int32_t *) ((uint8_t *) xq + (size_t) rows * host::q8_1_row_bytes(ncols));
+        FNS_TRY(mmq_compact(ids, n_tok, n_used, n_expert, x_rows_per_tok, ids_src1, ids_dst, bounds, gprefix, st));
+        FNS_TRY(quantize_q8_1(x, xq, ncols, rows, st));
+        return mmvq_experts_div(type, table, off, ncols, nrows, xq, rows, x_rows_per_tok == 1 ? n_used : 1, ids,
+                                n_tok * n_used, dst, st);
+    }
     FNS_TRY(check_mmq_shape(type, ncols, nrows));
     if (!x || !xq || n_used < 1 || n_tok < 0) return host::set_error(host::ERR_SHAPE, "mmq_experts: bad arguments");
     if (n_tok == 0) return host::OK;

@@ -446,8 +446,13 @@ int mmvq_experts_swiglu(int type, const char *const *table, size_t gate_off, siz
 
 int mmvq_experts(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, const void *xq,
                  int64_t n_xq, const int32_t *ids, int64_t n_ids, float *dst, hipStream_t st) {
+    return mmvq_experts_div(type, table, off, ncols, nrows, xq, n_xq, 1, ids, n_ids, dst, st);
+}
+
+int mmvq_experts_div(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, const void *xq,
+                     int64_t n_xq, int64_t x_div, const int32_t *ids, int64_t n_ids, float *dst, hipStream_t st) {
     FNS_TRY(check_shape(type, ncols, nrows));
-    if (!table || !xq || !ids || !dst || n_xq < 1 || n_ids < 0 || n_ids > 65535)
+    if (!table || !xq || !ids || !dst || n_xq < 1 || x_div < 1 || x_div > 65535 || n_ids < 0 || n_ids > 65535)
         return host::set_error(host::ERR_SHAPE, "mmvq_experts: bad arguments");
     if (n_ids == 0) return host::OK;
     MmvqParams p{};
@@ -458,7 +463,7 @@ int mmvq_experts(int type, const char *const *table, size_t off, int64_t ncols, 
     p.xq = (const uint8_t *) xq;
     p.xq_row_bytes = host::q8_1_row_bytes(ncols);
     p.n_xq = (int) n_xq;
-    p.x_div = 1;
+    p.x_div = (int) x_div;
     p.dst = dst;
     p.ncols = (int) ncols;
     p.nrows = (int) nrows;

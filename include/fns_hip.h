@@ -190,7 +190,10 @@ size_t fns_hip_mmq_q8_1_bytes(int64_t ncols, int64_t nrows);
 /* bytes of the expert_bounds buffer of fns_hip_mmq_compact for n_expert experts (bounds + tile-group prefix) */
 size_t fns_hip_mmq_bounds_bytes(int64_t n_expert);
 /* include/fns/ggml_kernels.h:56-58 mmq: dst[t][nrows] = W . q8_1(x[t]), x f32 [n_tok][ncols]; xq scratch of
- * fns_hip_mmq_q8_1_bytes(ncols, n_tok) bytes. ncols a multiple of 256, nrows of 64. */
+ * fns_hip_mmq_q8_1_bytes(ncols, n_tok) bytes. ncols a multiple of 256, nrows of 64. Types (the reference's MMQ set,
+ * src/ggml/ggml_mmq.cu:59-66, plus Q3_K): the K-quants and IQ4_XS / IQ3_XXS / IQ3_S / IQ2_S (the last three once
+ * their codebooks are registered) on the tiled MFMA GEMM; Q8_0 (any nrows) on the GEMV kernels, a few token columns
+ * per weight pass. */
 int fns_hip_mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq,
                 float *dst, void *stream);
 /* include/fns/ggml_kernels.h:60-69 MmqIdsScratch + mmq_experts: dst[t][j][nrows] = W_e . q8_1(x[t][j % x_rows_per_tok]),

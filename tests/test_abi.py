@@ -76,7 +76,8 @@ def test_mmq_sizes():
 
 def test_mmq_preconditions():
     L = _lib.lib()
-    assert L.fns_hip_mmq(8, _buf(), 2048, 64, _buf(), 4, _buf(), _buf(), None) == -1     # Q8_0: not a K-quant
+    assert L.fns_hip_mmq(10, _buf(), 2048, 64, _buf(), 4, _buf(), _buf(), None) == -1    # Q2_K: not supported
+    assert L.fns_hip_mmq(8, _buf(), 1000, 64, _buf(), 4, _buf(), _buf(), None) == -2     # Q8_0 too: ncols % 256
     assert L.fns_hip_mmq(12, _buf(), 1000, 64, _buf(), 4, _buf(), _buf(), None) == -2    # ncols % 256
     assert L.fns_hip_mmq(12, _buf(), 2048, 100, _buf(), 4, _buf(), _buf(), None) == -2   # nrows % 64
     assert L.fns_hip_mmq(12, _buf(), 2048, 64, _buf(), 0, _buf(), _buf(), None) == 0     # no tokens: no-op

@@ -183,6 +183,30 @@ def test_mmq_experts_group_shapes(ops, qtype):
     assert_close(got.reshape(T * K, nrows), ref, f"mmq_experts group shapes {orc.TYPE_NAMES[qtype]}")
 
 
+def test_mmq_q8_0_dense_and_experts(ops):
+    """Q8_0 (the reference's dense and output-head type, src/ggml/ggml_mmq.cu:59) through fns_hip_mmq and
+    fns_hip_mmq_experts (the GEMV kernels over the token columns) against the float64 oracle; gate-like and down-like
+    activation rows."""
+    rng = np.random.default_rng(8)
+    T, ncols, nrows = 37, 512, 96
+    w = orc.quantize(orc.Q8_0, rng.normal(0, 0.02, (nrows, ncols)).astype(np.float32))
+    x = gaussian(rng, (T, ncols))
+    got = host(ops.mmq(orc.Q8_0, dev(w), ncols, nrows, dev(x)))
+    xq = orc.quantize_q8_1(x)
+    assert_close(got, orc.mmvq_experts(orc.Q8_0, [w], ncols, nrows, xq, T, 1, np.zeros(T, np.int32)), "mmq dense Q8_0")
+    K, NE = 3, 5
+    mats = np.stack([orc.quantize(orc.Q8_0, rng.normal(0, 0.02, (nrows, ncols)).astype(np.float32)) for _ in range(NE)])
+    ids = distinct_ids(rng, T, K, NE)
+    md = dev(mats.reshape(NE, -1))
+    for xr in (1, K):
+        xx = gaussian(rng, (T, xr, ncols))
+        got = host(ops.mmq_experts(orc.Q8_0, table_of(md), 0, ncols, nrows, NE, dev(xx), xr, dev(ids)))
+        xq = orc.quantize_q8_1(xx.reshape(T * xr, ncols))
+        ref = orc.mmvq_experts(orc.Q8_0, list(mats), ncols, nrows, xq, T * xr if xr > 1 else T, 1 if xr > 1 else K,
+                               ids.ravel())
+        assert_close(got.reshape(T * K, nrows), ref, f"mmq_experts Q8_0 x_rows_per_tok={xr}")
+
+
 def test_mmq_dense(ops):
     T, ncols, nrows = 130, 768, 192
     rng = np.random.default_rng(3)
