@@ -61,6 +61,9 @@ inline size_t gprefix_bytes(int64_t n_expert) { return (size_t) 2 * (n_expert + 
 // histograms (LDS atomics), one prefix over (expert, wave) in that order, then each wave walks its chunk again in
 // order, ranking the lanes that share an expert by ballots on the expert id bits, and advances its own running
 // positions - two passes over the ids, four barriers.
+// Workgroup barrier for LDS data only: no global memory is produced and consumed inside the compaction kernel, so its
+// barriers need not wait for the id loads and the output stores still in flight (__syncthreads' fence would).
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *__restrict__ ids, int n, int k, int ne,
                                                                  int x_rows_per_tok, int32_t *__restrict__ ids_src1,
                                                                  int32_t *__restrict__ ids_dst, int32_t *bounds,
@@ -72,7 +75,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     for (int i = tid; i < NW * 256; i += kCompactThreads) (&wpos[0][0])[i] = 0;
     for (int i = tid; i < n_gdone; i += kCompactThreads) gdone[i] = 0;  // the next fused GEMM launch's arrivals
-    __syncthreads();
+    lds_sync();
     PF_MARK(2, 2);
     const int chunk = (n + NW * kWave - 1) / (NW * kWave) * kWave;  // pairs per wave, a multiple of 64
     const int p0 = wave * chunk, p1 = min(n, p0 + chunk);
@@ -97,7 +100,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         const int e = id_at(p);
         if (e >= 0 && e < ne) atomicAdd(&wpos[wave][e], 1);
     }
-    __syncthreads();
+    lds_sync();
     PF_MARK(2, 3);
     if (tid < ne) {
         int c = 0;
@@ -105,7 +108,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
         for (int w = 0; w < NW; ++w) c += wpos[w][tid];
         cnt[tid] = c;
     }
-    __syncthreads();
+    lds_sync();
     PF_MARK(2, 4);
     if (wave == 0) {  // exclusive prefix over <= 256 experts: 4 per lane, then a lane scan
         int v[4], g[4], g2[4], s = 0, sg = 0, sg2 = 0;
@@ -149,7 +152,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
             gprefix[2 * ne + 1] = inclg2;
         }
     }
-    __syncthreads();
+    lds_sync();
     PF_MARK(2, 5);
     if (tid < ne) {  // the expert's sorted positions, split over the waves in wave order
         int pos = cnt[tid];
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
             pos += c;
         }
     }
-    __syncthreads();
+    lds_sync();
     PF_MARK(2, 6);
     for (int it = 0, p = p0 + lane; p < p0 + chunk; ++it, p += kWave) {
         int e = -1;

@@ -82,7 +82,8 @@ void mmvq_experts(ggml_type type, const char *const *table, size_t off, int64_t 
 size_t mmq_q8_1_bytes(int64_t ncols, int64_t nrows);
 
 // dst[t][r] = (W . x[t])[r], t < n_tok; x f32 [n_tok][ncols]; xq: mmq_q8_1_bytes(ncols, n_tok) bytes of scratch.
-// Reference: include/fns/ggml_kernels.h:56-58, src/ggml/ggml_mmq.cu:80-96.
+// Types: the reference's MMQ set (src/ggml/ggml_mmq.cu:59-66: Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, IQ3_S, IQ3_XXS, IQ2_S)
+// and Q3_K. Reference: include/fns/ggml_kernels.h:56-58, src/ggml/ggml_mmq.cu:80-96.
 void mmq(ggml_type type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq,
          float *dst, hipStream_t stream);
 
