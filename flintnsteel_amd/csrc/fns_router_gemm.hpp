@@ -94,6 +94,9 @@ __device__ __forceinline__ void router_gemm_tile(const void *__restrict__ w, con
             gb0 = ldw(wo0 + k0), gb1 = ldw(wo1 + k0), gb2 = ldw(wo2 + k0), gb3 = ldw(wo3 + k0);
         }
         for (; k0 < ncols; k0 += NW * 64) {
+            // (the tile is wave-private: LDS accesses of one wave complete in order; the wave barriers keep the
+            // compiler from moving the reads of one chunk across the writes of the next)
+            __builtin_amdgcn_wave_barrier();
             *(float4 *) &xs[lr][lc] = ga0, *(float4 *) &xs[4 + lr][lc] = ga1;
             *(float4 *) &xs[8 + lr][lc] = ga2, *(float4 *) &xs[12 + lr][lc] = ga3;
             *(float4 *) &wsh[lr][lc] = gb0, *(float4 *) &wsh[4 + lr][lc] = gb1;
@@ -104,6 +107,7 @@ __device__ __forceinline__ void router_gemm_tile(const void *__restrict__ w, con
                 ga2 = *(const float4 *) (x + xo2 + kn), ga3 = *(const float4 *) (x + xo3 + kn);
                 gb0 = ldw(wo0 + kn), gb1 = ldw(wo1 + kn), gb2 = ldw(wo2 + kn), gb3 = ldw(wo3 + kn);
             }
+            __builtin_amdgcn_wave_barrier();
             float4 ca[4], cb[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {

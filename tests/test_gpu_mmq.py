@@ -387,6 +387,26 @@ def test_moe_prefill_guard_bf16_sigmoid_residual(ops):
                          "guarded bf16 sigmoid prefill", resid=host(resid))
 
 
+def test_moe_prefill_unaligned_inputs_take_the_two_launch_router(ops):
+    """x 4 bytes off a 16-byte boundary: the prefill takes the separate router GEMM (guarded loads) and activation
+    quantiser instead of the one-launch router + image kernel. Same chunk order, products and Q8_1 arithmetic, so the
+    logits, the x image and the output equal the aligned call's bit for bit."""
+    from flintnsteel_amd import synth
+    H, F, NE, K, T = 512, 256, 16, 4, 45
+    layer = synth.build_layer(H, F, NE, K, orc.Q4_K, orc.Q4_K, seed=3, layer=31)
+    pre = ops.MoePrefill(layer)
+    x = synth.activations(T, H, seed=3, layer=32)
+    xu = torch.empty(T * H + 1, device="cuda")[1:].view(T, H)
+    xu.copy_(x)
+    assert xu.data_ptr() % 16 == 4
+    wa, wu = pre.workspace(T), pre.workspace(T)
+    a, b = host(pre(x, ws=wa)), host(pre(xu, ws=wu))
+    ta, tb = pre.trace(wa, T), pre.trace(wu, T)
+    for name in ("logits", "xpack", "ids", "w"):
+        assert np.array_equal(host(ta[name]), host(tb[name])), f"{name} differs on the unaligned path"
+    assert np.array_equal(a, b), "output differs on the unaligned path"
+
+
 def _skewed_q4k_layer(ops, guard):
     from flintnsteel_amd import synth
     H, F, NE, K = 2048, 768, 128, 8
