@@ -182,3 +182,34 @@ def test_exchange_timeout_is_reported(ops, synth):
     assert layer.status(ws, clear=True) == STATUS_EXCHANGE_TIMEOUT, "sticky until cleared"
     assert layer.status(ws) == 0
     assert np.array_equal(host(layer(x_d, ws=ws)), good)
+
+
+def test_config3_stack_48_layers_chained(ops, synth):
+    """Config 3's 48-layer Q4_K / Q6_K stack as a chain at batch 1: x_{l+1} = MoE_l(x_l) + x_l (residual added by the
+    layer), every layer's inputs the previous layer's GPU output. Each layer against the oracle on the same input:
+    ids and weights bit-exact from the layer's logits, ids equal to the oracle's own routing where the 8th / 9th logit
+    margin is clear, the output within the tight bounds of the chain fed with the GPU's act; the final state finite
+    and of the magnitude of the input (no drift through the stack)."""
+    n_layers = 48
+    layers = [synth.build_layer(H, F, NE, K, 12, 14, SEED, layer=300 + l) for l in range(n_layers)]
+    x = synth.activations(1, H, SEED, layer=800)
+    clear = 0
+    for l, layer in enumerate(layers):
+        print(f"config-3 chain layer {l}", flush=True)
+        ws = layer.workspace(1)
+        out = layer(x, ws=ws, x_resid=x)
+        tr = {k: host(v) for k, v in layer.trace(ws, 1).items()}
+        xh = host(x)
+        ids_l, w_l, _, _ = orc.route_topk(tr["logits"], K, 0)
+        assert np.array_equal(tr["ids"], ids_l) and np.array_equal(tr["w"].view(np.uint32), w_l.view(np.uint32))
+        ref_logits = orc.router_f32(host(layer.router_w), xh)
+        ids_o, _, _, margin = orc.route_topk(ref_logits, K, 0)
+        if margin[0] > 2.0 * float(np.abs(tr["logits"] - ref_logits).max()) + 1e-7:
+            clear += 1
+            assert np.array_equal(tr["ids"], ids_o), f"layer {l}: ids differ from the oracle's routing"
+        _, out_ref, _ = oracle_layer(layer, xh, tr["ids"], tr["w"], tr["act"], guard=False)
+        assert_close(host(out) - xh, out_ref, f"layer {l} of the chain")
+        x = out
+    assert clear >= n_layers - 2, f"only {clear} of {n_layers} layers had a clear routing margin"
+    xf = host(x)
+    assert np.isfinite(xf).all() and 0.5 < np.abs(xf).mean() / np.abs(host(synth.activations(1, H, SEED, layer=800))).mean() < 4
