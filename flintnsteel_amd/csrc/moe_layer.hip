@@ -593,11 +593,14 @@ __global__ __launch_bounds__(NT) void k_gate_up_lds(const LayerArgs a) {
 // barrier between the weight loads and the dot products), so waves whose data lands first compute first.
 constexpr int kQThreads = 1024, kQWaves = kQThreads / kWave;
 
-template <int TQ, int NC>
-__global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
+// NTH threads, 32 gate/up rows per workgroup: LPR = NTH / 32 lanes per row, each lane 32 / LPR quarters of it (all of
+// its loads issued before the dot products). 1024 threads: one workgroup per CU; 256 threads (the verify step, whose
+// hundreds of (expert, row block) workgroups then all fit on the device at once): four per CU.
+template <int TQ, int NC, int NTH = kQThreads>
+__global__ __launch_bounds__(NTH) void k_gate_up_q(const LayerArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ RouteLds rs;
-    constexpr int BB = Traits<TQ>::bytes;
+    constexpr int BB = Traits<TQ>::bytes, NW = NTH / kWave, LPR = NTH / kGuRows;
     float *s_act = (float *) smem;  // [NC][32]
     uint8_t *s_x = smem + NC * kGuRows * 4;
     const int tid = threadIdx.x, wave = tid / kWave;
@@ -608,11 +611,13 @@ __global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
     FNS_MARK(1, wgid, 0);
 
     __shared__ const uint8_t *s_tab[256];
-    // waves 1-15: the x images and the expert table (so the slot address is an LDS read once routing is done)
-    if (wave != 0 && tid - kWave < a.NE) s_tab[tid - kWave] = gload<const uint8_t *>((const uint8_t *) (a.table + (tid - kWave)));
-    dma_waves_from<kQWaves>(s_x, a.xpack, T * xbytes, 1);
+    // waves 1..NW-1: the x images and the expert table (so the slot address is an LDS read once routing is done)
+    if (wave != 0)
+        for (int i = tid - kWave; i < a.NE; i += NTH - kWave)
+            s_tab[i] = gload<const uint8_t *>((const uint8_t *) (a.table + i));
+    dma_waves_from<NW>(s_x, a.xpack, T * xbytes, 1);
     if (wave != 0) dma_wait();
-    const int e = route_channel<kQThreads>(a, rs);  // the x images and the table are complete after its first barrier
+    const int e = route_channel<NTH>(a, rs);  // the x images and the table are complete after its first barrier
     FNS_MARK(1, wgid, 1);
     if (e < 0) return;
     const int ncol = rs.ncol;
@@ -626,32 +631,54 @@ __global__ __launch_bounds__(kQThreads) void k_gate_up_q(const LayerArgs a) {
     // weights straight from global memory (each lane reads its own quarters; staging them through LDS cost an LDS
     // footprint of 74 KB and a DMA wait per workgroup), with 16-byte loads when the blocks are 16-byte aligned
     const bool al16 = (((uintptr_t) wa | (uintptr_t) wb | (uintptr_t) BB) & 15u) == 0;
-    const int r2 = 2 * wave;  // this wave's rows r2, r2 + 1
     FNS_MARK(1, wgid, 2);
 
-    const int lane = tid % 32;
-    const int rl = r2 + (tid % kWave) / 32, row = rowb + rl;
+    const int lane = tid % LPR;
+    const int rl = tid / LPR, row = rowb + rl;
     ActImg img[NC];
 #pragma unroll
     for (int n = 0; n < NC; ++n) img[n] = act_img(s_x + (n < ncol ? rs.xrow[n] : 0) * xbytes, npad);
     float acc[NC], accg[NC];
 #pragma unroll
     for (int n = 0; n < NC; ++n) acc[n] = accg[n] = 0.0f;
-    for (int qi = lane; qi < 4 * nblk; qi += 32) {
-        const int bb = qi >> 2, qt = qi & 3;
-        const int off = rl * row_bytes + bb * BB;
-        if (al16) {
-            quarter_dot_nc<TQ, Aligned16, NC>(wa + off, img, ncol, bb, qt, acc);
-            quarter_dot_nc<TQ, Aligned16, NC>(wb + off, img, ncol, bb, qt, accg);
-        } else {
-            quarter_dot_nc<TQ, Any2, NC>(wa + off, img, ncol, bb, qt, acc);
-            quarter_dot_nc<TQ, Any2, NC>(wb + off, img, ncol, bb, qt, accg);
+    // Lane `lane` stands for the V = 32 / LPR lanes lane + LPR m of the 32-lane form and sums in its order (each
+    // virtual lane's quarters in sequence, then the xor butterfly's first steps), so the result is that form's bit for
+    // bit: the verify columns equal their batch-1 results.
+    constexpr int V = kGuRows * 32 / NTH;
+    static_assert(V == 1 || V == 4, "1024 or 256 threads");
+    float vu[V][NC], vg[V][NC];
+#pragma unroll
+    for (int m = 0; m < V; ++m)
+#pragma unroll
+        for (int n = 0; n < NC; ++n) vu[m][n] = vg[m][n] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < V; ++m) {
+        for (int qi = lane + LPR * m; qi < 4 * nblk; qi += 32) {
+            const int bb = qi >> 2, qt = qi & 3;
+            const int off = rl * row_bytes + bb * BB;
+            if (al16) {
+                quarter_dot_nc<TQ, Aligned16, NC>(wa + off, img, ncol, bb, qt, vu[m]);
+                quarter_dot_nc<TQ, Aligned16, NC>(wb + off, img, ncol, bb, qt, vg[m]);
+            } else {
+                quarter_dot_nc<TQ, Any2, NC>(wa + off, img, ncol, bb, qt, vu[m]);
+                quarter_dot_nc<TQ, Any2, NC>(wb + off, img, ncol, bb, qt, vg[m]);
+            }
         }
     }
-    gate_up_epilogue<32, NC>(a, rs, s_act, kGuRows, rl, row, lane, acc, accg);
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+        if constexpr (V == 1) {
+            acc[n] = vu[0][n];
+            accg[n] = vg[0][n];
+        } else {
+            acc[n] = (vu[0][n] + vu[2][n]) + (vu[1][n] + vu[3][n]);
+            accg[n] = (vg[0][n] + vg[2][n]) + (vg[1][n] + vg[3][n]);
+        }
+    }
+    gate_up_epilogue<LPR, NC>(a, rs, s_act, kGuRows, rl, row, lane, acc, accg);
     __syncthreads();
     FNS_MARK(1, wgid, 3);
-    quant_act<kQThreads>(a, rs, s_act, kGuRows, rowb);
+    quant_act<NTH>(a, rs, s_act, kGuRows, rowb);
     FNS_MARK(1, wgid, 4);
 }
 
@@ -946,19 +973,31 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
     for (int c = 0; c < CH; ++c) mis |= (uintptr_t) s_dp[c];
     const bool al16 = (mis & 15u) == 0;
     const int sub = lane64 / 16, lane = tid % 16;
-    for (int g = wave; g < 2 * CH; g += kQWaves) {
-        const int ch = g >> 1, rb = 4 * (g & 1);  // rows rb .. rb + 3 of the workgroup's eight
-        const ActImg img = act_img(smem + (size_t) ch * fbytes, fpad);
-        const int rr = rb + sub;
-        const uint8_t *wr = s_dp[ch] + rr * row_bytes;
-        float acc = 0.0f;
-        for (int qi = lane; qi < 4 * nblk; qi += 16) {
-            const int bb = qi >> 2, qt = qi & 3;
-            if (al16) acc += quarter_dot<TQ, Aligned16>(wr + bb * BB, img, bb, qt);
-            else acc += quarter_dot<TQ, Any2>(wr + bb * BB, img, bb, qt);
+    // A wave's (channel, 4-row) groups in batches of kDnBatch, each group as before (its quarters in sequence, then
+    // the 16-lane butterfly): the batch's weight loads are all in flight before its first dot product. Groups past
+    // the last one repeat a valid group (clamped; their results are dropped).
+    constexpr int kDnBatch = 4;
+    for (int g0 = wave; g0 < 2 * CH; g0 += kDnBatch * kQWaves) {
+        float acc[kDnBatch];
+#pragma unroll
+        for (int u = 0; u < kDnBatch; ++u) {
+            const int g = min(g0 + u * kQWaves, 2 * CH - 1);
+            const int ch = g >> 1, rr = 4 * (g & 1) + sub;  // rows 4 (g & 1) .. + 3 of the workgroup's eight
+            const ActImg img = act_img(smem + (size_t) ch * fbytes, fpad);
+            const uint8_t *wr = s_dp[ch] + rr * row_bytes;
+            acc[u] = 0.0f;
+            for (int qi = lane; qi < 4 * nblk; qi += 16) {
+                const int bb = qi >> 2, qt = qi & 3;
+                if (al16) acc[u] += quarter_dot<TQ, Aligned16>(wr + bb * BB, img, bb, qt);
+                else acc[u] += quarter_dot<TQ, Any2>(wr + bb * BB, img, bb, qt);
+            }
         }
-        acc = lanes_sum<16>(acc);
-        if (lane == 0) s_dexp[ch][rr] = acc;
+#pragma unroll
+        for (int u = 0; u < kDnBatch; ++u) {
+            const int g = g0 + u * kQWaves;
+            const float v = lanes_sum<16>(acc[u]);
+            if (g < 2 * CH && lane == 0) s_dexp[g >> 1][4 * (g & 1) + sub] = v;
+        }
     }
     __syncthreads();
     FNS_MARK(2, blockIdx.x, 3);
@@ -1329,7 +1368,7 @@ template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
             hipLaunchKernelGGL((k_gate_up_q<TQ, 1>), grid, dim3(kQThreads),
                                gate_up_q_lds_bytes(1, a.H, Traits<TQ>::bytes, 1), st, a);
         else
-            hipLaunchKernelGGL((k_gate_up_q<TQ, kMaxTok>), grid, dim3(kQThreads),
+            hipLaunchKernelGGL((k_gate_up_q<TQ, kMaxTok, 256>), grid, dim3(256),
                                gate_up_q_lds_bytes(a.T, a.H, Traits<TQ>::bytes, kMaxTok), st, a);
         return host::check_launch("moe gate_up (quarters)");
     }
