@@ -90,16 +90,13 @@ __device__ __forceinline__ void dma_waves_from(uint8_t *dst, const uint8_t *src,
 // s_waitcnt vmcnt(0) (gfx9 encoding: expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// 16 bytes at a 2-byte-aligned address (LDS, or global through a generic pointer): aligned dwords joined with funnel
-// shifts; the fifth dword is read only when the address is not 4-byte aligned, so nothing past the 16 bytes' last
-// dword is touched.
+// 16 bytes at a 2-byte-aligned address (LDS, or global through a generic pointer): one unaligned 16-byte load
+// (gfx950 runs with unaligned LDS and global access enabled, and the compiler emits ds_read_b128 / flat_load_dwordx4
+// for it); nothing outside the 16 bytes is touched.
 __device__ __forceinline__ uint4 lds16u(const uint8_t *p) {
-    const uintptr_t a = (uintptr_t) p;
-    const uint32_t *w = (const uint32_t *) (a & ~(uintptr_t) 3);
-    const uint32_t sh = (uint32_t) (a & 3u) * 8u;
-    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = sh ? w[4] : 0u;
-    return make_uint4(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh),
-                      __builtin_amdgcn_alignbit(w3, w2, sh), __builtin_amdgcn_alignbit(w4, w3, sh));
+    uint4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 16);
+    return v;
 }
 
 // Whole block from LDS (Q4_K / Q5_K blocks sit at 16-byte-aligned offsets of a staged region; Q6_K / Q3_K at 2-byte).

@@ -26,11 +26,9 @@ struct Any2 {
 };
 // 4 bytes at a 2-byte-aligned address.
 __device__ __forceinline__ uint32_t ld32u(const uint8_t *p) {
-    const uintptr_t a = (uintptr_t) p;
-    const uint32_t *w = (const uint32_t *) (a & ~(uintptr_t) 3);
-    const uint32_t sh = (uint32_t) (a & 3u) * 8u;
-    const uint32_t w0 = w[0], w1 = sh ? w[1] : 0u;
-    return __builtin_amdgcn_alignbit(w1, w0, sh);
+    uint32_t v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 4);
+    return v;
 }
 
 // The activation side of one quarter (64 consecutive columns of block bb, quarter qt) in registers: the 64 int8 values
