@@ -1117,10 +1117,19 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok], sh_grp[4];
     const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp, sh_grid};
     const int lid = blockIdx.x, r = lid / kXcds;
-    const int g = (r / a.n_cb) * kXcds + lid % kXcds, wb = r % a.n_cb;
-    if (g >= a.n_groups) return;
-    if (g < a.n_main) mmq_group<T, GLU, 2, false>(a, g, wb, L);
-    else mmq_group<T, GLU, 1, false>(a, g - a.n_main, wb, L);
+    int j = (r / a.n_cb) * kXcds + lid % kXcds;
+    const int wb = r % a.n_cb;
+    if (a.bounds) {
+        // expert path: the groups that exist in this call (the device-side counts of the 64-row list and of the
+        // remainder list) take the first workgroups; the rest of the grid (sized for the upper bound) returns at once
+        const int nm = a.gprefix[a.n_expert], nr = a.gprefix[2 * (a.n_expert + 1) - 1];
+        if (j >= nm + nr) return;
+        if (j < nm) mmq_group<T, GLU, 2, false>(a, j, wb, L);
+        else mmq_group<T, GLU, 1, false>(a, j - nm, wb, L);
+        return;
+    }
+    if (j >= a.n_groups) return;
+    mmq_group<T, GLU, 2, false>(a, j, wb, L);
 }
 
 // Gate/up (with SwiGLU and the Q8_1 of act) and down of the expert path in one launch. The gate/up items come first,
@@ -1152,13 +1161,18 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
     __shared__ int sh_src[kMmqTok], sh_dst[kMmqTok], sh_grp[4];
     const MmqLds L{sh_a0, sh_a1, *(uint8_t (*)[kMmqTok * kRowS]) sh_s, sh_src, sh_dst, sh_grp, nullptr};
     PF_MARK(3, 0);
-    const int total = m.n_main + m.n_expert;
-    const int items_gu = m.n_cb_gu * kXcds * ((total + kXcds - 1) / kXcds);  // a multiple of kXcds
+    // The groups that exist in this call (the device-side counts of the two lists: the 64-row groups, then the <= 32-row
+    // remainders) are numbered j = 0 .. R - 1 and take the first workgroups of the grid; the workgroups past them (the
+    // grid is sized for the upper bound) return at once, after every real item has been dispatched.
+    const int nm = m.gprefix[m.n_expert], nr = m.gprefix[2 * (m.n_expert + 1) - 1];
+    const int R = nm + nr, rounds = (R + kXcds - 1) / kXcds;
+    const int items_gu = m.n_cb_gu * kXcds * rounds;  // a multiple of kXcds
     const bool is_gu = (int) blockIdx.x < items_gu;
     const int cb = is_gu ? m.n_cb_gu : m.n_cb_dn;
     const int lid = is_gu ? (int) blockIdx.x : (int) blockIdx.x - items_gu, r = lid / kXcds;
-    const int g = (r / cb) * kXcds + lid % kXcds, wb = r % cb;
-    if (g >= total) return;
+    const int j = (r / cb) * kXcds + lid % kXcds, wb = r % cb;
+    if (j >= R) return;
+    const int g = j < nm ? j : m.n_main + (j - nm);
     MmqArgs a{};
     a.table = m.table;
     a.n_expert = m.n_expert;
@@ -1210,15 +1224,17 @@ template <bool GLU> const void *mmq_kernel(int type) {
     return nullptr;
 }
 
-// groups: upper bound of the 64-row list (its workgroups return past the device-side count); expert path: then the
-// <= 32-row remainders (at most one per expert), with the second prefix list
+// groups: upper bound of the 64-row list; expert path: of the 64-row list and the <= 32-row remainders together (the
+// workgroups past the device-side counts return at once)
 int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st) {
     const void *fn = glu ? mmq_kernel<true>(type) : mmq_kernel<false>(type);
     if (!fn) return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
     if (groups <= 0) return host::OK;
     MmqArgs arg = a;
     arg.n_main = groups;
-    const int total = groups + (a.bounds ? a.n_expert : 0);
+    // expert path: n_expert + ceil(pairs / 64) (the 64-row list's bound) bounds both lists together, as expert e
+    // has ceil(n_e / 64) groups in all
+    const int total = groups;
     void *args[] = {&arg};
     const int rows = glu ? 128 : 256;  // weight rows per workgroup
     arg.n_groups = total;
@@ -1255,7 +1271,8 @@ int launch_mmq_moe(int tgu, int tdn, MoeArgs m, hipStream_t st) {
     m.n_cb_gu = (m.inter + 127) / 128;
     m.n_cb_dn = (m.hidden + 255) / 256;
     m.gwait += m.n_cb_gu;
-    const int64_t total = m.n_main + m.n_expert;
+    // n_main = n_expert + ceil(pairs / 64) bounds both lists together: expert e has ceil(n_e / 64) groups in all
+    const int64_t total = m.n_main;
     const int64_t items = (int64_t) (m.n_cb_gu + m.n_cb_dn) * kXcds * ((total + kXcds - 1) / kXcds);
     if (items > INT32_MAX) return host::set_error(host::ERR_SHAPE, "mmq: grid too large");
     void *args[] = {&m};
