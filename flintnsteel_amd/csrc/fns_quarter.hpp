@@ -24,6 +24,13 @@ struct Aligned16 {
 struct Any2 {
     static __device__ __forceinline__ uint4 ld(const uint8_t *p) { return lds16u(p); }
 };
+// Padded: blocks staged in LDS at a 16-byte-aligned stride (kStageBytes), each block's last 16-byte piece holding the
+// block's last 16 bytes (so no piece reads past the block); for Q4_K / Q5_K / Q8_0 / IQ types the same as Aligned16
+// (their staged layout is the verbatim one).
+struct Padded {
+    static __device__ __forceinline__ uint4 ld(const uint8_t *p) { return *(const uint4 *) p; }
+};
+template <int T> constexpr int kStageBytes = T == T_Q6_K ? 224 : T == T_Q3_K ? 112 : Traits<T>::bytes;
 // 4 bytes at a 2-byte-aligned address.
 __device__ __forceinline__ uint32_t ld32u(const uint8_t *p) {
     uint32_t v;
@@ -101,6 +108,9 @@ template <> __device__ __forceinline__ float quarter_dot_r<T_Q4_K, Aligned16>(co
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q4_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
     return q4k_quarter<Any2>(blk, x, qt);
 }
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q4_K, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q4k_quarter<Aligned16>(blk, x, qt);
+}
 
 template <class L> __device__ __forceinline__ float q5k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
     const uint4 h = L::ld(blk);
@@ -125,15 +135,20 @@ template <> __device__ __forceinline__ float quarter_dot_r<T_Q5_K, Aligned16>(co
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q5_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
     return q5k_quarter<Any2>(blk, x, qt);
 }
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q5_K, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q5k_quarter<Aligned16>(blk, x, qt);
+}
 
 // Q6_K and Q3_K blocks are only 2-byte aligned: both policies read through Any2.
-__device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+// PAD: the block is staged at a 16-byte-aligned address with its last piece (bytes 194 .. 209) at offset 208.
+template <bool PAD = false> __device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
     const int n = qt >> 1, hh = qt & 1;
-    const uint4 A0 = lds16u(blk + 64 * n), A1 = lds16u(blk + 64 * n + 16);       // ql[64n .. 64n+31]
-    const uint4 B0 = lds16u(blk + 64 * n + 32), B1 = lds16u(blk + 64 * n + 48);  // ql[64n+32 .. 64n+63]
-    const uint4 Q0 = lds16u(blk + 128 + 32 * n), Q1 = lds16u(blk + 144 + 32 * n);  // qh[32n .. 32n+31]
-    const uint32_t scw = ld32u(blk + 192 + 4 * qt);  // int8 scales of groups 4qt .. 4qt+3
-    const uint32_t dbits = ld32u(blk + 208) & 0xffffu;
+    auto ld = [&](int o) { return PAD ? *(const uint4 *) (blk + o) : lds16u(blk + o); };
+    const uint4 A0 = ld(64 * n), A1 = ld(64 * n + 16);       // ql[64n .. 64n+31]
+    const uint4 B0 = ld(64 * n + 32), B1 = ld(64 * n + 48);  // ql[64n+32 .. 64n+63]
+    const uint4 Q0 = ld(128 + 32 * n), Q1 = ld(144 + 32 * n);  // qh[32n .. 32n+31]
+    const uint32_t scw = PAD ? *(const uint32_t *) (blk + 192 + 4 * qt) : ld32u(blk + 192 + 4 * qt);  // int8 scales of groups 4qt .. 4qt+3
+    const uint32_t dbits = PAD ? *(const uint32_t *) (blk + 220) >> 16 : ld32u(blk + 208) & 0xffffu;
     const uint32_t A[8] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w};
     const uint32_t B[8] = {B0.x, B0.y, B0.z, B0.w, B1.x, B1.y, B1.z, B1.w};
     const uint32_t Q[8] = {Q0.x, Q0.y, Q0.z, Q0.w, Q1.x, Q1.y, Q1.z, Q1.w};
@@ -158,12 +173,17 @@ template <> __device__ __forceinline__ float quarter_dot_r<T_Q6_K, Aligned16>(co
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q6_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
     return q6k_quarter(blk, x, qt);
 }
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q6_K, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q6k_quarter<true>(blk, x, qt);
+}
 
-__device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+// PAD: the block is staged at a 16-byte-aligned address with its last piece (bytes 94 .. 109) at offset 96.
+template <bool PAD = false> __device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
     const int n = qt >> 1, hh = qt & 1;
-    const uint4 H0 = lds16u(blk), H1 = lds16u(blk + 16);                          // hmask[0 .. 31]
-    const uint4 q0 = lds16u(blk + 32 + 32 * n), q1 = lds16u(blk + 48 + 32 * n);  // qs[32n .. 32n+31]
-    const uint4 t = lds16u(blk + 94);                                             // scales at +2, d at +14
+    auto ld = [&](int o) { return PAD ? *(const uint4 *) (blk + o) : lds16u(blk + o); };
+    const uint4 H0 = ld(0), H1 = ld(16);                          // hmask[0 .. 31]
+    const uint4 q0 = ld(32 + 32 * n), q1 = ld(48 + 32 * n);  // qs[32n .. 32n+31]
+    const uint4 t = ld(PAD ? 96 : 94);                            // scales at +2, d at +14
     const uint32_t HM[8] = {H0.x, H0.y, H0.z, H0.w, H1.x, H1.y, H1.z, H1.w};
     const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     const uint32_t S0 = __builtin_amdgcn_alignbit(t.y, t.x, 16), S1 = __builtin_amdgcn_alignbit(t.z, t.y, 16);
@@ -195,6 +215,9 @@ template <> __device__ __forceinline__ float quarter_dot_r<T_Q3_K, Aligned16>(co
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q3_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
     return q3k_quarter(blk, x, qt);
 }
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q3_K, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q3k_quarter<true>(blk, x, qt);
+}
 
 // Q8_0 quarter qt = blocks 2qt and 2qt+1 of the 8-block unit (68 bytes at offset 68 qt, 2-byte aligned at least):
 // sum over the two blocks of (d_w * d8) * (q_w . a), the block product of ggml vec_dot_q8_0_q8_1.
@@ -216,6 +239,9 @@ template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Aligned16>(co
     return q80_quarter(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
+    return q80_quarter(blk, x, qt);
+}
+template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
     return q80_quarter(blk, x, qt);
 }
 
@@ -352,6 +378,9 @@ __device__ __forceinline__ float iq2s_quarter(const uint8_t *blk, const ActQ &x,
         return F(blk, x, qt);                                                                                        \
     }                                                                                                                \
     template <> __device__ __forceinline__ float quarter_dot_r<T, Any2>(const uint8_t *blk, const ActQ &x, int qt) {     \
+        return F(blk, x, qt);                                                                                        \
+    }                                                                                                                \
+    template <> __device__ __forceinline__ float quarter_dot_r<T, Padded>(const uint8_t *blk, const ActQ &x, int qt) {   \
         return F(blk, x, qt);                                                                                        \
     }
 FNS_IQ_QUARTER(T_IQ4_XS, iq4xs_quarter)

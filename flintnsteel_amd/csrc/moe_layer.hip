@@ -1035,6 +1035,29 @@ __device__ __forceinline__ void store_dev(uint32_t *p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// One wave's LDS-DMA of blocks [b0, b1) of consecutive type-T blocks at src into LDS at dst with the staged stride
+// kStageBytes<T>: verbatim when that is the block size; otherwise piece k of a block copies bytes 16 k .. 16 k + 15 and
+// its last piece the block's last 16 bytes, so every piece lies inside its block.
+template <int T>
+__device__ __forceinline__ void dma_blocks(uint8_t *dst, const uint8_t *src, int b0, int b1) {
+    constexpr int BB = Traits<T>::bytes, SB = kStageBytes<T>;
+    if constexpr (SB == BB) {
+        dma_wave(dst, src, b0 * BB, b1 * BB);
+    } else {
+        constexpr int NP = SB / 16;
+        const int lane = threadIdx.x % kWave;
+        for (int p0 = b0 * NP; p0 < b1 * NP; p0 += kWave) {
+            const int p = p0 + lane;
+            if (p < b1 * NP) {
+                const int i = p / NP, k = p % NP;
+                const uint8_t *g = src + i * BB + (k < NP - 1 ? 16 * k : BB - 16);
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *) g,
+                                                 (__attribute__((address_space(3))) void *) (dst + 16 * p0), 16, 0, 0);
+            }
+        }
+    }
+}
+
 template <int TGU, int TDN, bool SH>
 __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1061,7 +1084,10 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     const int c = shared_p ? K : blockIdx.x / upc;
     const int u = shared_p ? blockIdx.x - K * upc : blockIdx.x % upc;  // meaningful for producers
     const int r0 = blockIdx.x * kFusedRows;
-    const int gu_region = kGuRows * rbg, dn_region = kFusedRows * rbd, dn_region_s = kFusedRows * rbd_s;
+    // LDS images of the weight rows: blocks at the staged stride (Q6_K / Q3_K padded to 16-byte multiples)
+    constexpr int SG = kStageBytes<TGU>, SD = kStageBytes<TDN>;
+    const int lrbg = nbg * SG, lrbd = nbd * SD, lrbd_s = nbd_s * SD;
+    const int gu_region = kGuRows * lrbg, dn_region = kFusedRows * lrbd;
     uint8_t *s_x = smem;
     uint8_t *s_a = s_x + xbytes;         // [K] act images, then the shared expert's
     uint8_t *s_gu = s_a + K * fbytes + fsbytes;  // [32 up rows | 32 gate rows]
@@ -1096,24 +1122,24 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     const bool staged = (mis & 15u) == 0;
     // down: wave w takes pieces [w * dn_piece, (w + 1) * dn_piece) of the flattened [K][dn_region] image
     auto dma_down = [&]() {
-        const int dn_total = K * dn_region, dn_piece = ((dn_total + kQWaves * 16 - 1) / (kQWaves * 16)) * 16;
-        const int p_lo = wave * dn_piece, p_hi = min(dn_total, p_lo + dn_piece);
-        for (int j = p_lo / dn_region; j < K && j * dn_region < p_hi; ++j) {
-            const int lo = max(p_lo - j * dn_region, 0), hi = min(p_hi - j * dn_region, dn_region);
-            dma_wave(s_dn + j * dn_region, s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd, lo, hi);
+        const int per = kFusedRows * nbd, total = K * per;  // blocks of the [K][8 rows] image
+        const int bp = (total + kQWaves - 1) / kQWaves, b_lo = wave * bp, b_hi = min(total, b_lo + bp);
+        for (int j = b_lo / per; j < K && j * per < b_hi; ++j) {
+            const int lo = max(b_lo - j * per, 0), hi = min(b_hi - j * per, per);
+            dma_blocks<TDN>(s_dn + j * dn_region, s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd, lo, hi);
         }
         if (SH) {  // the shared expert's rows, split over the waves the same way
-            const int sp = ((dn_region_s + kQWaves * 16 - 1) / (kQWaves * 16)) * 16;
-            dma_wave(s_dn + K * dn_region, a.shd + (int64_t) r0 * rbd_s, min(wave * sp, dn_region_s),
-                     min((wave + 1) * sp, dn_region_s));
+            const int ps = kFusedRows * nbd_s, sp = (ps + kQWaves - 1) / kQWaves;
+            dma_blocks<TDN>(s_dn + K * dn_region, a.shd + (int64_t) r0 * rbd_s, min(wave * sp, ps),
+                            min((wave + 1) * sp, ps));
         }
     };
     // Producers fetch their gate/up rows first and their down rows only once those are consumed: the gate/up bytes,
     // which the critical path waits for, then get the HBM to themselves, and the down bytes land during the exchange.
     if (staged) {
         if (producer) {
-            dma_wave(s_gu, wa, 2 * wave * rbg, (2 * wave + 2) * rbg);
-            dma_wave(s_gu + gu_region, wb, 2 * wave * rbg, (2 * wave + 2) * rbg);
+            dma_blocks<TGU>(s_gu, wa, 2 * wave * nbg, (2 * wave + 2) * nbg);
+            dma_blocks<TGU>(s_gu + gu_region, wb, 2 * wave * nbg, (2 * wave + 2) * nbg);
         } else {
             dma_down();
         }
@@ -1128,11 +1154,11 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         float acc = 0.0f, accg = 0.0f;
         for (int qi = lane; qi < 4 * nbg; qi += 32) {
             const int bb = qi >> 2, qt = qi & 3;
-            const int off = rl * rbg + bb * BG;
+            const int off = rl * rbg + bb * BG, loff = rl * lrbg + bb * SG;
             const ActQ xq = act_q(img, bb, qt);  // shared by the gate and the up row
             if (staged) {
-                acc += quarter_dot_r<TGU, Aligned16>(s_gu + off, xq, qt);
-                accg += quarter_dot_r<TGU, Aligned16>(s_gu + gu_region + off, xq, qt);
+                acc += quarter_dot_r<TGU, Padded>(s_gu + loff, xq, qt);
+                accg += quarter_dot_r<TGU, Padded>(s_gu + gu_region + loff, xq, qt);
             } else {
                 acc += quarter_dot_r<TGU, Any2>(wa + off, xq, qt);
                 accg += quarter_dot_r<TGU, Any2>(wb + off, xq, qt);
@@ -1256,12 +1282,12 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         const int ch = it / kFusedRows, rr = it % kFusedRows;
         const bool shc = SH && ch == K;  // the shared expert's rows
         const ActImg img = act_img(s_a + ch * fbytes, shc ? fspad : fpad);
-        const int nb_c = shc ? nbd_s : nbd, rb_c = shc ? rbd_s : rbd;
+        const int nb_c = shc ? nbd_s : nbd, rb_c = shc ? rbd_s : rbd, lrb_c = shc ? lrbd_s : lrbd;
         const uint8_t *gsrc = (shc ? a.shd : s_tab[rs.sel[ch]] + a.down_off) + (int64_t) (r0 + rr) * rb_c;
         float acc = 0.0f;
         for (int qi = lane16; qi < 4 * nb_c; qi += 16) {
             const int bb = qi >> 2, qt = qi & 3;
-            if (staged) acc += quarter_dot<TDN, Aligned16>(s_dn + ch * dn_region + rr * rb_c + bb * BD, img, bb, qt);
+            if (staged) acc += quarter_dot<TDN, Padded>(s_dn + ch * dn_region + rr * lrb_c + bb * SD, img, bb, qt);
             else acc += quarter_dot<TDN, Any2>(gsrc + bb * BD, img, bb, qt);
         }
         acc = lanes_sum<16>(acc);
@@ -1284,6 +1310,8 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
 
 // Fused-kernel plan for one layer shape (n_tok = 1): LDS bytes, or 0 when the shape does not fit the scheme.
 // Fs > 0: with the shared expert (width Fs, the routed types) as slot K.
+// Bytes per block of the fused kernel's LDS weight images (kStageBytes of the type).
+inline int stage_bytes_of(int t) { return t == T_Q6_K ? kStageBytes<T_Q6_K> : t == T_Q3_K ? kStageBytes<T_Q3_K> : block_bytes(t); }
 inline size_t fused_lds(int H, int F, int K, int BG, int BD, int Fs = 0) {
     // every producer is a workgroup
     if (F % kGuRows || (int64_t) K * (F / kGuRows) + Fs / kGuRows > H / kFusedRows) return 0;
@@ -1500,13 +1528,13 @@ int resident_groups(const void *fn, size_t lds) {
 // True when this call (n_tok = 1, a shape that fits) takes the fused kernel.
 bool use_fused(const FnsMoeLayer *L, const LayerArgs &a) {
     if (!a.fused) return false;
-    const size_t lds = fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type), a.shd ? a.Fs : 0);
+    const size_t lds = fused_lds(a.H, a.F, a.K, stage_bytes_of(L->gu_type), stage_bytes_of(L->down_type), a.shd ? a.Fs : 0);
     const void *fn = fused_kernel(L->gu_type, L->down_type, a.shd != nullptr);
     return fn && resident_groups(fn, lds) >= a.H / kFusedRows;
 }
 
 int launch_fused(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t st) {
-    const size_t lds = fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type), a.shd ? a.Fs : 0);
+    const size_t lds = fused_lds(a.H, a.F, a.K, stage_bytes_of(L->gu_type), stage_bytes_of(L->down_type), a.shd ? a.Fs : 0);
     LayerArgs arg = a;
     void *args[] = {&arg};
     const hipError_t e = hipLaunchKernel(fused_kernel(L->gu_type, L->down_type, a.shd != nullptr),
@@ -1687,11 +1715,11 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     const bool sh_same = L->shexp_inter > 0 && (!L->shexp_gu_type || L->shexp_gu_type == L->gu_type) &&
                          (!L->shexp_down_type || L->shexp_down_type == L->down_type);
     const int fs_fused = n_tok == 1 && sh_same &&
-                                 fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type),
+                                 fused_lds(a.H, a.F, a.K, stage_bytes_of(L->gu_type), stage_bytes_of(L->down_type),
                                            L->shexp_inter) > 0
                              ? L->shexp_inter
                              : 0;
-    a.fused = n_tok == 1 && fused_lds(a.H, a.F, a.K, block_bytes(L->gu_type), block_bytes(L->down_type),
+    a.fused = n_tok == 1 && fused_lds(a.H, a.F, a.K, stage_bytes_of(L->gu_type), stage_bytes_of(L->down_type),
                                       L->shexp_inter > 0 ? fs_fused : 0) > 0 &&
               (L->shexp_inter == 0 || fs_fused > 0);
     a.x_in = x;
