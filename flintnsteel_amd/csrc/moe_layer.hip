@@ -1244,15 +1244,23 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
             __builtin_amdgcn_global_load_lds(
                 (const __attribute__((address_space(1))) void *) (a.apack + p + lane64 * 16),
                 (__attribute__((address_space(3))) void *) (s_a + p), 16, 0, kCpolDevice);
+    // with the guard, the block maxima [K][fpad / 32] come along in the same wait, into the gate/up rows' LDS (consumed)
+    float *s_bamax = (float *) s_gu;
+    if (a.guard) {
+        const int mbytes = K * fpad / 8;
+        for (int p = wave * 1024; p < mbytes; p += kQThreads * 16)
+            if (p + lane64 * 16 < mbytes)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *) ((const uint8_t *) a.blk_amax + p + lane64 * 16),
+                    (__attribute__((address_space(3))) void *) ((uint8_t *) s_bamax + p), 16, 0, kCpolDevice);
+    }
     dma_wait();
     __syncthreads();
     FNS_MARK(1, blockIdx.x, 9);
     if (a.guard) {
         for (int ch = wave; ch < K; ch += kQWaves) {
             float m = 0.0f;
-            for (int bl = lane64; bl < fpad / 32; bl += kWave)
-                m = fmaxf(m, __hip_atomic_load(a.blk_amax + (size_t) ch * (fpad / 32) + bl, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT));
+            for (int bl = lane64; bl < fpad / 32; bl += kWave) m = fmaxf(m, s_bamax[ch * (fpad / 32) + bl]);
             m = lanes_max<64>(m);
             const float esc = guard_scale(m);
             if (lane64 == 0) {
@@ -1316,6 +1324,8 @@ inline size_t fused_lds(int H, int F, int K, int BG, int BD, int Fs = 0) {
     // every producer is a workgroup
     if (F % kGuRows || (int64_t) K * (F / kGuRows) + Fs / kGuRows > H / kFusedRows) return 0;
     if (K + (Fs > 0 ? 1 : 0) > 16) return 0;
+    // the guard's block maxima are staged where the gate/up rows were
+    if ((size_t) K * host::pad512(F) / 8 > 2 * (size_t) kGuRows * (H / 256) * BG) return 0;
     size_t lds = (size_t) img_bytes((int) host::pad512(H)) + (size_t) K * img_bytes((int) host::pad512(F)) +
                  2 * (size_t) kGuRows * (H / 256) * BG + (size_t) K * kFusedRows * (F / 256) * BD + 48;
     if (Fs > 0) lds += (size_t) img_bytes((int) host::pad512(Fs)) + (size_t) kFusedRows * (Fs / 256) * BD;
