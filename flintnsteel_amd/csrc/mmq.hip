@@ -1107,6 +1107,7 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
 // workgroup L runs on XCD L % 8 (the hardware's round-robin dispatch), and the n_cb weight row blocks of a group are
 // consecutive items of one XCD, so the group's activation rows are fetched into that XCD's L2 once, not once per
 // row block; groups go to the XCDs in turn (group u on XCD u % 8) in increasing order.
+// (SPX mode: one partition of all 8 XCDs. In a partitioned mode the mapping is a performance assumption only.)
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 template <int T, bool GLU>
 __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 4))) void k_mmq(const MmqArgs a) {
