@@ -1,20 +1,20 @@
-// moe_layer.hip - the fused MoE FFN decode / speculative-verify layer for MI355X gfx950: three kernels per layer.
+// moe_layer.hip - the MoE FFN decode / speculative-verify layer for MI355X gfx950.
 //
-//   K1 k_route_quant : router logits (one workgroup per expert row, fp32 or bf16 weights) and Q8_1 of the token rows
-//                      (the reference's 36-byte blocks, plus an unpacked copy laid out exactly as the LDS image the
-//                      GEMV kernels read, so they stage it with plain 16-byte copies).
-//   K2 k_gate_up     : every workgroup runs gating + top-k for the n_tok tokens on one wave (~1 us of ALU; cheaper
-//                      than publishing the result through a grid barrier), compacts the selected experts (distinct ids
-//                      ascending for n_tok > 1, slot order for n_tok = 1), computes act = up . x * silu(gate . x) for
-//                      32 consecutive rows of one expert for every token routed to it (each expert's weights are read
-//                      once per call), and quantises those 32 rows - one Q8_1 block per (token, slot) - for the down
-//                      projection.
-//   K3 k_down_combine: reads the selected experts' down pointers, issues its weight loads, stages the Q8_1 act rows,
-//                      applies the F16 guard when enabled (re-quantising a row only when its scale is not 1), computes
-//                      its 8 output rows of down_e . act for every (token, slot) and combines them in slot order
-//                      (reference src/kernels.cu:579-586).
-// A kernel boundary inside a HIP graph costs less on this GPU than a software grid barrier across 256 CUs (measured),
-// so the layer's two global dependencies (all logits -> routing, all act rows -> down) are kernel boundaries.
+// One token (n_tok = 1), two kernels per layer:
+//   k_route_quant  : router logits (one workgroup per expert row, fp32 or bf16 weights) and Q8_1 of x (the reference's
+//                    36-byte blocks, plus an unpacked copy laid out as the LDS image the GEMV code reads); zeroes the
+//                    fused kernel's arrival counters.
+//   k_layer_fused  : one workgroup per 8 output rows, all resident at once: every workgroup ranks the top-k itself,
+//                    producers compute act = up . x * silu(gate . x) for 32 rows of one slot and publish its Q8_1
+//                    block, a two-level arrival count releases every workgroup, which then applies the F16 guard,
+//                    computes its 8 rows of down_e . act for every slot and combines them in slot order (reference
+//                    src/kernels.cu:579-586). The kernel boundary before it is the logits exchange; the software
+//                    exchange inside it replaces a second boundary (measured faster than three kernels).
+// Several tokens (the speculative verify, n_tok <= 4), or a shape the fused kernel cannot hold, three kernels:
+//   k_route_quant  : as above; for n_tok > 1 its last workgroup routes every token once and builds the channel table
+//                    (distinct experts ascending, each with its (token, slot) columns).
+//   k_gate_up_q    : act rows and their Q8_1 blocks for every channel (each distinct expert's weights read once).
+//   k_down_q       : the down rows of every (token, slot), the F16 guard, the combine in slot order.
 //
 // Caller contract: the MoE section of the reference's Engine::ffn_block (src/engine.cu:655-696) - router, route_topk,
 // mmvq_experts_swiglu, amax_guard_q8_1, mmvq_experts, moe_combine - in one call. Per-(token, row) arithmetic does not
