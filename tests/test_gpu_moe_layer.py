@@ -72,6 +72,7 @@ CASES = {
     "cfg0_q4k": (12, 12, 0),   # gate/up Q4_K, down Q4_K, softmax
     "cfg1_q3k_q5k": (11, 13, 0),
     "cfg3_q4k_q6k": (12, 14, 0),
+    "q6k_q3k": (14, 11, 0),    # both staged at the padded LDS stride on the other side (gate/up Q6_K, down Q3_K)
     "flint_sigmoid": (12, 14, 1),
     "q8_0": (8, 8, 0),         # the reference's dense / Q8_0 expert type (src/ggml/ggml_mmvq.cu:377,405)
 }
