@@ -1260,7 +1260,8 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     if (a.guard) {
         for (int ch = wave; ch < K; ch += kQWaves) {
             float m = 0.0f;
-            for (int bl = lane64; bl < fpad / 32; bl += kWave) m = fmaxf(m, s_bamax[ch * (fpad / 32) + bl]);
+            // (the F / 32 blocks the producers wrote: the padding blocks of act are zeros and never stored here)
+            for (int bl = lane64; bl < F / 32; bl += kWave) m = fmaxf(m, s_bamax[ch * (fpad / 32) + bl]);
             m = lanes_max<64>(m);
             const float esc = guard_scale(m);
             if (lane64 == 0) {

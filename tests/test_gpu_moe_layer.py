@@ -133,6 +133,21 @@ def test_moe_layer_verify_columns(ops, synth, qtype):
     assert_close(out4, out_ref, "verify out")
 
 
+def test_moe_layer_guard_workspace_reused(ops, synth):
+    """The F16 guard in the fused kernel with a workspace full of stale non-zero bytes (as after other layers' calls):
+    inter 768 leaves padding blocks past F / 32 in the act maxima that no producer writes; the guard must read only
+    the real blocks, so the result equals the zero-filled workspace's bit for bit."""
+    layer = synth.build_layer(H, F, NE, K, 12, 14, SEED, layer=5, guard=True, std=0.5)
+    x_d = synth.activations(1, H, SEED, layer=11) * 40.0
+    ws0 = layer.workspace(1)
+    out0 = host(layer(x_d, ws=ws0))
+    ws1 = layer.workspace(1)
+    ws1.fill_(0x4F)  # every float field 3.5e9: would dominate a guard maximum that read it
+    out1 = host(layer(x_d, ws=ws1))
+    assert np.array_equal(out0, out1)
+    assert np.array_equal(host(layer.trace(ws0, 1)["escale"]), host(layer.trace(ws1, 1)["escale"]))
+
+
 def test_moe_layer_guard_and_residual(ops, synth):
     """F16 guard on (large activations: e > 1) and the residual add of the reference's combine."""
     layer = synth.build_layer(H, F, NE, K, 12, 14, SEED, layer=5, guard=True, std=0.5)
