@@ -10,7 +10,7 @@
 //                          d * sum_g (sc_g - 32) * (d8 * (u . a) - 4 * d8 * sum a)
 //   Q8_0 quarter q       : blocks 2q and 2q+1 of 8 consecutive 34-byte blocks; sum_b (d_b * d8) * (q_b . a)
 // The integer products are exact (v_dot4 on int8 lanes); the zero points (32 for Q6_K, 4 for Q3_K) are folded into
-// the activation sums, as in block_dot.
+// the activation sums (group_term), so the unsigned codes are never re-biased per byte.
 #pragma once
 
 #include "fns_block.hpp"

@@ -95,11 +95,6 @@ struct LayerArgs {
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t) b << 16); }
 
-// Plain copy of `bytes` (multiple of 16) from global memory into LDS by the whole workgroup.
-__device__ __forceinline__ void copy_to_lds(uint8_t *dst, const uint8_t *__restrict__ src, int bytes, int tid, int nt) {
-    for (int i = tid; i < bytes / 16; i += nt) ((uint4 *) dst)[i] = ((const uint4 *) src)[i];
-}
-
 // Writes one lane's Q8_1 value into the LDS-image row `pack` (npad columns) at column i; lanes of one block agree
 // on d and the sums.
 __device__ __forceinline__ void pack_store(uint8_t *pack, int npad, int i, const Q8Lane &r) {
@@ -252,7 +247,6 @@ __global__ __launch_bounds__(NT) void k_route_quant(const LayerArgs a) {
 
 // ---- K2: routing + gate/up + SwiGLU + Q8_1 of act ------------------------------------------------------------------
 // NT threads per workgroup; LPR lanes per row; rows per workgroup RPB = max(32, NT / LPR) (whole Q8_1 blocks of act).
-template <int NT, int LPR> constexpr int gu_rows_per_group() { return (NT / LPR) >= 32 ? 1 : 32 / (NT / LPR); }
 
 // LDS of the routing preamble.
 struct alignas(16) RouteLds {
@@ -422,170 +416,7 @@ __device__ __forceinline__ void quant_act(const LayerArgs &a, const RouteLds &rs
     }
 }
 
-// Register-staged form (any row length): each lane loads whole blocks of its rows straight into VGPRs.
-template <int TQ, int LPR, int BPL, int NC, int NT>
-__global__ __launch_bounds__(NT) void k_gate_up(const LayerArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ RouteLds rs;
-    constexpr int BB = Traits<TQ>::bytes;
-    constexpr int G = NT / LPR;
-    constexpr int RPG = gu_rows_per_group<NT, LPR>();
-    constexpr int RPB = G * RPG;  // rows per workgroup, a multiple of 32
-    constexpr int BPLX = BPL > 0 ? BPL : 1;
-    float *s_act = (float *) smem;  // [NC][RPB]
-    uint8_t *s_x = smem + NC * RPB * 4;
-    const int tid = threadIdx.x;
-    const int T = a.T, H = a.H;
-    const int npad = (H + 511) / 512 * 512;
-    const int xbytes = img_bytes(npad);
-
-    for (int t = 0; t < T; ++t) copy_to_lds(s_x + t * xbytes, a.xpack + (size_t) t * xbytes, xbytes, tid, NT);
-    const int e = route_channel<NT>(a, rs);
-    if (e < 0) return;  // fewer distinct experts than channels: uniform exit of the whole workgroup
-    const int ncol = rs.ncol;
-
-    const uint8_t *slot = (const uint8_t *) a.table[e];
-    const uint8_t *wa = slot + a.up_off, *wb = slot + a.gate_off;
-    const int nblk = H / 256;
-    const int64_t row_bytes = (int64_t) nblk * BB;
-    const int lane = tid % LPR, grp = tid / LPR;
-    const int rowb = blockIdx.x * RPB;  // inter is a multiple of 256: every row of the workgroup exists
-    BlockRegs<TQ> ru[RPG][BPLX], rg[RPG][BPLX];
-    if constexpr (BPL > 0) {
-#pragma unroll
-        for (int r = 0; r < RPG; ++r) {
-            const int row = rowb + r * G + grp;
-#pragma unroll
-            for (int k = 0; k < BPL; ++k) {
-                const int bb = lane + k * LPR;
-                if (bb < nblk) {
-                    block_load<TQ>(wa + row * row_bytes + (int64_t) bb * BB, ru[r][k]);
-                    block_load<TQ>(wb + row * row_bytes + (int64_t) bb * BB, rg[r][k]);
-                }
-            }
-        }
-    }
-    ActImg img[NC];
-#pragma unroll
-    for (int n = 0; n < NC; ++n) img[n] = act_img(s_x + (n < ncol ? rs.xrow[n] : 0) * xbytes, npad);
-
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) {
-        const int row = rowb + r * G + grp;
-        float acc[NC], accg[NC];
-#pragma unroll
-        for (int n = 0; n < NC; ++n) acc[n] = accg[n] = 0.0f;
-        if constexpr (BPL > 0) {
-#pragma unroll
-            for (int k = 0; k < BPL; ++k) {
-                const int bb = lane + k * LPR;
-                if (bb < nblk) {
-#pragma unroll
-                    for (int n = 0; n < NC; ++n) {
-                        if (NC == 1 || n < ncol) {
-                            acc[n] += block_dot<TQ>(ru[r][k], img[n], bb * 256);
-                            accg[n] += block_dot<TQ>(rg[r][k], img[n], bb * 256);
-                        }
-                    }
-                }
-            }
-        } else {
-            for (int bb = lane; bb < nblk; bb += LPR) {
-                BlockRegs<TQ> u, g;
-                block_load<TQ>(wa + row * row_bytes + (int64_t) bb * BB, u);
-                block_load<TQ>(wb + row * row_bytes + (int64_t) bb * BB, g);
-#pragma unroll
-                for (int n = 0; n < NC; ++n) {
-                    if (NC == 1 || n < ncol) {
-                        acc[n] += block_dot<TQ>(u, img[n], bb * 256);
-                        accg[n] += block_dot<TQ>(g, img[n], bb * 256);
-                    }
-                }
-            }
-        }
-        gate_up_epilogue<LPR, NC>(a, rs, s_act, RPB, r * G + grp, row, lane, acc, accg);
-    }
-    __syncthreads();
-    quant_act<NT>(a, rs, s_act, RPB, rowb);
-}
-
-// LDS-staged form (whole rows of both matrices fit in LDS): the workgroup's 32 up rows and 32 gate rows - two
-// contiguous byte ranges - are moved into LDS with coalesced LDS-DMA loads, then each lane takes whole blocks of
-// its row from LDS. Expert slots that are not 16-byte aligned take the register path inside the same kernel.
-constexpr int kGuRows = 32;
-
-template <int TQ, int LPR, int NC, int NT>
-__global__ __launch_bounds__(NT) void k_gate_up_lds(const LayerArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ RouteLds rs;
-    constexpr int BB = Traits<TQ>::bytes;
-    constexpr int G = NT / LPR;
-    static_assert(G == kGuRows, "one row per lane group");
-    float *s_act = (float *) smem;  // [NC][32]
-    uint8_t *s_x = smem + NC * kGuRows * 4;
-    const int tid = threadIdx.x;
-    const int T = a.T, H = a.H;
-    const int npad = (H + 511) / 512 * 512;
-    const int xbytes = img_bytes(npad);
-    uint8_t *s_w = s_x + T * xbytes;  // [up rows | gate rows]
-
-    const int wgid = blockIdx.y * gridDim.x + blockIdx.x;
-    FNS_MARK(1, wgid, 0);
-    dma_to_lds<NT>(s_x, a.xpack, T * xbytes);
-    route_channel<NT>(a, rs);
-    FNS_MARK(1, wgid, 1);
-    const int e = rs.e;
-    if (e < 0) return;
-    const int ncol = rs.ncol;
-
-    const int nblk = H / 256;
-    const int row_bytes = nblk * BB;
-    const int rowb = blockIdx.x * kGuRows;
-    const uint8_t *slot = (const uint8_t *) a.table[e];
-    const uint8_t *wa = slot + a.up_off + (int64_t) rowb * row_bytes;
-    const uint8_t *wb = slot + a.gate_off + (int64_t) rowb * row_bytes;
-    const int region = kGuRows * row_bytes;  // a multiple of 16 (block sizes are even)
-    const bool staged = (((uintptr_t) wa | (uintptr_t) wb) & 15u) == 0;
-    if (staged) {
-        dma_to_lds<NT>(s_w, wa, region);
-        dma_to_lds<NT>(s_w + region, wb, region);
-    }
-    dma_wait();
-    __syncthreads();
-    FNS_MARK(1, wgid, 2);
-
-    const int lane = tid % LPR, grp = tid / LPR;
-    const int row = rowb + grp;
-    ActImg img[NC];
-#pragma unroll
-    for (int n = 0; n < NC; ++n) img[n] = act_img(s_x + (n < ncol ? rs.xrow[n] : 0) * xbytes, npad);
-    float acc[NC], accg[NC];
-#pragma unroll
-    for (int n = 0; n < NC; ++n) acc[n] = accg[n] = 0.0f;
-    for (int bb = lane; bb < nblk; bb += LPR) {
-        BlockRegs<TQ> u, g;
-        const int off = grp * row_bytes + bb * BB;
-        if (staged) {
-            lds_block_load<TQ>(s_w + off, u);
-            lds_block_load<TQ>(s_w + region + off, g);
-        } else {
-            block_load<TQ>(wa + off, u);
-            block_load<TQ>(wb + off, g);
-        }
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            if (NC == 1 || n < ncol) {
-                acc[n] += block_dot<TQ>(u, img[n], bb * 256);
-                accg[n] += block_dot<TQ>(g, img[n], bb * 256);
-            }
-        }
-    }
-    gate_up_epilogue<LPR, NC>(a, rs, s_act, kGuRows, grp, row, lane, acc, accg);
-    __syncthreads();
-    FNS_MARK(1, wgid, 3);
-    quant_act<NT>(a, rs, s_act, kGuRows, rowb);
-    FNS_MARK(1, wgid, 4);
-}
+constexpr int kGuRows = 32;  // gate/up rows per workgroup (one Q8_1 block of act)
 
 // Quarter-block form (the decode path): 1024 threads, 32 rows per workgroup, 32 lanes per row, each lane one or more
 // 64-value quarters of the row's blocks. Waves 1-15 start the copy of the x images while wave 0 loads the logits;
@@ -691,228 +522,6 @@ __device__ __forceinline__ float guard_scale(float amax) {
     e = fminf(fmaxf(e, 0.0f), 127.0f);
     e = e * 0.6931471805599453f;
     return expf(e);
-}
-
-// Items are (output row, channel) pairs; LPR lanes per item, each lane one or more whole blocks of the row.
-template <int TQ, int LPR, int BPL>
-__global__ __launch_bounds__(256) void k_down_combine(const LayerArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float s_e[kMaxCh], s_w[kMaxCh];
-    __shared__ float s_dexp[kMaxCh][kDownRows];
-    constexpr int BB = Traits<TQ>::bytes;
-    constexpr int G = 256 / LPR;
-    constexpr int BPLX = BPL > 0 ? BPL : 1;
-    const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
-    const int T = a.T, K = a.K, F = a.F, H = a.H;
-    const int CH = T * K;
-    const int fpad = (F + 511) / 512 * 512;
-    const int fbytes = img_bytes(fpad);
-    const int r0 = blockIdx.x * kDownRows;
-    const int nblk = F / 256;
-    const int64_t row_bytes = (int64_t) nblk * BB;
-    const int lane = tid % LPR, grp = tid / LPR;
-    const int n_items = kDownRows * CH;
-
-    BlockRegs<TQ> rb[BPLX];
-    int ch = 0, row = 0;
-    bool ok = false;
-    const uint8_t *wm = nullptr;
-    auto item = [&](int it) {
-        ch = it % CH;
-        row = r0 + it / CH;
-        ok = it < n_items && row < H;
-        wm = ok ? gload<const uint8_t *>((const uint8_t *) (a.dptr + ch)) : nullptr;
-    };
-    auto load_item = [&]() {
-        if constexpr (BPL > 0) {
-#pragma unroll
-            for (int k = 0; k < BPL; ++k) {
-                const int bb = lane + k * LPR;
-                if (ok && bb < nblk) block_load<TQ>(wm + row * row_bytes + (int64_t) bb * BB, rb[k]);
-            }
-        }
-    };
-    // 1. order of issue matters (a wave's loads complete in order): down pointer, then the act images, then the
-    //    weights; the images reach LDS while the weights are still in flight.
-    item(grp);
-    constexpr int kMaxCopy = 4;  // 16-byte pieces per thread held in registers
-    uint4 cp[kMaxCopy];
-    const int n16 = CH * fbytes / 16;
-#pragma unroll
-    for (int k = 0; k < kMaxCopy; ++k) {
-        const int i = tid + k * 256;
-        if (i < n16) cp[k] = gload<uint4>(a.apack + (size_t) i * 16);
-    }
-    float wv = 0.0f;
-    if (tid < CH) wv = a.w[tid];
-    load_item();
-#pragma unroll
-    for (int k = 0; k < kMaxCopy; ++k) {
-        const int i = tid + k * 256;
-        if (i < n16) ((uint4 *) smem)[i] = cp[k];
-    }
-    for (int i = tid + kMaxCopy * 256; i < n16; i += 256) ((uint4 *) smem)[i] = gload<uint4>(a.apack + (size_t) i * 16);
-    if (tid < CH) {
-        s_w[tid] = wv;
-        s_e[tid] = 1.0f;
-    }
-    __syncthreads();
-    // 2. F16 guard: rows whose scale is not 1 are divided and re-quantised (reference src/kernels.cu:554-577)
-    if (a.guard) {
-        for (int c = wave; c < CH; c += 4) {
-            float m = 0.0f;
-            for (int b = lane64; b < fpad / 32; b += kWave) m = fmaxf(m, a.blk_amax[(size_t) c * (fpad / 32) + b]);
-            m = lanes_max<64>(m);
-            const float e = guard_scale(m);
-            if (lane64 == 0) {
-                s_e[c] = e;
-                if (blockIdx.x == 0) a.escale[c] = e;
-            }
-            if (e != 1.0f) {
-                const float *src = a.act + (size_t) c * F;
-                for (int i0 = 0; i0 < fpad; i0 += kWave) {
-                    const int i = i0 + lane64;
-                    const Q8Lane r = q8_1_lane(i < F ? src[i] / e : 0.0f);
-                    pack_store(smem + c * fbytes, fpad, i, r);
-                }
-            }
-        }
-        __syncthreads();
-    } else if (blockIdx.x == 0 && tid < CH) {
-        a.escale[tid] = 1.0f;
-    }
-    // 3. dot products over (row, channel) items
-    for (int it = grp; it < n_items; it += G) {
-        if (it != grp) {
-            item(it);
-            load_item();
-        }
-        float acc = 0.0f;
-        if (ok) {
-            const ActImg img = act_img(smem + ch * fbytes, fpad);
-            if constexpr (BPL > 0) {
-#pragma unroll
-                for (int k = 0; k < BPL; ++k) {
-                    const int bb = lane + k * LPR;
-                    if (bb < nblk) acc += block_dot<TQ>(rb[k], img, bb * 256);
-                }
-            } else {
-                for (int bb = lane; bb < nblk; bb += LPR) {
-                    BlockRegs<TQ> t;
-                    block_load<TQ>(wm + row * row_bytes + (int64_t) bb * BB, t);
-                    acc += block_dot<TQ>(t, img, bb * 256);
-                }
-            }
-        }
-        acc = lanes_sum<LPR>(acc);
-        if (lane == 0 && ok) s_dexp[ch][row - r0] = acc;
-    }
-    __syncthreads();
-    // 4. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + sh) (+ x_resid), sh: shared expert or 0
-    if (tid < T * kDownRows) {
-        const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
-        if (r < H) {
-            float moe = (s_dexp[t * K][rr] * s_e[t * K]) * s_w[t * K];
-            for (int j = 1; j < K; ++j) moe = moe + (s_dexp[t * K + j][rr] * s_e[t * K + j]) * s_w[t * K + j];
-            moe = moe + (a.sh ? a.sh[(size_t) t * H + r] : 0.0f);
-            a.out[(size_t) t * H + r] = a.x_resid ? moe + a.x_resid[(size_t) t * H + r] : moe;
-        }
-    }
-}
-
-// LDS-staged form: the down rows [r0, r0 + 8) of every (token, slot) channel - one contiguous byte range per channel -
-// are gathered into LDS with coalesced LDS-DMA loads right after the act images; each lane then takes whole blocks
-// from LDS. Used when the ranges and the images fit in LDS; unaligned expert slots take global loads in place.
-template <int TQ, int LPR>
-__global__ __launch_bounds__(256) void k_down_lds(const LayerArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float s_e[kMaxCh], s_w[kMaxCh];
-    __shared__ float s_dexp[kMaxCh][kDownRows];
-    __shared__ const uint8_t *s_dp[kMaxCh];
-    constexpr int BB = Traits<TQ>::bytes;
-    constexpr int G = 256 / LPR;
-    const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
-    const int T = a.T, K = a.K, F = a.F, H = a.H;
-    const int CH = T * K;
-    const int fpad = (F + 511) / 512 * 512;
-    const int fbytes = img_bytes(fpad);
-    const int r0 = blockIdx.x * kDownRows;  // hidden is a multiple of 256: all 8 rows exist
-    const int nblk = F / 256;
-    const int row_bytes = nblk * BB;
-    const int region = kDownRows * row_bytes;  // a multiple of 16
-    uint8_t *s_wt = smem + CH * fbytes;
-
-    FNS_MARK(2, blockIdx.x, 0);
-    // 1. down pointers and combine weights (a barrier waits for every outstanding load, so only these go first)
-    if (tid < CH) {
-        s_dp[tid] = gload<const uint8_t *>((const uint8_t *) (a.dptr + tid)) + (int64_t) r0 * row_bytes;
-        s_w[tid] = a.w[tid];
-        s_e[tid] = 1.0f;
-    }
-    __syncthreads();
-    FNS_MARK(2, blockIdx.x, 1);
-    uintptr_t mis = 0;
-    for (int c = 0; c < CH; ++c) mis |= (uintptr_t) s_dp[c];
-    const bool staged = (mis & 15u) == 0;
-    // 2. act images, then the weights: piece o of the flattened [channel][region] image comes from that channel's slot
-    dma_to_lds<256>(smem, a.apack, CH * fbytes);
-    if (staged)
-        dma_gather_to_lds<256>(s_wt, CH * region, [&](int o) { return s_dp[o / region] + o % region; });
-    dma_wait();
-    __syncthreads();
-    FNS_MARK(2, blockIdx.x, 2);
-    // 3. F16 guard: rows whose scale is not 1 are divided and re-quantised (reference src/kernels.cu:554-577)
-    if (a.guard) {
-        for (int c = wave; c < CH; c += 4) {
-            float m = 0.0f;
-            for (int b = lane64; b < fpad / 32; b += kWave) m = fmaxf(m, a.blk_amax[(size_t) c * (fpad / 32) + b]);
-            m = lanes_max<64>(m);
-            const float e = guard_scale(m);
-            if (lane64 == 0) {
-                s_e[c] = e;
-                if (blockIdx.x == 0) a.escale[c] = e;
-            }
-            if (e != 1.0f) {
-                const float *src = a.act + (size_t) c * F;
-                for (int i0 = 0; i0 < fpad; i0 += kWave) {
-                    const int i = i0 + lane64;
-                    const Q8Lane r = q8_1_lane(i < F ? src[i] / e : 0.0f);
-                    pack_store(smem + c * fbytes, fpad, i, r);
-                }
-            }
-        }
-        __syncthreads();
-    } else if (blockIdx.x == 0 && tid < CH) {
-        a.escale[tid] = 1.0f;
-    }
-    // 4. dot products over (row, channel) items
-    const int lane = tid % LPR, grp = tid / LPR;
-    const int n_items = kDownRows * CH;
-    for (int it = grp; it < n_items; it += G) {
-        const int ch = it % CH, rr = it / CH;
-        const ActImg img = act_img(smem + ch * fbytes, fpad);
-        float acc = 0.0f;
-        for (int bb = lane; bb < nblk; bb += LPR) {
-            BlockRegs<TQ> t;
-            const int off = rr * row_bytes + bb * BB;
-            if (staged) lds_block_load<TQ>(s_wt + ch * region + off, t);
-            else block_load<TQ>(s_dp[ch] + off, t);
-            acc += block_dot<TQ>(t, img, bb * 256);
-        }
-        acc = lanes_sum<LPR>(acc);
-        if (lane == 0) s_dexp[ch][rr] = acc;
-    }
-    __syncthreads();
-    FNS_MARK(2, blockIdx.x, 3);
-    // 5. combine in slot order: out[t][r] = (sum_j (dexp * e_j) * w_j + sh) (+ x_resid), sh: shared expert or 0
-    if (tid < T * kDownRows) {
-        const int t = tid / kDownRows, rr = tid % kDownRows, r = r0 + rr;
-        float moe = (s_dexp[t * K][rr] * s_e[t * K]) * s_w[t * K];
-        for (int j = 1; j < K; ++j) moe = moe + (s_dexp[t * K + j][rr] * s_e[t * K + j]) * s_w[t * K + j];
-        moe = moe + (a.sh ? a.sh[(size_t) t * H + r] : 0.0f);
-        a.out[(size_t) t * H + r] = a.x_resid ? moe + a.x_resid[(size_t) t * H + r] : moe;
-    }
-    FNS_MARK(2, blockIdx.x, 4);
 }
 
 // Quarter-block form of the down projection + combine: 1024 threads; the work is 2 * n_chan groups of (channel, four
@@ -1333,12 +942,6 @@ inline size_t fused_lds(int H, int F, int K, int BG, int BD, int Fs = 0) {
     return lds <= kLdsBudget ? lds : 0;
 }
 
-// LDS bytes of the staged kernels (0 when they do not fit: the register forms run instead).
-inline size_t gate_up_lds_bytes(int T, int H, int BB, int NC) {
-    const size_t b = (size_t) NC * kGuRows * 4 + (size_t) T * img_bytes((int) host::pad512(H)) +
-                     2 * (size_t) kGuRows * (H / 256) * BB + 16;
-    return b <= kLdsBudget ? b : 0;
-}
 // Quarter forms: sized for kMaxTok tokens whatever the call's n_tok, so a verify call and a decode call of the same
 // layer take the same kernels (and so the same arithmetic).
 inline size_t gate_up_q_lds_bytes(int T, int H, int BB, int NC) {
@@ -1348,135 +951,30 @@ inline size_t gate_up_q_lds_bytes(int T, int H, int BB, int NC) {
 inline bool gate_up_q_fits(int H, int BB) { return gate_up_q_lds_bytes(kMaxTok, H, BB, kMaxTok) <= kLdsBudget; }
 inline size_t down_q_lds_bytes(int CH, int F) { return (size_t) CH * img_bytes((int) host::pad512(F)) + 16; }
 inline bool down_q_fits(int CH, int F) { return down_q_lds_bytes(CH, F) <= kLdsBudget; }
-inline size_t down_lds_bytes(int CH, int F, int BB) {
-    const size_t b = (size_t) CH * img_bytes((int) host::pad512(F)) + (size_t) CH * kDownRows * (F / 256) * BB + 16;
-    return b <= kLdsBudget ? b : 0;
-}
-
-// Lanes per row (a power of two, at most 8) and whole blocks per lane (0: runtime loop) for a row of nblk blocks.
-struct BplShape {
-    int lpr, bpl;
-};
-inline BplShape bpl_shape(int nblk) {
-    int lpr = 1;
-    while (lpr < nblk && lpr < 8) lpr *= 2;
-    const int bpl = (nblk + lpr - 1) / lpr;
-    return {lpr, bpl <= 2 ? bpl : 0};
-}
-
-template <int TQ, int LPR, int BPL, int NC, int NT> int launch_gate_up_nt(const LayerArgs &a, hipStream_t st) {
-    constexpr int RPB = (NT / LPR) * gu_rows_per_group<NT, LPR>();
-    const int n_chan = a.T == 1 ? a.K : std::min(a.T * a.K, a.NE);
-    const dim3 grid((unsigned) ((a.F + RPB - 1) / RPB), (unsigned) n_chan);
-    const int npad = (int) host::pad512(a.H);
-    const size_t lds = (size_t) NC * RPB * 4 + (size_t) a.T * img_bytes(npad);
-    if (lds > 64 * 1024) return host::set_error(host::ERR_SHAPE, "moe_layer: hidden too large for LDS staging");
-    hipLaunchKernelGGL((k_gate_up<TQ, LPR, BPL, NC, NT>), grid, dim3(NT), lds, st, a);
-    return host::check_launch("moe gate_up");
-}
-
-template <int TQ, int LPR, int BPL> int launch_gate_up(const LayerArgs &a, hipStream_t st) {
-    if (a.T == 1) return launch_gate_up_nt<TQ, LPR, BPL, 1, 256>(a, st);
-    return launch_gate_up_nt<TQ, LPR, BPL, kMaxTok, 256>(a, st);
-}
-
-template <int TQ, int LPR> int launch_gate_up_b(const LayerArgs &a, int bpl, hipStream_t st) {
-    if (bpl == 1) return launch_gate_up<TQ, LPR, 1>(a, st);
-    if (bpl == 2) return launch_gate_up<TQ, LPR, 2>(a, st);
-    return launch_gate_up<TQ, LPR, 0>(a, st);
-}
-
-template <int TQ, int LPR> int launch_gate_up_lds(const LayerArgs &a, size_t lds, hipStream_t st) {
+// The quarter kernels hold every shape moe_layer accepts: hidden <= 16384 keeps kMaxTok x images within the LDS budget
+// of the gate/up kernel, and prepare() rejects n_tok * k act images beyond 64 KiB for the down kernel. The checks
+// below only restate that.
+template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
+    if (!gate_up_q_fits(a.H, Traits<TQ>::bytes))
+        return host::set_error(host::ERR_SHAPE, "moe_layer: hidden %d too large for the gate/up kernel", a.H);
     const int n_chan = a.T == 1 ? a.K : std::min(a.T * a.K, a.NE);
     const dim3 grid((unsigned) (a.F / kGuRows), (unsigned) n_chan);
-    if (a.T == 1) hipLaunchKernelGGL((k_gate_up_lds<TQ, LPR, 1, kGuRows * LPR>), grid, dim3(kGuRows * LPR), lds, st, a);
-    else hipLaunchKernelGGL((k_gate_up_lds<TQ, LPR, kMaxTok, kGuRows * LPR>), grid, dim3(kGuRows * LPR), lds, st, a);
-    return host::check_launch("moe gate_up (lds)");
+    if (a.T == 1)
+        hipLaunchKernelGGL((k_gate_up_q<TQ, 1>), grid, dim3(kQThreads), gate_up_q_lds_bytes(1, a.H, Traits<TQ>::bytes, 1),
+                           st, a);
+    else
+        hipLaunchKernelGGL((k_gate_up_q<TQ, kMaxTok, 256>), grid, dim3(256),
+                           gate_up_q_lds_bytes(a.T, a.H, Traits<TQ>::bytes, kMaxTok), st, a);
+    return host::check_launch("moe gate_up (quarters)");
 }
-
-// Types that only the quarter kernels decode (the register- and LDS-staged whole-block forms are K-quant only).
-template <int T> constexpr bool kQuarterOnly = T == T_Q8_0 || T == T_IQ4_XS || T == T_IQ3_XXS || T == T_IQ3_S ||
-                                               T == T_IQ2_S;
-
-template <int TQ> int dispatch_gate_up(const LayerArgs &a, hipStream_t st) {
-    const int nblk = a.H / 256;
-    if (gate_up_q_fits(a.H, Traits<TQ>::bytes)) {
-        const int n_chan = a.T == 1 ? a.K : std::min(a.T * a.K, a.NE);
-        const dim3 grid((unsigned) (a.F / kGuRows), (unsigned) n_chan);
-        if (a.T == 1)
-            hipLaunchKernelGGL((k_gate_up_q<TQ, 1>), grid, dim3(kQThreads),
-                               gate_up_q_lds_bytes(1, a.H, Traits<TQ>::bytes, 1), st, a);
-        else
-            hipLaunchKernelGGL((k_gate_up_q<TQ, kMaxTok, 256>), grid, dim3(256),
-                               gate_up_q_lds_bytes(a.T, a.H, Traits<TQ>::bytes, kMaxTok), st, a);
-        return host::check_launch("moe gate_up (quarters)");
-    }
-    if constexpr (kQuarterOnly<TQ>) {
-        return host::set_error(host::ERR_SHAPE, "moe_layer: hidden %d too large for the quarter kernels", a.H);
-    } else {
-    const size_t lds = gate_up_lds_bytes(a.T, a.H, Traits<TQ>::bytes, a.T == 1 ? 1 : kMaxTok);
-    if (lds) {
-        if (nblk <= 2) return launch_gate_up_lds<TQ, 2>(a, lds, st);
-        if (nblk <= 4) return launch_gate_up_lds<TQ, 4>(a, lds, st);
-        return launch_gate_up_lds<TQ, 8>(a, lds, st);
-    }
-    const BplShape s = bpl_shape(nblk);
-    switch (s.lpr) {
-        case 1: return launch_gate_up_b<TQ, 1>(a, s.bpl, st);
-        case 2: return launch_gate_up_b<TQ, 2>(a, s.bpl, st);
-        case 4: return launch_gate_up_b<TQ, 4>(a, s.bpl, st);
-        default: return launch_gate_up_b<TQ, 8>(a, s.bpl, st);
-    }
-    }
-}
-
-template <int TQ, int LPR, int BPL> int launch_down(const LayerArgs &a, hipStream_t st) {
-    const dim3 grid((unsigned) ((a.H + kDownRows - 1) / kDownRows));
-    const size_t lds = (size_t) a.T * a.K * img_bytes((int) host::pad512(a.F));
-    hipLaunchKernelGGL((k_down_combine<TQ, LPR, BPL>), grid, dim3(256), lds, st, a);
-    return host::check_launch("moe down_combine");
-}
-
-template <int TQ, int LPR> int launch_down_b(const LayerArgs &a, int bpl, hipStream_t st) {
-    if (bpl == 1) return launch_down<TQ, LPR, 1>(a, st);
-    if (bpl == 2) return launch_down<TQ, LPR, 2>(a, st);
-    return launch_down<TQ, LPR, 0>(a, st);
-}
-
-template <int TQ, int LPR> int launch_down_lds(const LayerArgs &a, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((k_down_lds<TQ, LPR>), dim3((unsigned) (a.H / kDownRows)), dim3(256), lds, st, a);
-    return host::check_launch("moe down_combine (lds)");
-}
-
 template <int TQ> int dispatch_down(const LayerArgs &a, hipStream_t st) {
-    const int nblk = a.F / 256;
-    if (down_q_fits(a.T * a.K, a.F)) {
-        hipLaunchKernelGGL((k_down_q<TQ>), dim3((unsigned) (a.H / kDownRows)), dim3(kQThreads),
-                           down_q_lds_bytes(a.T * a.K, a.F), st, a);
-        return host::check_launch("moe down_combine (quarters)");
-    }
-    if constexpr (kQuarterOnly<TQ>) {
-        return host::set_error(host::ERR_SHAPE, "moe_layer: n_tok * k * inter too large for the quarter kernels");
-    } else {
-    const size_t lds = down_lds_bytes(a.T * a.K, a.F, Traits<TQ>::bytes);
-    if (lds) {
-        if (nblk <= 2) return launch_down_lds<TQ, 2>(a, lds, st);
-        if (nblk <= 4) return launch_down_lds<TQ, 4>(a, lds, st);
-        return launch_down_lds<TQ, 8>(a, lds, st);
-    }
-    const BplShape s = bpl_shape(nblk);
-    switch (s.lpr) {
-        case 1: return launch_down_b<TQ, 1>(a, s.bpl, st);
-        case 2: return launch_down_b<TQ, 2>(a, s.bpl, st);
-        case 4: return launch_down_b<TQ, 4>(a, s.bpl, st);
-        default: return launch_down_b<TQ, 8>(a, s.bpl, st);
-    }
-    }
+    if (!down_q_fits(a.T * a.K, a.F))
+        return host::set_error(host::ERR_SHAPE, "moe_layer: n_tok * k * inter too large for the down kernel");
+    hipLaunchKernelGGL((k_down_q<TQ>), dim3((unsigned) (a.H / kDownRows)), dim3(kQThreads),
+                       down_q_lds_bytes(a.T * a.K, a.F), st, a);
+    return host::check_launch("moe down_combine (quarters)");
 }
 
-// The fused kernel runs only when every workgroup can be resident at once (it waits on other workgroups): the
-// occupancy of each (gate/up type, down type, LDS size) is queried once per device and cached.
-// (sh: the instantiation with the shared expert as slot K)
 template <int TGU, int TDN> const void *fused_fn(bool sh) {
     return sh ? (const void *) k_layer_fused<TGU, TDN, true> : (const void *) k_layer_fused<TGU, TDN, false>;
 }
