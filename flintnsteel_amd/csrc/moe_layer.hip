@@ -334,9 +334,11 @@ __device__ void route_all(const LayerArgs &a) {
     // ranks one token with the block top-k (the groups past T repeat the last token; their result is unused)
     __shared__ __align__(16) uint64_t s_tk[kMaxTok][kTopkScratch];
     __shared__ float s_lg[kMaxTok][256];
+    __shared__ const uint8_t *s_tabp[256];  // the expert table, fetched with the logits (no dependent load later)
     const int grp = tid / 256, gt = tid % 256;
     if (grp < T && gt < NE)
         s_lg[grp][gt] = __hip_atomic_load(a.logits + (size_t) grp * NE + gt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < NE) s_tabp[tid] = gload<const uint8_t *>((const uint8_t *) (a.table + tid));
     __syncthreads();
     route_topk_filter<256>(gt, s_lg[grp < T ? grp : T - 1], NE, K, a.gating, s_tk[grp], s_sel[grp], s_pv[grp]);
     __syncthreads();
@@ -345,7 +347,7 @@ __device__ void route_all(const LayerArgs &a) {
         const int t = tid / K, j = tid % K, e = s_sel[t][j];
         a.ids[tid] = e;
         a.w[tid] = route_weight(s_pv[t], K, a.norm, j);
-        a.dptr[tid] = (const uint8_t *) gload<const char *>((const uint8_t *) (a.table + e)) + a.down_off;
+        a.dptr[tid] = s_tabp[e] + a.down_off;
         s_col[e][t] = (int8_t) (j + 1);
     }
     __syncthreads();
