@@ -15,20 +15,40 @@
 
 #include "fns_block.hpp"
 
+#include <type_traits>
+
 namespace fns::dev {
 
-// Loader policies: Aligned16 for 16-byte-aligned LDS data, Any2 for 2-byte-aligned data (LDS or global, generic).
+// Loader policies. Aligned16 (16-byte-aligned) and Any2 (2-byte-aligned) read weights in global memory through
+// global-address-space pointers: global loads count on the vector-memory counter only, so the compiler can keep
+// several quarters' loads in flight while LDS reads of the activations complete (a generic pointer becomes a flat
+// load, which counts on both counters and made it wait after every quarter). Padded reads blocks staged in LDS.
+typedef uint32_t gv4u __attribute__((ext_vector_type(4)));
+typedef gv4u gv4u_a2 __attribute__((aligned(2)));
+typedef uint32_t gu32_a2 __attribute__((aligned(2)));
+typedef __attribute__((address_space(1))) const gv4u GV4;
+typedef __attribute__((address_space(1))) const gv4u_a2 GV4a2;
+typedef __attribute__((address_space(1))) const gu32_a2 GU32a2;
 struct Aligned16 {
-    static __device__ __forceinline__ uint4 ld(const uint8_t *p) { return *(const uint4 *) p; }
+    static __device__ __forceinline__ uint4 ld(const uint8_t *p) {
+        const gv4u v = *(GV4 *) p;
+        return make_uint4(v.x, v.y, v.z, v.w);
+    }
+    static __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *(GU32a2 *) p; }
 };
 struct Any2 {
-    static __device__ __forceinline__ uint4 ld(const uint8_t *p) { return lds16u(p); }
+    static __device__ __forceinline__ uint4 ld(const uint8_t *p) {
+        const gv4u v = *(GV4a2 *) p;
+        return make_uint4(v.x, v.y, v.z, v.w);
+    }
+    static __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *(GU32a2 *) p; }
 };
 // Padded: blocks staged in LDS at a 16-byte-aligned stride (kStageBytes), each block's last 16-byte piece holding the
 // block's last 16 bytes (so no piece reads past the block); for Q4_K / Q5_K / Q8_0 / IQ types the same as Aligned16
 // (their staged layout is the verbatim one).
 struct Padded {
     static __device__ __forceinline__ uint4 ld(const uint8_t *p) { return *(const uint4 *) p; }
+    static __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *(const uint32_t *) p; }
 };
 template <int T> constexpr int kStageBytes = T == T_Q6_K ? 224 : T == T_Q3_K ? 112 : Traits<T>::bytes;
 // 4 bytes at a 2-byte-aligned address.
@@ -109,7 +129,7 @@ template <> __device__ __forceinline__ float quarter_dot_r<T_Q4_K, Any2>(const u
     return q4k_quarter<Any2>(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q4_K, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q4k_quarter<Aligned16>(blk, x, qt);
+    return q4k_quarter<Padded>(blk, x, qt);
 }
 
 template <class L> __device__ __forceinline__ float q5k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
@@ -136,19 +156,21 @@ template <> __device__ __forceinline__ float quarter_dot_r<T_Q5_K, Any2>(const u
     return q5k_quarter<Any2>(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q5_K, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q5k_quarter<Aligned16>(blk, x, qt);
+    return q5k_quarter<Padded>(blk, x, qt);
 }
 
 // Q6_K and Q3_K blocks are only 2-byte aligned: both policies read through Any2.
-// PAD: the block is staged at a 16-byte-aligned address with its last piece (bytes 194 .. 209) at offset 208.
-template <bool PAD = false> __device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+// L = Padded: the block is staged in LDS at a 16-byte-aligned address with its last piece (bytes 194 .. 209) at
+// offset 208; otherwise a 2-byte-aligned block in global memory.
+template <class L> __device__ __forceinline__ float q6k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+    constexpr bool PAD = std::is_same<L, Padded>::value;
     const int n = qt >> 1, hh = qt & 1;
-    auto ld = [&](int o) { return PAD ? *(const uint4 *) (blk + o) : lds16u(blk + o); };
+    auto ld = [&](int o) { return PAD ? L::ld(blk + o) : Any2::ld(blk + o); };
     const uint4 A0 = ld(64 * n), A1 = ld(64 * n + 16);       // ql[64n .. 64n+31]
     const uint4 B0 = ld(64 * n + 32), B1 = ld(64 * n + 48);  // ql[64n+32 .. 64n+63]
     const uint4 Q0 = ld(128 + 32 * n), Q1 = ld(144 + 32 * n);  // qh[32n .. 32n+31]
-    const uint32_t scw = PAD ? *(const uint32_t *) (blk + 192 + 4 * qt) : ld32u(blk + 192 + 4 * qt);  // int8 scales of groups 4qt .. 4qt+3
-    const uint32_t dbits = PAD ? *(const uint32_t *) (blk + 220) >> 16 : ld32u(blk + 208) & 0xffffu;
+    const uint32_t scw = PAD ? L::ld32(blk + 192 + 4 * qt) : Any2::ld32(blk + 192 + 4 * qt);  // int8 scales of groups 4qt .. 4qt+3
+    const uint32_t dbits = PAD ? L::ld32(blk + 220) >> 16 : Any2::ld32(blk + 208) & 0xffffu;
     const uint32_t A[8] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w};
     const uint32_t B[8] = {B0.x, B0.y, B0.z, B0.w, B1.x, B1.y, B1.z, B1.w};
     const uint32_t Q[8] = {Q0.x, Q0.y, Q0.z, Q0.w, Q1.x, Q1.y, Q1.z, Q1.w};
@@ -168,19 +190,21 @@ template <bool PAD = false> __device__ __forceinline__ float q6k_quarter(const u
     return half_to_float(dbits) * sum;
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q6_K, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q6k_quarter(blk, x, qt);
+    return q6k_quarter<Any2>(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q6_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q6k_quarter(blk, x, qt);
+    return q6k_quarter<Any2>(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q6_K, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q6k_quarter<true>(blk, x, qt);
+    return q6k_quarter<Padded>(blk, x, qt);
 }
 
-// PAD: the block is staged at a 16-byte-aligned address with its last piece (bytes 94 .. 109) at offset 96.
-template <bool PAD = false> __device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+// L = Padded: the block is staged in LDS at a 16-byte-aligned address with its last piece (bytes 94 .. 109) at
+// offset 96; otherwise a 2-byte-aligned block in global memory.
+template <class L> __device__ __forceinline__ float q3k_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+    constexpr bool PAD = std::is_same<L, Padded>::value;
     const int n = qt >> 1, hh = qt & 1;
-    auto ld = [&](int o) { return PAD ? *(const uint4 *) (blk + o) : lds16u(blk + o); };
+    auto ld = [&](int o) { return PAD ? L::ld(blk + o) : Any2::ld(blk + o); };
     const uint4 H0 = ld(0), H1 = ld(16);                          // hmask[0 .. 31]
     const uint4 q0 = ld(32 + 32 * n), q1 = ld(48 + 32 * n);  // qs[32n .. 32n+31]
     const uint4 t = ld(PAD ? 96 : 94);                            // scales at +2, d at +14
@@ -210,22 +234,24 @@ template <bool PAD = false> __device__ __forceinline__ float q3k_quarter(const u
     return half_to_float(t.w >> 16) * sum;
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q3_K, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q3k_quarter(blk, x, qt);
+    return q3k_quarter<Any2>(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q3_K, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q3k_quarter(blk, x, qt);
+    return q3k_quarter<Any2>(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q3_K, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q3k_quarter<true>(blk, x, qt);
+    return q3k_quarter<Padded>(blk, x, qt);
 }
 
 // Q8_0 quarter qt = blocks 2qt and 2qt+1 of the 8-block unit (68 bytes at offset 68 qt, 2-byte aligned at least):
 // sum over the two blocks of (d_w * d8) * (q_w . a), the block product of ggml vec_dot_q8_0_q8_1.
-__device__ __forceinline__ float q80_quarter(const uint8_t *blk, const ActQ &x, int qt) {
+template <class L> __device__ __forceinline__ float q80_quarter(const uint8_t *blk, const ActQ &x, int qt) {
     const uint8_t *p = blk + 68 * qt;
-    const uint4 A0 = lds16u(p), A1 = lds16u(p + 16), A2 = lds16u(p + 32), A3 = lds16u(p + 48);
-    const uint32_t W[17] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w, A2.x,
-                            A2.y, A2.z, A2.w, A3.x, A3.y, A3.z, A3.w, ld32u(p + 64)};
+    // (Padded: LDS data, 2-byte aligned within the staged unit; otherwise global memory)
+    auto ld = [&](int o) { return std::is_same<L, Padded>::value ? lds16u(p + o) : Any2::ld(p + o); };
+    const uint4 A0 = ld(0), A1 = ld(16), A2 = ld(32), A3 = ld(48);
+    const uint32_t W[17] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w, A2.x, A2.y, A2.z, A2.w, A3.x, A3.y, A3.z, A3.w,
+                            std::is_same<L, Padded>::value ? ld32u(p + 64) : Any2::ld32(p + 64)};
     int s0 = 0, s1 = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -236,13 +262,13 @@ __device__ __forceinline__ float q80_quarter(const uint8_t *blk, const ActQ &x, 
     return fmaf_(d1, (float) s1, d0 * (float) s0);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Aligned16>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q80_quarter(blk, x, qt);
+    return q80_quarter<Any2>(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Any2>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q80_quarter(blk, x, qt);
+    return q80_quarter<Any2>(blk, x, qt);
 }
 template <> __device__ __forceinline__ float quarter_dot_r<T_Q8_0, Padded>(const uint8_t *blk, const ActQ &x, int qt) {
-    return q80_quarter(blk, x, qt);
+    return q80_quarter<Padded>(blk, x, qt);
 }
 
 // ---- IQ formats: quarter qt = sub-blocks 2qt and 2qt+1 (32 values each). Per sub-block the integer arithmetic of
@@ -399,6 +425,39 @@ template <int T, class L> __device__ __forceinline__ float quarter_dot(const uin
     return quarter_dot_r<T, L>(blk, act_q(x, bb, qt), qt);
 }
 
+// A Q4_K quarter's weight bytes (header, the 32 code bytes of the quarter), loaded apart from the arithmetic so a caller
+// can have several quarters' loads in flight before the first dot product.
+struct Q4Frag {
+    uint4 h, q0, q1;
+};
+template <class L> __device__ __forceinline__ Q4Frag q4k_frag(const uint8_t *blk, int qt) {
+    return Q4Frag{L::ld(blk), L::ld(blk + 16 + 32 * qt), L::ld(blk + 32 + 32 * qt)};
+}
+// quarter_dot_nc's Q4_K arithmetic on a loaded fragment.
+template <int NC>
+__device__ __forceinline__ void q4k_nc(const Q4Frag &f, const ActImg (&x)[NC], int ncol, int bb, int qt, float (&acc)[NC]) {
+    const uint32_t q[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+    int lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        lo[i] = (int) (q[i] & kLo4);
+        hi[i] = (int) ((q[i] >> 4) & kLo4);
+    }
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+        if (NC == 1 || n < ncol) {
+            const ActQ a = act_q(x[n], bb, qt);
+            int dl = 0, dh = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                dl = dot4(lo[i], a.a[i], dl);
+                dh = dot4(hi[i], a.a[8 + i], dh);
+            }
+            acc[n] += k4_finish(f.h, a, qt, dl, dh);
+        }
+    }
+}
+
 // The same dot for NC activation columns (n < ncol live; NC == 1 ignores ncol): acc[n] += quarter_dot(blk, x[n]).
 // Q4_K reads and unpacks the weight quarter once for all columns; each column's arithmetic is exactly that of
 // quarter_dot (a verify column equals the batch-1 result bit for bit). Other types call quarter_dot per column.
@@ -406,28 +465,7 @@ template <int T, class L, int NC>
 __device__ __forceinline__ void quarter_dot_nc(const uint8_t *blk, const ActImg (&x)[NC], int ncol, int bb, int qt,
                                                float (&acc)[NC]) {
     if constexpr (T == T_Q4_K) {
-        const uint4 h = L::ld(blk);
-        const uint4 q0 = L::ld(blk + 16 + 32 * qt), q1 = L::ld(blk + 32 + 32 * qt);
-        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        int lo[8], hi[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            lo[i] = (int) (q[i] & kLo4);
-            hi[i] = (int) ((q[i] >> 4) & kLo4);
-        }
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            if (NC == 1 || n < ncol) {
-                const ActQ a = act_q(x[n], bb, qt);
-                int dl = 0, dh = 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    dl = dot4(lo[i], a.a[i], dl);
-                    dh = dot4(hi[i], a.a[8 + i], dh);
-                }
-                acc[n] += k4_finish(h, a, qt, dl, dh);
-            }
-        }
+        q4k_nc<NC>(q4k_frag<L>(blk, qt), x, ncol, bb, qt, acc);
     } else {
 #pragma unroll
         for (int n = 0; n < NC; ++n)
