@@ -858,7 +858,8 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
 
     // eight 16-column steps of one half from LDS chunk buf (step i: sub-block 4 h + i / 2, column group 2 hh + i % 2):
     // acc[t][m] += A (hi, lo) x B (integer-scaled codes). Software-pipelined: while the MFMAs of step i issue, the A
-    // fragments of step i + 1 are read from LDS and its B operands decoded (VALU), interleaved one MFMA / a few VALU.
+    // fragments of step i + 1 are read from LDS and its B operands decoded (VALU); the compiler interleaves them
+    // (pinning one MFMA to a fixed number of VALU instructions with scheduling-group barriers measured 2% slower).
     auto load_a = [&](const uint8_t *buf, int i, v8h (&av)[2][NT]) __attribute__((always_inline)) {
         const int piece = a_piece<T>(i, hh);
 #pragma unroll
@@ -899,16 +900,6 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
                     if (i < 7) load_a1(buf, i + 1, x, av[x]);
                 }
                 if (i < 7) {
-#pragma unroll
-                    for (int x = 0; x < 2; ++x) {
-#pragma unroll
-                        for (int k = 0; k < 2 * NT; ++k) {
-                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                            __builtin_amdgcn_sched_group_barrier(0x002, 6 / NT, 0);
-                        }
-#pragma unroll
-                        for (int k = 0; k < NT; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    }
                     b0 = d0;
                     b1 = d1;
                 }
@@ -934,14 +925,6 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
                             acc[t][1] = mfma32(av[x][t], b1.b[g], acc[t][1]);
                         }
                 if (i < 7) {
-                    // order: the 2 NT LDS reads first, then MFMA / VALU groups
-#pragma unroll
-                    for (int k = 0; k < 2 * NT; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-                    for (int k = 0; k < 4 * NT * NB; ++k) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x002, 6 / NT, 0);
-                    }
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         av[0][t] = an[0][t];
@@ -954,6 +937,9 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
         }
     };
 
+    // The scheduling barriers (sched_barrier 0) between the phases below are load-bearing: they keep the compiler from
+    // moving instructions across the explicit vmcnt waits that stand for the DMA and fragment loads (removing them
+    // all fails the GEMM tests).
     // one superblock with fragments f0, f1 (current; their first part loaded) and n0, n1 (next, first part loaded here)
     auto superblock = [&](int kb, WFrag<T> &f0, WFrag<T> &f1, WFrag<T> &n0, WFrag<T> &n1)
                           __attribute__((always_inline)) {
