@@ -1,7 +1,7 @@
 """Pins the CPU oracle (oracle/fns_oracle.c) before it is trusted as the checker.
 
-The reference holds no golden vectors for this path (its parity programs need a GPU and the real GGUF files;
-SURVEY.md section 8c), so each oracle function is pinned here by what fixes it independently:
+The reference holds no golden vectors for this path (its parity programs need a GPU and the real GGUF files),
+so each oracle function is pinned here by what fixes it independently:
   - half precision: exhaustively against numpy's IEEE float16;
   - exp: against float64 math.exp (<= 2 ulp);
   - block dequantisation: hand-built blocks with hand-computed values (the scale/min bit packing, nibble and
