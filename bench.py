@@ -295,8 +295,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the MoE layer would shard "
-              f"experts across GPUs (one expert range per GPU, tokens exchanged all-to-all), which is not built or measured "
-              f"here.", file=sys.stderr)
+              f"experts across GPUs (one expert range per GPU, partial outputs summed by an all-reduce), which is not built "
+              f"or measured here.", file=sys.stderr)
         return 2
 
     import torch
