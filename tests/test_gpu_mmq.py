@@ -320,7 +320,7 @@ def test_moe_prefill_config4_sample(ops):
     """Config 4 shapes (512 tokens, hidden 2048, 128 experts top-8, inter 768, Q4_K) with a Dirichlet-skewed router
     bias: logits against the oracle, ids against the oracle's routing of its own logits (tokens with a clear margin),
     the x image of all 512 tokens byte-exact, 64 tokens (among them every token of the largest expert group up to 40)
-    against the float64 chain, residual added."""
+    against the float64 chain, residual added; then all 512 tokens against the batch-1 decode path."""
     from flintnsteel_amd import synth
     H, F, NE, K, T = 2048, 768, 128, 8, 512
     layer = synth.build_layer(H, F, NE, K, orc.Q4_K, orc.Q4_K, seed=20261022, layer=400)
@@ -349,6 +349,17 @@ def test_moe_prefill_config4_sample(ops):
     tr["out"] = out
     check_prefill_chains(tr, layer, slots_np, xh, toks, ids, orc.Q4_K, orc.Q4_K, H, F, "config-4 prefill sample",
                          resid=host(resid))
+    # all 512 tokens against the batch-1 decode path of the same layer (parity-checked against the oracle on its own):
+    # the tokens both paths route alike agree within the chain bounds (the two paths round act to Q8_1 from different
+    # fp32 sums, so a code can differ by one step)
+    ws1 = layer_b.workspace(1)
+    dec = np.zeros_like(out)
+    same = np.zeros(T, bool)
+    for t in range(T):
+        dec[t] = host(layer_b(x[t:t + 1].contiguous(), ws=ws1, x_resid=resid[t:t + 1].contiguous()))[0]
+        same[t] = np.array_equal(host(layer_b.trace(ws1, 1)["ids"])[0], ids[t])
+    assert same.mean() >= 0.98, f"decode and prefill routing agree on {same.sum()} of {T} tokens"
+    assert_close_chain(out[same] - host(resid)[same], dec[same] - host(resid)[same], "config-4 prefill vs decode, all tokens")
 
 
 def test_moe_prefill_guard_bf16_sigmoid_residual(ops):
