@@ -1313,7 +1313,9 @@ int mmq_quant_image_scaled(const float *x, const float *escale, int64_t ncols, i
 int mmq_compact(const int32_t *ids, int64_t n_tok, int64_t k, int64_t n_expert, int64_t x_rows_per_tok,
                 int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, int32_t *gprefix, hipStream_t st, int32_t *gdone,
                 int n_gdone) {
-    if (!ids || !ids_src1 || !ids_dst || !bounds || !gprefix || n_tok < 0 || k < 1 || n_expert < 1 || n_expert > 256 ||
+    // an empty batch (n_tok = 0) may pass null id arrays: it only writes zero bounds
+    const bool any = n_tok > 0;
+    if ((any && (!ids || !ids_src1 || !ids_dst)) || !bounds || !gprefix || n_tok < 0 || k < 1 || n_expert < 1 || n_expert > 256 ||
         n_tok * k > (1 << 20) || (x_rows_per_tok != 1 && x_rows_per_tok != k))
         return host::set_error(host::ERR_SHAPE, "mmq compaction: bad arguments");
     hipLaunchKernelGGL(k_mmq_compact, dim3(1), dim3(kCompactThreads), 0, st, ids, (int) (n_tok * k), (int) k,

@@ -36,6 +36,8 @@ def host(t):
 
 
 def distinct_ids(rng, n_tok, k, n_expert):
+    if n_tok == 0:
+        return np.zeros((0, k), np.int32)
     return np.stack([rng.permutation(n_expert)[:k] for _ in range(n_tok)]).astype(np.int32)
 
 
@@ -44,7 +46,7 @@ def table_of(mats_dev):
                         dtype=torch.int64, device="cuda")
 
 
-@pytest.mark.parametrize("n_tok,k,n_expert,xr", [(77, 8, 16, 1), (77, 8, 16, 8), (1, 1, 1, 1), (600, 8, 128, 1),
+@pytest.mark.parametrize("n_tok,k,n_expert,xr", [(0, 8, 16, 1), (77, 8, 16, 1), (77, 8, 16, 8), (1, 1, 1, 1), (600, 8, 128, 1),
                                                  (5, 6, 256, 6), (1100, 4, 8, 1), (4096, 8, 128, 1),
                                                  (1024, 8, 128, 1), (1023, 8, 64, 8)])
 def test_compaction_bit_exact(ops, n_tok, k, n_expert, xr):
