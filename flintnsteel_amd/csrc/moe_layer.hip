@@ -731,18 +731,22 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     for (int j = 0; j < K; ++j) mis |= (uintptr_t) (s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd);
     if (SH) mis |= (uintptr_t) (a.shd + (int64_t) r0 * rbd_s);
     const bool staged = (mis & 15u) == 0;
-    // down: wave w takes pieces [w * dn_piece, (w + 1) * dn_piece) of the flattened [K][dn_region] image
+    // down: waves 1-15 take equal shares of the flattened [K][dn_region] image. Wave 0 takes none: its thread 0 polls
+    // the release flag, and a poll's value would wait for every earlier load of its wave, down rows included.
     auto dma_down = [&]() {
+        constexpr int NWD = kQWaves - 1;
+        const int wd = wave - 1;
+        if (wd < 0) return;
         const int per = kFusedRows * nbd, total = K * per;  // blocks of the [K][8 rows] image
-        const int bp = (total + kQWaves - 1) / kQWaves, b_lo = wave * bp, b_hi = min(total, b_lo + bp);
+        const int bp = (total + NWD - 1) / NWD, b_lo = wd * bp, b_hi = min(total, b_lo + bp);
         for (int j = b_lo / per; j < K && j * per < b_hi; ++j) {
             const int lo = max(b_lo - j * per, 0), hi = min(b_hi - j * per, per);
             dma_blocks<TDN>(s_dn + j * dn_region, s_tab[rs.sel[j]] + a.down_off + (int64_t) r0 * rbd, lo, hi);
         }
         if (SH) {  // the shared expert's rows, split over the waves the same way
-            const int ps = kFusedRows * nbd_s, sp = (ps + kQWaves - 1) / kQWaves;
-            dma_blocks<TDN>(s_dn + K * dn_region, a.shd + (int64_t) r0 * rbd_s, min(wave * sp, ps),
-                            min((wave + 1) * sp, ps));
+            const int ps = kFusedRows * nbd_s, sp = (ps + NWD - 1) / NWD;
+            dma_blocks<TDN>(s_dn + K * dn_region, a.shd + (int64_t) r0 * rbd_s, min(wd * sp, ps),
+                            min((wd + 1) * sp, ps));
         }
     };
     // Producers fetch their gate/up rows first and their down rows only once those are consumed: the gate/up bytes,
@@ -830,7 +834,6 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
                                        __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (producer && wave == 0 && staged) dma_down();
     if (tid == 0) {
         const int *sy = a.sync;
         const int *flag = sy + (kSyncGroups + 1 + blockIdx.x % kSyncGroups) * kSyncStride;
