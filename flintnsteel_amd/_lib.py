@@ -54,6 +54,8 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_moe_noalloc_max_bytes": [],
     "fns_hip_moe_layer_status": [_P, _I, _P, _I, _P, _P],
     "fns_hip_moe_set_test_hooks": [_I, _I],
+    "fns_hip_moe_set_path": [_I],
+    "fns_hip_moe_layer_kernels": [_P, _I, _P],
     "fns_hip_mmq_q8_1_bytes": [_I64, _I64],
     "fns_hip_mmq_bounds_bytes": [_I64],
     "fns_hip_mmq": [_I, _P, _I64, _I64, _P, _I64, _P, _P, _P],

@@ -154,6 +154,12 @@ int fns_hip_moe_layer_status(const FnsMoeLayer *layer, int n_tok, void *workspac
     return impl::moe_layer_status(layer, n_tok, workspace, clear, status, S(stream));
 }
 
+int fns_hip_moe_set_path(int path) { return impl::moe_set_path(path); }
+
+int fns_hip_moe_layer_kernels(const FnsMoeLayer *layer, int n_tok, int *kernels) {
+    return impl::moe_layer_kernels(layer, n_tok, kernels);
+}
+
 int fns_hip_moe_set_test_hooks(int spin_limit, int withhold_arrivals) {
     return impl::moe_set_test_hooks(spin_limit, withhold_arrivals);
 }

@@ -79,6 +79,8 @@ int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, i
                 int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, void *xq, float *dst, hipStream_t st);
 int moe_set_test_hooks(int spin_limit, int withhold);
 void moe_test_hooks(int *spin_limit, int *withhold);  // the values set by moe_set_test_hooks
+int moe_set_path(int path);
+int moe_layer_kernels(const FnsMoeLayer *L, int n_tok, int *kernels);
 int moe_layer_status(const FnsMoeLayer *L, int n_tok, void *ws, int clear, uint32_t *status, hipStream_t st);
 int moe_prefill_workspace(const FnsMoeLayer *L, int64_t n_tok, size_t *offsets, size_t *total);
 int moe_prefill_section(const FnsMoeLayer *L, int64_t n_tok, int section, size_t *offset, size_t *bytes);

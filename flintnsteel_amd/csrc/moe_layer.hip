@@ -30,6 +30,8 @@
 
 #include <algorithm>
 #include <mutex>
+
+
 #include <vector>
 
 namespace fns {
@@ -48,6 +50,8 @@ constexpr size_t kLdsBudget = 150 * 1024;  // dynamic LDS per workgroup (gfx950:
 // Fused-kernel synchronisation words, each on its own 256-byte line: 16 group counters, the count of complete groups,
 // and 16 copies of the release flag (workgroups poll copy b % 16, so no line has more than 1/16 of the pollers).
 constexpr int kSyncStride = 64, kSyncGroups = 16, kSyncLines = 2 * kSyncGroups + 1;
+// Decode path override (fns_hip_moe_set_path test hook): 0 automatic, 1 never the fused kernel.
+int g_path_override = 0;
 
 struct LayerArgs {
     int H, F, NE, K, T;
@@ -931,6 +935,12 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     FNS_MARK(1, blockIdx.x, 13);
 }
 
+// Fixed header at the start of every workspace, whatever the layer's shape: the fused kernel's counters and flags
+// (kSyncLines lines, zeroed by the router kernel each call), then the sticky status line (not cleared per call). A
+// workspace (or the no-allocation scratch) shared by layers of different shapes keeps these words at the same places.
+constexpr size_t kHdrSyncOff = 0, kHdrStatusOff = (size_t) kSyncLines * kSyncStride * 4;
+constexpr size_t kHeaderBytes = (kHdrStatusOff + (size_t) kSyncStride * 4 + 255) / 256 * 256;
+
 // Fused-kernel plan for one layer shape (n_tok = 1): LDS bytes, or 0 when the shape does not fit the scheme.
 // Fs > 0: with the shared expert (width Fs, the routed types) as slot K.
 // Bytes per block of the fused kernel's LDS weight images (kStageBytes of the type).
@@ -1041,7 +1051,7 @@ int resident_groups(const void *fn, size_t lds) {
 
 // True when this call (n_tok = 1, a shape that fits) takes the fused kernel.
 bool use_fused(const FnsMoeLayer *L, const LayerArgs &a) {
-    if (!a.fused) return false;
+    if (!a.fused || g_path_override == 1) return false;
     const size_t lds = fused_lds(a.H, a.F, a.K, stage_bytes_of(L->gu_type), stage_bytes_of(L->down_type), a.shd ? a.Fs : 0);
     const void *fn = fused_kernel(L->gu_type, L->down_type, a.shd != nullptr);
     return fn && resident_groups(fn, lds) >= a.H / kFusedRows;
@@ -1108,7 +1118,7 @@ void section_sizes(const FnsMoeLayer *L, int n_tok, size_t *sizes) {
     sizes[7] = ch * img_bytes((int) fpad) + (L->shexp_inter > 0 ? img_bytes((int) host::pad512(L->shexp_inter)) : 0);
     sizes[8] = ch * (fpad / 32) * 4;
     sizes[9] = ch * 8;
-    sizes[10] = (size_t) (kSyncLines + 1) * kSyncStride * 4;  // + the status line (not cleared per call)
+    sizes[10] = 0;  // (the synchronisation words live in the fixed header before section 0)
     sizes[11] = (size_t) (kMaxCh * kChanInts + 2) * 4;
     const size_t fs = L->shexp_inter > 0 ? (size_t) L->shexp_inter : 0;
     sizes[12] = 0;  // (unused: the router kernel applies the RMSNorm)
@@ -1131,7 +1141,7 @@ int moe_workspace_layout(const FnsMoeLayer *L, int n_tok, size_t *offsets, size_
         return host::set_error(host::ERR_SHAPE, "moe_layer: bad shape");
     size_t sizes[kSections];
     section_sizes(L, n_tok, sizes);
-    size_t off = 0;
+    size_t off = kHeaderBytes;
     for (int i = 0; i < kSections; ++i) {
         if (offsets && i < 6) offsets[i] = off;
         off += align256(sizes[i]);
@@ -1186,7 +1196,7 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     size_t sizes[kSections];
     section_sizes(L, n_tok, sizes);
     uint8_t *sec[kSections];
-    size_t off = 0;
+    size_t off = kHeaderBytes;
     for (int i = 0; i < kSections; ++i) {
         sec[i] = (uint8_t *) ws + off;
         off += align256(sizes[i]);
@@ -1220,7 +1230,7 @@ static int prepare(const FnsMoeLayer *L, const float *x, const float *x_resid, f
     a.apack = sec[7];
     a.blk_amax = (float *) sec[8];
     a.dptr = (const uint8_t **) sec[9];
-    a.sync = (int *) sec[10];
+    a.sync = (int *) ((uint8_t *) ws + kHdrSyncOff);  // the status word follows at kHdrStatusOff
     a.spin_limit = g_spin_limit;
     a.withhold = g_withhold;
     a.chan = (int *) sec[11];
@@ -1398,20 +1408,35 @@ int iq_grids_upload_layer(const void *grids) {
 // so far has completed; clear: zero it afterwards (a kernel on `st`).
 int moe_layer_status(const FnsMoeLayer *L, int n_tok, void *ws, int clear, uint32_t *status, hipStream_t st) {
     if (!status) return host::set_error(host::ERR_SHAPE, "moe_layer_status: null status");
-    size_t sizes[kSections];
     FNS_TRY(moe_workspace_layout(L, n_tok, nullptr, nullptr));
-    section_sizes(L, n_tok, sizes);
-    size_t off = 0;
-    for (int i = 0; i < 10; ++i) off += align256(sizes[i]);
     uint8_t *base = (uint8_t *) ws;
     if (!base) FNS_TRY(scratch_of_device(st, &base));
-    uint32_t *word = (uint32_t *) (base + off) + kSyncLines * kSyncStride;
+    uint32_t *word = (uint32_t *) (base + kHdrStatusOff);  // the fixed header: the same place for every shape
     if (hipMemcpyAsync(status, word, 4, hipMemcpyDeviceToHost, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
         return host::set_error(host::ERR_LAUNCH, "moe_layer_status: reading the status word failed");
     if (clear) {
         hipLaunchKernelGGL(k_zero_words, dim3(1), dim3(64), 0, st, word, (size_t) 1);
         FNS_TRY(host::check_launch("moe_layer_status: clearing"));
     }
+    return host::OK;
+}
+
+int moe_set_path(int path) {
+    if (path < 0 || path > 1) return host::set_error(host::ERR_SHAPE, "moe_set_path: path must be 0 or 1");
+    g_path_override = path;
+    return host::OK;
+}
+
+int moe_layer_kernels(const FnsMoeLayer *L, int n_tok, int *kernels) {
+    if (!kernels) return host::set_error(host::ERR_SHAPE, "moe_layer_kernels: null result");
+    FNS_TRY(moe_workspace_layout(L, n_tok, nullptr, nullptr));
+    // prepare() needs real pointers only for its null checks: a dummy workspace of the right size stands in
+    size_t total = 0;
+    FNS_TRY(moe_workspace_layout(L, n_tok, nullptr, &total));
+    LayerArgs a;
+    static float dummy;
+    FNS_TRY(prepare(L, &dummy, nullptr, &dummy, n_tok, (void *) &dummy, total, a));
+    *kernels = use_fused(L, a) ? 2 : 3;
     return host::OK;
 }
 

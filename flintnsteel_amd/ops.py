@@ -252,6 +252,23 @@ class MoeLayerDesc(ctypes.Structure):
 
 WS_SECTIONS = ("logits", "xq", "ids", "w", "act", "escale")
 
+PATH_AUTO, PATH_THREE_KERNELS = 0, 1
+
+
+class decode_path:
+    """Context manager (test hook fns_hip_moe_set_path): restricts the decode path of the calls inside it."""
+
+    def __init__(self, path: int):
+        self.path = path
+
+    def __enter__(self):
+        call("fns_hip_moe_set_path", self.path)
+        return self
+
+    def __exit__(self, *exc):
+        call("fns_hip_moe_set_path", PATH_AUTO)
+        return False
+
 
 class MoeLayer:
     """One MoE FFN layer resident in HBM: fp32/bf16 router + expert slots, run by fns_hip_moe_layer."""
@@ -317,6 +334,13 @@ class MoeLayer:
         st = ctypes.c_uint32()
         call("fns_hip_moe_layer_status", ctypes.byref(self.desc), n_tok, _p(ws), int(clear), ctypes.byref(st), _s())
         return st.value
+
+    def kernels(self, n_tok: int = 1) -> int:
+        """Kernels one call at n_tok tokens launches on the current device: 2 (router + fused layer) or 3 (router,
+        gate/up, down)."""
+        k = ctypes.c_int()
+        call("fns_hip_moe_layer_kernels", ctypes.byref(self.desc), n_tok, ctypes.byref(k))
+        return k.value
 
     def stage(self, stage: int, x: torch.Tensor, out: torch.Tensor, ws: torch.Tensor,
               x_resid: torch.Tensor | None = None) -> None:

@@ -175,9 +175,17 @@ int fns_hip_moe_layer_status(const FnsMoeLayer *layer, int n_tok, void *workspac
  * spin_limit polls) for the calls that follow; the failure path is then exercised with every kernel exiting normally.
  * Process-wide; set it only while no other thread launches layers. */
 int fns_hip_moe_set_test_hooks(int spin_limit, int withhold_arrivals);
+/* No counterpart in the reference: how many kernels a call of this layer at n_tok tokens launches on the current
+ * device - 2 (n_tok = 1 and a shape the fused kernel holds, all its workgroups resident: router kernel + fused layer
+ * kernel) or 3 (router, gate/up, down). Both give the same results bit for bit. */
+int fns_hip_moe_layer_kernels(const FnsMoeLayer *layer, int n_tok, int *kernels);
+/* Test hook, no counterpart in the reference: restricts the decode path for the calls that follow (0: automatic,
+ * 1: never the fused kernel - the three-kernel path). Process-wide, like fns_hip_moe_set_test_hooks. */
+int fns_hip_moe_set_path(int path);
 /* One of the three kernels of fns_hip_moe_layer (stage 0 router + Q8_1 of x, 1 routing + gate/up + SwiGLU,
  * 2 F16 guard + Q8_1 of act + down + combine), each reading what the previous stage left in the workspace:
- * per-stage tracing (the reference's FNS_TRACE nodes, src/engine.cu:590-599) and per-kernel timing. */
+ * per-stage tracing (the reference's FNS_TRACE nodes, src/engine.cu:590-599) and per-kernel timing. A call that takes
+ * the fused kernel (fns_hip_moe_layer_kernels = 2) launches it at stage 1; stage 2 then launches nothing. */
 int fns_hip_moe_layer_stage(const FnsMoeLayer *layer, int stage, const float *x, const float *x_resid, float *out,
                             int n_tok, void *workspace, size_t workspace_bytes, void *stream);
 
