@@ -183,9 +183,16 @@ Gguf::Gguf(const std::string &path) : path_(path) {
             const size_t row = ggml_row_bytes(t.type, t.ne[0]);
             if (!row) c.fail("tensor " + t.name + ": type " + std::to_string(t.type) + " with ne0 " +
                              std::to_string(t.ne[0]) + " is not supported");
-            const unsigned __int128 nb = (unsigned __int128) row * (uint64_t) t.ne[1] * (uint64_t) t.ne[2] *
-                                         (uint64_t) t.ne[3];
-            if (nb > (unsigned __int128) size_) c.fail("tensor " + t.name + ": larger than the file");
+            // row * ne1 * ne2 * ne3, one factor at a time: any partial product beyond the file size is rejected
+            // before the next multiplication, so nothing wraps (each factor is at most 2^40, the file below 2^64)
+            uint64_t nb = (uint64_t) row;
+            for (int d = 1; d < 4; ++d) {
+                uint64_t next = 0;
+                if (__builtin_mul_overflow(nb, (uint64_t) t.ne[d], &next) || next > (uint64_t) size_)
+                    c.fail("tensor " + t.name + ": larger than the file");
+                nb = next;
+            }
+            if (nb > (uint64_t) size_) c.fail("tensor " + t.name + ": larger than the file");
             t.nbytes = (size_t) nb;
             if (t.offset % alignment_) c.fail("tensor " + t.name + ": offset not aligned");
         }

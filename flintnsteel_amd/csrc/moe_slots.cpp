@@ -72,6 +72,9 @@ void build_resident_moe_layer(const Gguf &f, int il, ResidentMoeLayer &out) {
     if (k < 1 || k > NE) fail(il, "bad expert_used_count");
     const uint32_t gf = f.get_u32_or(arch + ".expert_gating_func", arch == "flint" ? 2u : 1u);
     if (gf != 1 && gf != 2) fail(il, "expert_gating_func must be 1 (softmax) or 2 (sigmoid)");
+    // the reference requires an expert weight scale of 1 (src/model.cpp:83,167): the combine applies none
+    const float ews = f.get_f32_or(arch + ".expert_weights_scale", 1.0f);
+    if (ews != 1.0f) fail(il, "expert_weights_scale " + std::to_string(ews) + " is not 1 (the combine applies no scale)");
 
     out.hidden = (int) H;
     out.inter = (int) F;

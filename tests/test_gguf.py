@@ -21,7 +21,7 @@ H, F, NE, K, FS = 512, 256, 16, 4, 512
 
 
 def _moe_file(path, arch="flint", gating=None, gu=orc.Q4_K, dn=orc.Q6_K, router_dtype=BF16, with_shexp=True,
-              with_bias=True, layer=1, seed=3, alignment=32):
+              with_bias=True, layer=1, seed=3, alignment=32, extra_kv=()):
     """A checkpoint with one MoE block at blk.<layer> (Flint tensor names and metadata) and the arrays it holds."""
     rng = np.random.default_rng(seed)
     w = lambda *s: rng.normal(0, 0.02, s).astype(np.float32)  # noqa: E731
@@ -53,6 +53,7 @@ def _moe_file(path, arch="flint", gating=None, gu=orc.Q4_K, dn=orc.Q6_K, router_
           ("tokenizer.ggml.tokens", GGUF_ARRAY, (GGUF_STRING, ["<s>", "a", "b"]))]
     if gating is not None:
         kv.append((f"{arch}.expert_gating_func", GGUF_U32, gating))
+    kv += list(extra_kv)
     # a tensor of another kind first, so the MoE tensors sit at non-zero offsets
     tensors.insert(0, ("token_embd.weight", 8, [H, 3], np.zeros(3 * H // 32 * 34, np.uint8) + 7))  # Q8_0
     write_gguf(path, kv, tensors, alignment=alignment)
@@ -104,6 +105,37 @@ def test_reader_rejects_malformed_files(tmp_path):
             ops.GgufFile(p)
     with pytest.raises(FnsError, match="cannot open"):
         ops.GgufFile(tmp_path / "missing.gguf")
+
+
+def test_reader_rejects_sizes_that_would_wrap(tmp_path):
+    """A tensor whose dimensions multiply past 2^128 bytes (each one allowed, 2^40: 2^42-byte f32 rows x 2^120 = 2^162,
+    which a 128-bit product wraps to 0) is rejected as larger than the file instead of wrapping to a small byte count
+    (the product is checked one factor at a time); so is one past 2^64."""
+    from flintnsteel_amd import ops
+    from flintnsteel_amd._lib import FnsError
+    p = tmp_path / "huge.gguf"
+    big = 1 << 40
+    write_gguf(p, [("general.architecture", GGUF_STRING, "flint")],
+               [("blk.0.huge.weight", F32, [big, big, big, big], np.zeros(64, np.float32))])
+    with pytest.raises(FnsError, match="larger than the file"):
+        ops.GgufFile(p)
+    p2 = tmp_path / "wrap.gguf"  # 2^40 x 2^24 f32 = 2^66 bytes: a plain 64-bit product would wrap to 0
+    write_gguf(p2, [("general.architecture", GGUF_STRING, "flint")],
+               [("blk.0.wrap.weight", F32, [big, 1 << 24], np.zeros(64, np.float32))])
+    with pytest.raises(FnsError, match="larger than the file"):
+        ops.GgufFile(p2)
+
+
+def test_layer_build_rejects_expert_weights_scale(tmp_path):
+    """The reference requires <arch>.expert_weights_scale == 1 (src/model.cpp:83,167); the combine applies no scale,
+    so a checkpoint with another value is rejected (CPU: the check runs before any device allocation)."""
+    from flintnsteel_amd import ops
+    from flintnsteel_amd._lib import FnsError
+    p = tmp_path / "scaled.gguf"
+    _moe_file(p, with_shexp=False, extra_kv=[("flint.expert_weights_scale", GGUF_F32, 2.5)])
+    f = ops.GgufFile(p)
+    with pytest.raises(FnsError, match="expert_weights_scale"):
+        ops.MoeLayer.from_gguf(f, 1)
 
 
 def test_layer_build_rejects_unsupported_checkpoints(tmp_path):
