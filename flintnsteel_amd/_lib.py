@@ -79,6 +79,12 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_gguf_get_str": [_P, ctypes.c_char_p, _P],
     "fns_hip_moe_layer_from_gguf": [_P, _I, _P, _P],
     "fns_hip_moe_resident_free": [_P],
+    "fns_hip_add": [_P, _P, _P, _I64, _P],
+    "fns_hip_dense_ffn_workspace": [_P, _I64, _P],
+    "fns_hip_dense_ffn": [_P, _P, _P, _I64, _P, _SZ, _P],
+    "fns_hip_dense_ffn_prefill": [_P, _P, _P, _I64, _P, _SZ, _P],
+    "fns_hip_dense_ffn_from_gguf": [_P, _I, _P, _P],
+    "fns_hip_dense_resident_free": [_P],
 }
 _RESTYPE = {
     "fns_hip_last_error": ctypes.c_char_p,
@@ -88,6 +94,7 @@ _RESTYPE = {
     "fns_hip_moe_noalloc_max_bytes": _SZ,
     "fns_hip_gguf_close": None,
     "fns_hip_moe_resident_free": None,
+    "fns_hip_dense_resident_free": None,
 }
 
 _lib = None

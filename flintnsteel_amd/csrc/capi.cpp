@@ -209,6 +209,24 @@ int fns_hip_moe_prefill_section(const FnsMoeLayer *layer, int64_t n_tok, int sec
     return impl::moe_prefill_section(layer, n_tok, section, offset, bytes);
 }
 
+int fns_hip_add(const float *x, const float *y, float *out, int64_t n, void *stream) {
+    return impl::add(x, y, out, n, S(stream));
+}
+
+int fns_hip_dense_ffn_workspace(const FnsDenseFfn *ffn, int64_t n_tok, size_t *total_bytes) {
+    return impl::dense_ffn_workspace(ffn, n_tok, total_bytes);
+}
+
+int fns_hip_dense_ffn(const FnsDenseFfn *ffn, const float *x, float *out, int64_t n_tok, void *workspace,
+                      size_t workspace_bytes, void *stream) {
+    return impl::dense_ffn(ffn, x, out, n_tok, workspace, workspace_bytes, false, S(stream));
+}
+
+int fns_hip_dense_ffn_prefill(const FnsDenseFfn *ffn, const float *x, float *out, int64_t n_tok, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+    return impl::dense_ffn(ffn, x, out, n_tok, workspace, workspace_bytes, true, S(stream));
+}
+
 int fns_hip_moe_prefill_status(const FnsMoeLayer *layer, int64_t n_tok, void *workspace, int clear, uint32_t *status,
                                void *stream) {
     return impl::moe_prefill_status(layer, n_tok, workspace, clear, status, S(stream));

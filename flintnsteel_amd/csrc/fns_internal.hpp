@@ -18,6 +18,7 @@ int amax_guard(float *act, float *escale, int n, int rows, hipStream_t st);
 int amax_guard_q8_1(const float *act, float *escale, void *xq, int n, int rows, hipStream_t st);
 int swiglu(const float *g, const float *u, float *act, int n, int rows, hipStream_t st);
 int glu_mmvq(const float *g, const float *u, float *act, int n, hipStream_t st);
+int add(const float *x, const float *y, float *out, int64_t n, hipStream_t st);
 
 int mmvq(int type, const void *w, int64_t ncols, int64_t nrows, const void *xq, float *dst, int64_t n_cols,
          hipStream_t st);
@@ -87,6 +88,10 @@ int moe_prefill_section(const FnsMoeLayer *L, int64_t n_tok, int section, size_t
 int moe_prefill_status(const FnsMoeLayer *L, int64_t n_tok, void *ws, int clear, uint32_t *status, hipStream_t st);
 int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int64_t n_tok, void *ws,
                 size_t ws_bytes, hipStream_t st);
+
+int dense_ffn_workspace(const FnsDenseFfn *D, int64_t n_tok, size_t *total);
+int dense_ffn(const FnsDenseFfn *D, const float *x, float *out, int64_t n_tok, void *ws, size_t ws_bytes, bool prefill,
+              hipStream_t st);
 
 int fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t st);
 int quantize_weights(int type, const float *x, void *out, int64_t nrows, int64_t ncols, hipStream_t st);

@@ -1,4 +1,4 @@
-// gguf_capi.cpp - extern "C" entry points of the GGUF reader and the resident MoE layer (include/fns_hip.h): thin
+// gguf_capi.cpp - extern "C" entry points of the GGUF reader and the resident MoE and dense FFN layers (include/fns_hip.h): thin
 // forwards to include/fns/gguf.h; exceptions become FNS_ERR_IO / FNS_ERR_SHAPE with their message kept for
 // fns_hip_last_error().
 #include <cstring>
@@ -18,6 +18,9 @@ struct FnsGguf {
 };
 struct FnsMoeResident {
     ResidentMoeLayer layer;
+};
+struct FnsDenseResident {
+    ResidentDenseFfn ffn;
 };
 
 namespace {
@@ -151,5 +154,35 @@ int fns_hip_moe_layer_from_gguf(const FnsGguf *file, int layer, FnsMoeResident *
 }
 
 void fns_hip_moe_resident_free(FnsMoeResident *resident) { delete resident; }
+
+int fns_hip_dense_ffn_from_gguf(const FnsGguf *file, int layer, FnsDenseResident **resident, FnsDenseFfn *desc) {
+    if (!file || !resident || !desc) return host::set_error(host::ERR_SHAPE, "dense_ffn_from_gguf: null argument");
+    *resident = nullptr;
+    return guarded(FNS_ERR_IO, [&] {
+        FnsDenseResident *r = new FnsDenseResident;
+        try {
+            build_resident_dense_ffn(file->file, layer, r->ffn);
+        } catch (...) {
+            delete r;
+            throw;
+        }
+        const ResidentDenseFfn &D = r->ffn;
+        std::memset(desc, 0, sizeof *desc);
+        desc->hidden = D.hidden;
+        desc->inter = D.inter;
+        desc->gate_type = D.gate_type;
+        desc->up_type = D.up_type;
+        desc->down_type = D.down_type;
+        desc->gate = D.gate;
+        desc->up = D.up;
+        desc->down = D.down;
+        desc->ffn_norm = D.ffn_norm;
+        desc->norm_eps = D.norm_eps;
+        *resident = r;
+        return host::OK;
+    });
+}
+
+void fns_hip_dense_resident_free(FnsDenseResident *resident) { delete resident; }
 
 }  // extern "C"

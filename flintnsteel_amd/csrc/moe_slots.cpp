@@ -1,5 +1,6 @@
 // moe_slots.cpp - one MoE layer of a GGUF checkpoint made fully resident in HBM: expert slots [gate | up | down],
-// the device table of slot pointers, router, RMSNorm weights and shared expert (include/fns/gguf.h).
+// the device table of slot pointers, router, RMSNorm weights and shared expert; and a dense FFN layer's matrices
+// (include/fns/gguf.h).
 // Reference: /root/reference/src/engine.cu:375-471 (Engine::place_experts; here every expert is resident),
 // src/model.cpp:120-129,159-178 (tensor names, shapes, types and the mmvq_supports check).
 #include "fns/gguf.h"
@@ -17,8 +18,8 @@ namespace {
 
 constexpr size_t kAlign = 256, kPad = 4096;  // slot alignment and trailing zero bytes (reference src/engine.cu:381)
 
-[[noreturn]] void fail(int il, const std::string &what) {
-    throw std::runtime_error("MoE layer " + std::to_string(il) + ": " + what);
+[[noreturn]] void fail(int il, const std::string &what, const char *kind = "MoE layer ") {
+    throw std::runtime_error(kind + std::to_string(il) + ": " + what);
 }
 void hip_ok(hipError_t e, const char *what) {
     if (e != hipSuccess) throw std::runtime_error(std::string("MoE layer build: ") + what + ": " + hipGetErrorString(e));
@@ -33,12 +34,12 @@ void *upload(const void *src, size_t n) {
     }
     return d;
 }
-void check_shape(int il, const GgufTensor &t, std::initializer_list<int64_t> ne) {
+void check_shape(int il, const GgufTensor &t, std::initializer_list<int64_t> ne, const char *kind = "MoE layer ") {
     int d = 0;
     for (int64_t v : ne)
-        if (t.ne[d++] != v) fail(il, "unexpected shape of " + t.name);
+        if (t.ne[d++] != v) fail(il, "unexpected shape of " + t.name, kind);
     for (; d < 4; ++d)
-        if (t.ne[d] != 1) fail(il, "unexpected shape of " + t.name);
+        if (t.ne[d] != 1) fail(il, "unexpected shape of " + t.name, kind);
 }
 
 }  // namespace
@@ -136,6 +137,46 @@ void build_resident_moe_layer(const Gguf &f, int il, ResidentMoeLayer &out) {
         out.shexp_up = upload(su.data, su.nbytes);
         out.shexp_down = upload(sd.data, sd.nbytes);
     }
+}
+
+ResidentDenseFfn::~ResidentDenseFfn() {
+    for (void *p : {gate, up, down, (void *) ffn_norm})
+        if (p) (void) hipFree(p);
+}
+
+void build_resident_dense_ffn(const Gguf &f, int il, ResidentDenseFfn &out) {
+    const std::string arch = f.get_str("general.architecture");
+    const std::string p = "blk." + std::to_string(il) + ".";
+    constexpr const char *kind = "dense FFN layer ";
+    auto failf = [&](const std::string &what) { fail(il, what, kind); };
+    const GgufTensor &g = f.get_tensor(p + "ffn_gate.weight");
+    const GgufTensor &u = f.get_tensor(p + "ffn_up.weight");
+    const GgufTensor &dn = f.get_tensor(p + "ffn_down.weight");
+    const int64_t H = g.ne[0], F = g.ne[1];
+    check_shape(il, g, {H, F}, kind);
+    check_shape(il, u, {H, F}, kind);
+    check_shape(il, dn, {F, H}, kind);
+    if (H <= 0 || H % 256 || F <= 0 || F % 256 || H > 65536 || F > 65536)
+        failf("hidden and inter must be multiples of 256 (<= 65536)");
+    for (const GgufTensor *t : {&g, &u, &dn})
+        if (!host::is_supported(t->type))
+            failf("type " + std::to_string(t->type) + " of " + t->name + " is not supported by the GEMV kernels "
+                  "(mmvq_supports)");
+    const GgufTensor *n = f.find_tensor(p + "ffn_norm.weight");
+    if (n) {
+        check_shape(il, *n, {H}, kind);
+        if (n->type != 0) failf("ffn_norm.weight must be F32");
+    }
+    out.hidden = (int) H;
+    out.inter = (int) F;
+    out.gate_type = g.type;
+    out.up_type = u.type;
+    out.down_type = dn.type;
+    out.norm_eps = f.get_f32_or(arch + ".attention.layer_norm_rms_epsilon", 1e-6f);
+    out.gate = upload(g.data, g.nbytes);
+    out.up = upload(u.data, u.nbytes);
+    out.down = upload(dn.data, dn.nbytes);
+    if (n) out.ffn_norm = (float *) upload(n->data, n->nbytes);
 }
 
 }  // namespace fns

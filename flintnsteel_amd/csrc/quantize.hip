@@ -112,6 +112,19 @@ __global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ 
     act[i] = x / (1.0f + fns_expf(-x)) * u[i];
 }
 
+// out = x + y, four elements per thread (n4 = n / 4 float4s), then the tail
+__global__ void k_add(const float *x, const float *y, float *out, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t n4 = n / 4;
+    if (i < n4) {
+        const float4 a = ((const float4 *) x)[i], b = ((const float4 *) y)[i];
+        ((float4 *) out)[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    } else if (i < n4 + n % 4) {
+        const int64_t j = 4 * n4 + (i - n4);
+        out[j] = x[j] + y[j];
+    }
+}
+
 __global__ void k_glu_mmvq(const float *__restrict__ g, const float *u, float *act, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -167,6 +180,16 @@ int swiglu(const float *g, const float *u, float *act, int n, int rows, hipStrea
     if (total == 0) return host::OK;
     hipLaunchKernelGGL(k_swiglu, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, st, g, u, act, total);
     return host::check_launch("swiglu");
+}
+
+int add(const float *x, const float *y, float *out, int64_t n, hipStream_t st) {
+    if (!x || !y || !out || n < 0) return host::set_error(host::ERR_SHAPE, "add: bad arguments");
+    if (((uintptr_t) x | (uintptr_t) y | (uintptr_t) out) % 16)
+        return host::set_error(host::ERR_SHAPE, "add: arrays must be 16-byte aligned");
+    if (n == 0) return host::OK;
+    const int64_t threads = n / 4 + n % 4;
+    hipLaunchKernelGGL(k_add, dim3((unsigned) ((threads + 255) / 256)), dim3(256), 0, st, x, y, out, n);
+    return host::check_launch("add");
 }
 
 int glu_mmvq(const float *g, const float *u, float *act, int n, hipStream_t st) {

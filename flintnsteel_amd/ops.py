@@ -495,6 +495,65 @@ def selftest_lanes() -> int:
     return int(bad.item())
 
 
+def add(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = x + y (reference add_inplace, src/kernels.cuh:119); out may be x."""
+    out = torch.empty_like(x) if out is None else out
+    call("fns_hip_add", _p(x), _p(y), _p(out), x.numel(), _s())
+    return out
+
+
+class DenseFfnDesc(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("inter", ctypes.c_int), ("gate_type", ctypes.c_int),
+                ("up_type", ctypes.c_int), ("down_type", ctypes.c_int), ("gate", ctypes.c_void_p),
+                ("up", ctypes.c_void_p), ("down", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p),
+                ("norm_eps", ctypes.c_float)]
+
+
+class DenseFfn:
+    """A dense FFN layer (the reference model's leading dense blocks, src/engine.cu:655-667 decode and :331-337
+    prefill): out = x + down . q8_1(silu(gate . q8_1(h)) * (up . q8_1(h))), h = RMSNorm(x) * ffn_norm."""
+
+    def __init__(self, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor, gate_type: int, up_type: int,
+                 down_type: int, hidden: int, inter: int, ffn_norm: torch.Tensor | None = None,
+                 norm_eps: float = 1e-6):
+        self.gate, self.up, self.down, self.ffn_norm = gate, up, down, ffn_norm
+        self.desc = DenseFfnDesc(hidden, inter, gate_type, up_type, down_type, gate.data_ptr(), up.data_ptr(),
+                                 down.data_ptr(), ffn_norm.data_ptr() if ffn_norm is not None else None, norm_eps)
+
+    @classmethod
+    def from_gguf(cls, file: "GgufFile", layer: int) -> "DenseFfn":
+        """Dense layer `layer` of a GGUF checkpoint made resident by fns_hip_dense_ffn_from_gguf."""
+        obj = cls.__new__(cls)
+        obj.desc = DenseFfnDesc()
+        obj.gate = obj.up = obj.down = obj.ffn_norm = None
+        obj._file = file
+        res = ctypes.c_void_p()
+        call("fns_hip_dense_ffn_from_gguf", file.handle, layer, ctypes.byref(res), ctypes.byref(obj.desc))
+        obj._resident = res
+        return obj
+
+    def __del__(self):
+        res = getattr(self, "_resident", None)
+        if res:
+            lib().fns_hip_dense_resident_free(res)
+            self._resident = None
+
+    def workspace(self, n_tok: int) -> torch.Tensor:
+        total = ctypes.c_size_t()
+        call("fns_hip_dense_ffn_workspace", ctypes.byref(self.desc), n_tok, ctypes.byref(total))
+        return torch.empty(total.value, dtype=torch.uint8, device="cuda")
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
+                 prefill: bool = False) -> torch.Tensor:
+        x = x.contiguous()
+        n_tok = x.numel() // self.desc.hidden
+        out = torch.empty_like(x) if out is None else out
+        ws = self.workspace(n_tok) if ws is None else ws
+        call("fns_hip_dense_ffn_prefill" if prefill else "fns_hip_dense_ffn", ctypes.byref(self.desc), _p(x),
+             _p(out), n_tok, _p(ws), ws.numel(), _s())
+        return out
+
+
 class GgufTensorInfo(ctypes.Structure):
     """Mirror of FnsGgufTensorInfo (include/fns_hip.h)."""
     _fields_ = [("type", ctypes.c_int), ("n_dims", ctypes.c_int), ("ne", ctypes.c_int64 * 4),

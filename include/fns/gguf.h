@@ -137,4 +137,26 @@ struct ResidentMoeLayer {
 // std::runtime_error on a missing tensor, a shape or type mismatch or a HIP failure.
 void build_resident_moe_layer(const Gguf &file, int il, ResidentMoeLayer &out);
 
+// A dense FFN block of the reference model (its leading dense layers, src/model.cpp:120-125): blk.N.ffn_gate.weight,
+// ffn_up.weight ([inter][hidden] blocks), ffn_down.weight ([hidden][inter]) and ffn_norm.weight copied into HBM.
+// Device memory is owned by this object and freed by its destructor.
+struct ResidentDenseFfn {
+    int hidden = 0, inter = 0;
+    int gate_type = -1, up_type = -1, down_type = -1;
+    float norm_eps = 0.0f;
+    void *gate = nullptr, *up = nullptr, *down = nullptr;
+    float *ffn_norm = nullptr;  // [hidden] or null
+
+    ResidentDenseFfn() = default;
+    ResidentDenseFfn(const ResidentDenseFfn &) = delete;
+    ResidentDenseFfn &operator=(const ResidentDenseFfn &) = delete;
+    ~ResidentDenseFfn();
+};
+
+// Builds dense layer `il`: shapes checked against each other (hidden and inter multiples of 256), types against the
+// GEMV kernels (mmvq_supports, as the reference's check, src/model.cpp:193-196); the epsilon from
+// <arch>.attention.layer_norm_rms_epsilon. Throws std::runtime_error on a missing tensor, a mismatch or a HIP failure;
+// every check runs before the first device allocation.
+void build_resident_dense_ffn(const Gguf &file, int il, ResidentDenseFfn &out);
+
 }  // namespace fns

@@ -241,6 +241,32 @@ int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x
 int fns_hip_moe_prefill_status(const FnsMoeLayer *layer, int64_t n_tok, void *workspace, int clear, uint32_t *status,
                                void *stream);
 
+/* --- dense FFN layer (the reference model's leading dense blocks) ---
+ * The dense branch of the reference's Engine::ffn_block (src/engine.cu:655-667: rms_norm_q8_1, dense_glu
+ * (src/engine.cu:644-653: mmvq_swiglu at one column, else two mmvq and glu_mmvq), gemv of ffn_down (quantize_q8_1 +
+ * mmvq, src/engine.cu:585-588), add_inplace) and of Engine::prefill_chunk (src/engine.cu:331-337: rms_norm_mul, mmq of
+ * ffn_gate and ffn_up, swiglu, mmq of ffn_down, add_inplace):
+ *   out[t] = x[t] + down . q8_1(silu(gate . q8_1(h[t])) * (up . q8_1(h[t]))), h = RMSNorm(x) * ffn_norm (or x).
+ * Matrices are GGUF blocks: gate and up [inter][hidden], down [hidden][inter]; any type of the GEMV kernels
+ * (fns_hip_mmvq_supports) for the decode form, any type of fns_hip_mmq for the prefill form. out may alias x. */
+typedef struct FnsDenseFfn {
+    int hidden, inter;                 /* positive multiples of 256 */
+    int gate_type, up_type, down_type; /* ggml types */
+    const void *gate, *up, *down;
+    const float *ffn_norm;             /* NULL or f32 [hidden] */
+    float norm_eps;
+} FnsDenseFfn;
+/* Device bytes of the workspace of either form at n_tok tokens (no zero-fill needed). */
+int fns_hip_dense_ffn_workspace(const FnsDenseFfn *ffn, int64_t n_tok, size_t *total_bytes);
+/* Decode / verify form (the reference's forward at cols_ = n_tok columns). */
+int fns_hip_dense_ffn(const FnsDenseFfn *ffn, const float *x, float *out, int64_t n_tok, void *workspace,
+                      size_t workspace_bytes, void *stream);
+/* Prefill form (the MMQ GEMMs). */
+int fns_hip_dense_ffn_prefill(const FnsDenseFfn *ffn, const float *x, float *out, int64_t n_tok, void *workspace,
+                              size_t workspace_bytes, void *stream);
+/* src/kernels.cuh:119 add_inplace, out-of-place: out[i] = x[i] + y[i]; out may alias x. */
+int fns_hip_add(const float *x, const float *y, float *out, int64_t n, void *stream);
+
 /* --- GGUF checkpoints: reader and fully resident MoE layers ---
  * Replaces the reference's loader (src/model.cpp:30-136: gguf header and tensor table, the file mapped without copying)
  * and expert placement (src/engine.cu:375-471: slots [gate | up | down] 256-byte aligned with 4096 zero bytes after the
@@ -277,6 +303,12 @@ int fns_hip_gguf_get_str(const FnsGguf *file, const char *key, const char **valu
 typedef struct FnsMoeResident FnsMoeResident;
 int fns_hip_moe_layer_from_gguf(const FnsGguf *file, int layer, FnsMoeResident **resident, FnsMoeLayer *desc);
 void fns_hip_moe_resident_free(FnsMoeResident *resident);
+/* Dense FFN layer `layer` of the file made resident in HBM (reference src/model.cpp:120-125,193-196:
+ * blk.N.ffn_{gate,up,down}.weight and ffn_norm.weight, metadata attention.layer_norm_rms_epsilon). Fills *desc for
+ * fns_hip_dense_ffn / fns_hip_dense_ffn_prefill; the device memory it points to is owned by *resident. */
+typedef struct FnsDenseResident FnsDenseResident;
+int fns_hip_dense_ffn_from_gguf(const FnsGguf *file, int layer, FnsDenseResident **resident, FnsDenseFfn *desc);
+void fns_hip_dense_resident_free(FnsDenseResident *resident);
 
 /* --- seeded synthetic data on the device (benchmarks and large tests) ---
  * out[i] = mean + std * N(0,1), Philox-4x32-10 counter (offset + i) / 4 and Box-Muller; offset % 4 == 0. */

@@ -109,3 +109,26 @@ def test_moe_block_extras_host_checks():
     assert L.fns_hip_moe_layer(ctypes.byref(d), ptr, None, ptr, 1, ctypes.addressof(ws), with_sh4, None) == -2
     d.shexp_down, d.shexp_gu_type = ptr, 10  # Q2_K: not accepted
     assert L.fns_hip_moe_layer(ctypes.byref(d), ptr, None, ptr, 1, ctypes.addressof(ws), with_sh4, None) == -1
+
+
+def test_dense_ffn_host_checks():
+    """fns_hip_dense_ffn: workspace sizing and the host-side shape / type / size checks (no launch)."""
+    from flintnsteel_amd import ops
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    ptr = ctypes.addressof(buf)
+    d = ops.DenseFfnDesc(2048, 6144, 12, 12, 14, ptr, ptr, ptr, None, 1e-6)
+    t1, t4 = ctypes.c_size_t(), ctypes.c_size_t()
+    assert L.fns_hip_dense_ffn_workspace(ctypes.byref(d), 1, ctypes.byref(t1)) == 0
+    assert L.fns_hip_dense_ffn_workspace(ctypes.byref(d), 4, ctypes.byref(t4)) == 0
+    assert 0 < t1.value < t4.value and t4.value >= 4 * 4 * (2 * 2048 + 2 * 6144)
+    ws = ctypes.create_string_buffer(t1.value)
+    assert L.fns_hip_dense_ffn(ctypes.byref(d), ptr, ptr, 1, ctypes.addressof(ws), t1.value - 1, None) == -2
+    d.inter = 6000  # not a multiple of 256
+    assert L.fns_hip_dense_ffn(ctypes.byref(d), ptr, ptr, 1, ctypes.addressof(ws), t1.value, None) == -2
+    d.inter, d.down = 6144, None
+    assert L.fns_hip_dense_ffn_prefill(ctypes.byref(d), ptr, ptr, 1, ctypes.addressof(ws), t1.value, None) == -2
+    d.down, d.gate_type = ptr, 10  # Q2_K: no GEMV kernel
+    assert L.fns_hip_dense_ffn(ctypes.byref(d), ptr, ptr, 1, ctypes.addressof(ws), t1.value, None) == -1
+    assert L.fns_hip_dense_ffn(ctypes.byref(d), ptr, ptr, 0, None, 0, None) == 0  # no tokens: no-op
+    assert L.fns_hip_add(ptr, ptr + 4, ptr, 8, None) == -2  # misaligned

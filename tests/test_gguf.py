@@ -204,3 +204,113 @@ def test_gguf_layer_equals_directly_built_layer(tmp_path, variant):
     assert np.array_equal(a.cpu().numpy(), b.cpu().numpy()), "prefill differs"
     del g
     f.close()
+
+
+DF = 768  # dense FFN width of the small files
+
+
+def _dense_file(path, gt=orc.Q4_K, ut=orc.Q4_K, dt=orc.Q6_K, layer=0, seed=11, h=H, f=DF, down_shape=None):
+    """A checkpoint with one dense FFN block at blk.<layer> (reference names, src/model.cpp:120-125)."""
+    rng = np.random.default_rng(seed)
+    w = lambda *s: rng.normal(0, 0.02, s).astype(np.float32)  # noqa: E731
+    gate, up, down = orc.quantize(gt, w(f, h)), orc.quantize(ut, w(f, h)), orc.quantize(dt, w(h, f))
+    norm = (1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+    p = f"blk.{layer}."
+    tensors = [(p + "ffn_norm.weight", F32, [h], norm), (p + "ffn_gate.weight", gt, [h, f], gate),
+               (p + "ffn_up.weight", ut, [h, f], up), (p + "ffn_down.weight", dt, down_shape or [f, h], down)]
+    kv = [("general.architecture", GGUF_STRING, "flint"), ("flint.block_count", GGUF_U32, layer + 1),
+          ("flint.attention.layer_norm_rms_epsilon", GGUF_F32, 1e-5)]
+    tensors.insert(0, ("token_embd.weight", 8, [h, 3], np.zeros(3 * h // 32 * 34, np.uint8) + 7))
+    write_gguf(path, kv, tensors)
+    return {"gate": gate, "up": up, "down": down, "norm": norm}
+
+
+def test_dense_build_rejects_unsupported_checkpoints(tmp_path):
+    """The dense loader's checks run before any device allocation (CPU): a type without a GEMV kernel, a down matrix
+    whose shape does not match gate / up, a missing tensor."""
+    from flintnsteel_amd import ops
+    from flintnsteel_amd._lib import FnsError
+    p = tmp_path / "d.gguf"
+    _dense_file(p)
+    f = ops.GgufFile(p)
+    with pytest.raises(FnsError, match="missing tensor"):
+        ops.DenseFfn.from_gguf(f, 1)
+    f.close()
+    p2 = tmp_path / "d2.gguf"
+    rng = np.random.default_rng(1)
+    q2k = rng.integers(0, 255, DF * (H // 256) * 84, dtype=np.uint8)
+    q4k = orc.quantize(orc.Q4_K, np.zeros((DF, H), np.float32))
+    write_gguf(p2, [("general.architecture", GGUF_STRING, "flint")],
+               [("blk.0.ffn_gate.weight", 10, [H, DF], q2k), ("blk.0.ffn_up.weight", 10, [H, DF], q2k),
+                ("blk.0.ffn_down.weight", orc.Q4_K, [DF, H], orc.quantize(orc.Q4_K, np.zeros((H, DF), np.float32))),
+                ("blk.1.ffn_gate.weight", orc.Q4_K, [H, DF], q4k), ("blk.1.ffn_up.weight", orc.Q4_K, [H, DF], q4k),
+                ("blk.1.ffn_down.weight", orc.Q4_K, [DF, H // 2],
+                 orc.quantize(orc.Q4_K, np.zeros((H // 2, DF), np.float32)))])
+    f2 = ops.GgufFile(p2)
+    with pytest.raises(FnsError, match="not supported by the GEMV kernels"):
+        ops.DenseFfn.from_gguf(f2, 0)
+    with pytest.raises(FnsError, match="dense FFN layer 1: unexpected shape of blk.1.ffn_down.weight"):
+        ops.DenseFfn.from_gguf(f2, 1)
+    f2.close()
+
+
+def _dense_ref(arrays, gt, ut, dt, h_dim, f_dim, x: np.ndarray, eps: float) -> np.ndarray:
+    """float64 chain of the dense block: RMSNorm, Q8_1, gate / up GEMVs, SwiGLU, Q8_1 of act, down, + x."""
+    x64 = x.astype(np.float64)
+    hn = (x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + eps) * arrays["norm"]).astype(np.float32)
+    xq = orc.quantize_q8_1(hn)
+    n = x.shape[0]
+    mv = lambda t, m, nc, nr, q: orc.mmvq_experts(t, [m], nc, nr, q, q.shape[0], 1, np.zeros(q.shape[0], np.int32))  # noqa: E731
+    g = mv(gt, arrays["gate"].reshape(f_dim, -1), h_dim, f_dim, xq)
+    u = mv(ut, arrays["up"].reshape(f_dim, -1), h_dim, f_dim, xq)
+    act = orc.swiglu(g, u).astype(np.float32)
+    y = mv(dt, arrays["down"].reshape(h_dim, -1), f_dim, h_dim, orc.quantize_q8_1(act))
+    assert y.shape == (n, h_dim)
+    return y + x64
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", ["small", "flint"])
+def test_gguf_dense_ffn(tmp_path, shape):
+    """A dense FFN block loaded from GGUF (fns_hip_dense_ffn_from_gguf) equals the same block built from the arrays,
+    bit for bit, in the decode (1 and 4 tokens) and prefill forms, and both forms match the float64 chain. "flint" is
+    the reference model's dense shape (hidden 2048, FFN 6144, src/model.cpp:163) with Q8_0 gate / up."""
+    import torch
+    from flintnsteel_amd import ops, synth
+    from tests.helpers import assert_close_chain
+    h_dim, f_dim = (H, DF) if shape == "small" else (2048, 6144)
+    gt, ut, dt = (orc.Q4_K, orc.Q5_K, orc.Q6_K) if shape == "small" else (orc.Q8_0, orc.Q8_0, orc.Q6_K)
+    print(f"dense ffn {shape} {h_dim}x{f_dim}", flush=True)
+    path = tmp_path / "d.gguf"
+    arrays = _dense_file(path, gt, ut, dt, layer=1, h=h_dim, f=f_dim)
+    f = ops.GgufFile(path)
+    g = ops.DenseFfn.from_gguf(f, 1)
+    d = g.desc
+    assert (d.hidden, d.inter, d.gate_type, d.up_type, d.down_type) == (h_dim, f_dim, gt, ut, dt)
+    assert abs(d.norm_eps - 1e-5) < 1e-12
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    ref = ops.DenseFfn(cu(arrays["gate"]), cu(arrays["up"]), cu(arrays["down"]), gt, ut, dt, h_dim, f_dim,
+                       ffn_norm=cu(arrays["norm"]), norm_eps=1e-5)
+    for n_tok, prefill in ((1, False), (4, False), (37, True)):
+        x = synth.activations(n_tok, h_dim, 5, layer=n_tok)
+        a, b = g(x, prefill=prefill), ref(x, prefill=prefill)
+        torch.cuda.synchronize()
+        a, b = a.cpu().numpy(), b.cpu().numpy()
+        assert np.array_equal(a, b), f"n_tok={n_tok} prefill={prefill}: GGUF-built layer differs"
+        toks = [0, n_tok - 1] if n_tok > 1 else [0]
+        xs = x.cpu().numpy()
+        assert_close_chain(a[toks], _dense_ref(arrays, gt, ut, dt, h_dim, f_dim, xs[toks], 1e-5),
+                           f"dense ffn {shape} n_tok={n_tok} prefill={prefill}")
+        if n_tok == 4:  # verify columns equal the single-token decode, column by column
+            for t in range(4):
+                one = ref(x[t:t + 1].contiguous())
+                torch.cuda.synchronize()
+                assert np.array_equal(one.cpu().numpy()[0], a[t]), f"verify column {t}"
+    # in place (out = x), as the reference's add_inplace on the residual stream
+    x = synth.activations(1, h_dim, 6, layer=0)
+    want = ref(x)
+    ref(x, out=x)
+    torch.cuda.synchronize()
+    assert np.array_equal(x.cpu().numpy(), want.cpu().numpy()), "in-place call differs"
+    del g
+    f.close()

@@ -321,7 +321,7 @@ def test_moe_prefill_vs_oracle(ops, gu, dn, guard):
 def test_moe_prefill_config4_sample(ops):
     """Config 4 shapes (512 tokens, hidden 2048, 128 experts top-8, inter 768, Q4_K) with a Dirichlet-skewed router
     bias: logits against the oracle, ids against the oracle's routing of its own logits (tokens with a clear margin),
-    the x image of all 512 tokens byte-exact, 64 tokens (among them every token of the largest expert group up to 40)
+    the x image of all 512 tokens and the fused launch's act image of all 4096 rows byte-exact, 64 tokens (among them every token of the largest expert group up to 40)
     against the float64 chain, residual added; then all 512 tokens against the batch-1 decode path."""
     from flintnsteel_amd import synth
     H, F, NE, K, T = 2048, 768, 128, 8, 512
@@ -342,6 +342,18 @@ def test_moe_prefill_config4_sample(ops):
     ids, w, _, _ = orc.route_topk(tr["logits"], K, 0, True)
     assert np.array_equal(ids, tr["ids"]) and np.array_equal(w, tr["w"])
     assert np.array_equal(tr["xpack"], split_image(orc.quantize_q8_1(xh), H)), "x image differs from the oracle"
+    # the fused launch's act image (the gate/up epilogue's Q8_1 of act, no f32 act kept) against the oracle's Q8_1 of
+    # the GPU's f32 act: the same layer with the F16 guard on runs gate/up as its own launch and keeps the f32 rows;
+    # with every guard scale 1 its image is that epilogue's too, and the fused image must equal it byte for byte
+    layer_g = ops.MoeLayer(layer.router_w, layer.slots, orc.Q4_K, orc.Q4_K, H, F, K, router_bias=dev(bias), guard=True)
+    pre_g = ops.MoePrefill(layer_g)
+    ws_g = pre_g.workspace(T)
+    pre_g(x, ws=ws_g, x_resid=resid)
+    tr_g = {k: host(v) for k, v in pre_g.trace(ws_g, T).items()}
+    assert np.array_equal(tr_g["ids"], tr["ids"]) and (tr_g["escale"] == 1.0).all()
+    assert np.array_equal(tr_g["apack"], split_image(orc.quantize_q8_1(tr_g["act"]), F)), \
+        "act image (two launches) differs from the oracle's Q8_1 of act"
+    assert np.array_equal(tr["apack"], tr_g["apack"]), "fused launch's act image differs"
     counts = np.bincount(ids.ravel(), minlength=NE)
     assert counts.max() > 128, "the skewed bias should give at least one expert more than one tile group"
     big = np.flatnonzero((ids == counts.argmax()).any(axis=1))
