@@ -21,8 +21,10 @@ The JSON line also carries:
                  on this host's cores on a bounded sample.
   extra        - configs 1 (Q3_K/Q5_K mix), 2 (4-token speculative verify), 3 (48-layer Q4_K/Q6_K stack) and 4
                  (512-token prefill through the f16-MFMA split-operand grouped GEMM, Dirichlet(0.3)-skewed router bias; MFMA
-                 utilisation = 38.65 G int8 ops per layer / time / 5.0 POP/s dense int8 peak), and the reference
-                 model's whole MoE block (RMSNorm, 256 experts top-6 sigmoid, width 512, shared expert) at decode.
+                 utilisation = 38.65 G int8 ops per layer / time / 5.0 POP/s dense int8 peak), the reference
+                 model's whole MoE block (RMSNorm, 256 experts top-6 sigmoid, width 512, shared expert) at decode with
+                 K-quant and with IQ3_XXS / IQ3_S gate/up + IQ4_XS down experts, and its dense FFN block (2048 ->
+                 6144, Q8_0) at 512 prefill tokens.
 """
 from __future__ import annotations
 
@@ -88,11 +90,21 @@ def capture(torch, layers, xs, outs, wss, steps_per_graph: int):
     return g
 
 
-def run_flint(torch, synth, n_layers: int = 8, replays: int = 40) -> dict:
+IQ3_XXS, IQ3_S, IQ4_XS, Q8_0 = 18, 21, 23, 8
+BLOCK.update({IQ3_XXS: 98, IQ3_S: 110, IQ4_XS: 136})
+
+
+def run_flint(torch, synth, n_layers: int = 8, replays: int = 40, gu: int = Q4_K, dn: int = Q5_K) -> dict:
     """The reference model's MoE block shape (src/model.cpp:159-164: RMSNorm, bf16 router, sigmoid top-6 of 256
-    experts of width 512, F16 guard, shared expert of width 1024; gate/up Q4_K, down Q5_K), decode batch 1 through
-    fns_hip_moe_layer with the residual added; n_layers resident copies replayed in one graph."""
-    layers = [synth.build_flint_layer(H, 512, 256, 6, 1024, Q4_K, Q5_K, SEED, layer=600 + l) for l in range(n_layers)]
+    experts of width 512, F16 guard, shared expert of width 1024; gate/up Q4_K, down Q5_K, or the checkpoint's IQ
+    formats with random blocks and seeded codebooks), decode batch 1 through fns_hip_moe_layer with the residual
+    added; n_layers resident copies replayed in one graph."""
+    if gu in synth.IQ_BLOCK_BYTES or dn in synth.IQ_BLOCK_BYTES:
+        synth.register_iq_grids()
+        layers = [synth.build_iq_flint_layer(H, 512, 256, 6, 1024, gu, dn, SEED, layer=600 + l)
+                  for l in range(n_layers)]
+    else:
+        layers = [synth.build_flint_layer(H, 512, 256, 6, 1024, gu, dn, SEED, layer=600 + l) for l in range(n_layers)]
     xs = [synth.activations(1, H, SEED, layer=700 + l) for l in range(n_layers)]
     outs = [torch.empty(1, H, device="cuda") for _ in layers]
     wss = [layer.workspace(1) for layer in layers]
@@ -108,8 +120,8 @@ def run_flint(torch, synth, n_layers: int = 8, replays: int = 40) -> dict:
         for l, layer in enumerate(layers):
             layer(xs[l], out=outs[l], ws=wss[l], x_resid=xs[l])
     us = time_graph(torch, g, replays, 3) * 1e3 / n_layers
-    routed = 6 * (2 * 512 * (H // 256) * 144 + H * 2 * 176)
-    shared = 2 * 1024 * (H // 256) * 144 + H * 4 * 176
+    routed = 6 * (2 * 512 * (H // 256) * BLOCK[gu] + H * 2 * BLOCK[dn])
+    shared = 2 * 1024 * (H // 256) * BLOCK[gu] + H * 4 * BLOCK[dn]
     byts = routed + shared + 256 * H * 2
     del g
     return {"us_per_layer": round(us, 3), "hbm_bytes_per_layer": byts, "hbm_gbs": round(byts / (us * 1e-6) / 1e9, 1)}
@@ -280,6 +292,50 @@ def run_prefill(torch, synth, n_layers: int = 4, T: int = 512, replays: int = 10
             "f16_pipe_util": round(2 * ops_per_layer / (us * 1e-6) / 2.5e15, 4)}
 
 
+def run_dense_q8_0(torch, n_layers: int = 4, T: int = 512, replays: int = 10) -> dict:
+    """The reference model's dense FFN block (src/model.cpp:121-125,163: hidden 2048, FFN 6144, the leading two
+    layers) with Q8_0 gate / up / down, prefill of T tokens through fns_hip_dense_ffn_prefill (RMSNorm, mmq of gate
+    and up, SwiGLU, mmq of down, residual), and one Q8_0 mmq (2048 -> 6144) alone; n_layers resident copies."""
+    from flintnsteel_amd import ops, synth
+    FD = 6144
+    ffns, mats = [], []
+    for l in range(n_layers):
+        g = torch.empty(FD * ops.row_bytes(Q8_0, H), dtype=torch.uint8, device="cuda")
+        u, d = torch.empty_like(g), torch.empty(H * ops.row_bytes(Q8_0, FD), dtype=torch.uint8, device="cuda")
+        for t, (nr, nc), kind in ((g, (FD, H), 1), (u, (FD, H), 2), (d, (H, FD), 3)):
+            synth.quantized_matrices(Q8_0, 1, nr, nc, synth.tensor_seed(SEED, 800 + l, kind), 0.02, t.view(1, -1))
+        norm = ops.fill_normal(torch.empty(H, device="cuda"), synth.tensor_seed(SEED, 800 + l, 9), mean=1.0, std=0.1)
+        ffns.append(ops.DenseFfn(g, u, d, Q8_0, Q8_0, Q8_0, H, FD, ffn_norm=norm, norm_eps=1e-6))
+        mats.append(g)
+    xs = [synth.activations(T, H, SEED, layer=900 + l) for l in range(n_layers)]
+    outs = [torch.empty(T, H, device="cuda") for _ in range(n_layers)]
+    wss = [f.workspace(T) for f in ffns]
+    ys = [torch.empty(T, FD, device="cuda") for _ in range(n_layers)]
+    xq = torch.empty(ops.mmq_q8_1_bytes(H, T), dtype=torch.uint8, device="cuda")
+    res = {}
+    for name, fn in (("dense_ffn", lambda l: ffns[l](xs[l], out=outs[l], ws=wss[l], prefill=True)),
+                     ("mmq", lambda l: ops.mmq(Q8_0, mats[l], H, FD, xs[l], xq=xq, out=ys[l]))):
+        gr = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for l in range(n_layers):
+                fn(l)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr):
+            for l in range(n_layers):
+                fn(l)
+        res[name] = time_graph(torch, gr, replays, 2) * 1e3 / n_layers
+        del gr
+    wbytes = 3 * FD * H * 34 // 32
+    flops = 2 * T * 3 * FD * H
+    return {"dense_ffn_us": round(res["dense_ffn"], 2), "dense_ffn_weight_gbs": round(wbytes / (res["dense_ffn"] * 1e-6) / 1e9, 1),
+            "dense_ffn_tops": round(flops / (res["dense_ffn"] * 1e-6) / 1e12, 2),
+            "mmq_2048x6144_us": round(res["mmq"], 2),
+            "mmq_tops": round(2 * T * FD * H / (res["mmq"] * 1e-6) / 1e12, 2)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -387,6 +443,13 @@ def main() -> int:
         torch.cuda.empty_cache()
         extra["flint_block_decode"] = run_flint(torch, synth)
         log(f"flint block (decode): {extra['flint_block_decode']}")
+        torch.cuda.empty_cache()
+        for name, gu, dn in (("flint_block_iq3xxs_iq4xs", IQ3_XXS, IQ4_XS), ("flint_block_iq3s_iq4xs", IQ3_S, IQ4_XS)):
+            extra[name] = run_flint(torch, synth, gu=gu, dn=dn)
+            log(f"{name} (decode): {extra[name]}")
+            torch.cuda.empty_cache()
+        extra["dense_q8_0_prefill512"] = run_dense_q8_0(torch)
+        log(f"dense Q8_0 prefill 512: {extra['dense_q8_0_prefill512']}")
     cpu = None
     if not args.no_cpu:
         if args.no_extra:

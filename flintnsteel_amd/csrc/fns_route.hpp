@@ -210,12 +210,13 @@ __device__ __forceinline__ void route_topk_filter(int gtid, const float *__restr
 // experts; the expert with rank r < k goes to slot r - the same result as k rounds of argmax with ties to the lower
 // index, without a dependent cross-lane chain. Must be called by every thread of the workgroup (it contains
 // barriers). Results: sel[0..k) and their probabilities pv[0..k) in LDS, visible to the whole workgroup on return.
+// gtid: the thread's index in its group of NT, as in route_topk_filter.
 template <int NT>
-__device__ __forceinline__ void route_topk_pairs(const float *__restrict__ lg, int n_expert, int k, int gating,
-                                                 uint64_t *s_key, int *sel, float *pv) {
+__device__ __forceinline__ void route_topk_pairs(int gtid, const float *__restrict__ lg, int n_expert, int k,
+                                                 int gating, uint64_t *s_key, int *sel, float *pv) {
     constexpr int P = 8;         // threads per expert
     constexpr int EPP = NT / P;  // experts per pass
-    const int tid = threadIdx.x, lane = tid % kWave;
+    const int tid = gtid, lane = tid % kWave;
     if (tid < kWave) {
         float p[4];
         if (gating == 0) {
@@ -276,11 +277,12 @@ __device__ __forceinline__ void route_topk_pairs(const float *__restrict__ lg, i
 
 // Gating + top-k + renormalisation for one token by a whole workgroup (n_expert <= 256): the all-pairs rank up to
 // 128 experts, the group-maximum filter beyond (4x the pairs at 256 experts); both give the same selection.
+// gtid: the thread's index in its group of NT (the workgroup, or one of its equal groups, each ranking its own token).
 template <int NT>
-__device__ __forceinline__ void route_topk_block(const float *__restrict__ lg, int n_expert, int k, int gating,
-                                                 uint64_t *scratch, int *sel, float *pv) {
-    if (n_expert <= 128) route_topk_pairs<NT>(lg, n_expert, k, gating, scratch, sel, pv);
-    else route_topk_filter<NT>((int) threadIdx.x, lg, n_expert, k, gating, scratch, sel, pv);
+__device__ __forceinline__ void route_topk_block(int gtid, const float *__restrict__ lg, int n_expert, int k,
+                                                 int gating, uint64_t *scratch, int *sel, float *pv) {
+    if (n_expert <= 128) route_topk_pairs<NT>(gtid, lg, n_expert, k, gating, scratch, sel, pv);
+    else route_topk_filter<NT>(gtid, lg, n_expert, k, gating, scratch, sel, pv);
 }
 
 // Combine weight of slot j (0 <= j < k < 16) from the selected probabilities pv[0..k): renormalised by their sum in

@@ -64,6 +64,53 @@ inline size_t gprefix_bytes(int64_t n_expert) { return (size_t) 2 * (n_expert + 
 // Workgroup barrier for LDS data only: no global memory is produced and consumed inside the compaction kernel, so its
 // barriers need not wait for the id loads and the output stores still in flight (__syncthreads' fence would).
 __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Exclusive prefix of the per-expert counts cnt[0..ne) (ne <= 256) by one wave (lane = its lane): cnt[e] becomes the
+// expert's first sorted position; bounds[0..ne], and the group prefixes gprefix[0..ne] of the 64-row groups
+// (n_e / 64 full ones, and the remainder if it is > 32 rows) and gprefix[ne + 1 .. 2 ne + 1] of the <= 32-row
+// remainders are written. 4 experts per lane, then a lane scan.
+__device__ __forceinline__ void expert_prefix_wave(int lane, int *cnt, int ne, int32_t *bounds, int32_t *gprefix) {
+    int v[4], g[4], g2[4], s = 0, sg = 0, sg2 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * lane + j, r = (e < ne ? cnt[e] : 0) % kMmqTok;
+        v[j] = e < ne ? cnt[e] : 0;
+        g[j] = v[j] / kMmqTok + (r > kMmqTok / 2);
+        g2[j] = r > 0 && r <= kMmqTok / 2;
+        s += v[j];
+        sg += g[j];
+        sg2 += g2[j];
+    }
+    int incl = s, inclg = sg, inclg2 = sg2;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64), tg = __shfl_up(inclg, o, 64), tg2 = __shfl_up(inclg2, o, 64);
+        if (lane >= o) {
+            incl += t;
+            inclg += tg;
+            inclg2 += tg2;
+        }
+    }
+    int run = incl - s, rung = inclg - sg, rung2 = inclg2 - sg2;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * lane + j;
+        if (e < ne) {
+            cnt[e] = run;  // the expert's first sorted position (its count is no longer needed)
+            bounds[e] = run;
+            gprefix[e] = rung;
+            gprefix[ne + 1 + e] = rung2;
+        }
+        run += v[j];
+        rung += g[j];
+        rung2 += g2[j];
+    }
+    if (lane == 63) {
+        bounds[ne] = incl;
+        gprefix[ne] = inclg;
+        gprefix[2 * ne + 1] = inclg2;
+    }
+}
+
 __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *__restrict__ ids, int n, int k, int ne,
                                                                  int x_rows_per_tok, int32_t *__restrict__ ids_src1,
                                                                  int32_t *__restrict__ ids_dst, int32_t *bounds,
@@ -110,48 +157,7 @@ __global__ __launch_bounds__(kCompactThreads) void k_mmq_compact(const int32_t *
     }
     lds_sync();
     PF_MARK(2, 4);
-    if (wave == 0) {  // exclusive prefix over <= 256 experts: 4 per lane, then a lane scan
-        int v[4], g[4], g2[4], s = 0, sg = 0, sg2 = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = 4 * lane + j, r = (e < ne ? cnt[e] : 0) % kMmqTok;
-            v[j] = e < ne ? cnt[e] : 0;
-            g[j] = v[j] / kMmqTok + (r > kMmqTok / 2);
-            g2[j] = r > 0 && r <= kMmqTok / 2;
-            s += v[j];
-            sg += g[j];
-            sg2 += g2[j];
-        }
-        int incl = s, inclg = sg, inclg2 = sg2;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int t = __shfl_up(incl, o, 64), tg = __shfl_up(inclg, o, 64), tg2 = __shfl_up(inclg2, o, 64);
-            if (lane >= o) {
-                incl += t;
-                inclg += tg;
-                inclg2 += tg2;
-            }
-        }
-        int run = incl - s, rung = inclg - sg, rung2 = inclg2 - sg2;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = 4 * lane + j;
-            if (e < ne) {
-                cnt[e] = run;  // the expert's first sorted position (its count is no longer needed)
-                bounds[e] = run;
-                gprefix[e] = rung;
-                gprefix[ne + 1 + e] = rung2;
-            }
-            run += v[j];
-            rung += g[j];
-            rung2 += g2[j];
-        }
-        if (lane == 63) {
-            bounds[ne] = incl;
-            gprefix[ne] = inclg;
-            gprefix[2 * ne + 1] = inclg2;
-        }
-    }
+    if (wave == 0) expert_prefix_wave(lane, cnt, ne, bounds, gprefix);
     lds_sync();
     PF_MARK(2, 5);
     if (tid < ne) {  // the expert's sorted positions, split over the waves in wave order

@@ -294,7 +294,7 @@ __device__ __forceinline__ int route_channel(const LayerArgs &a, RouteLds &rs) {
             rs.xrow[0] = 0;
             rs.orow[0] = blockIdx.y;
         }
-        route_topk_block<NT>(a.logits, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
+        route_topk_block<NT>((int) threadIdx.x, a.logits, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
         if (pub && tid < K) publish_route(a, rs, 0, tid);
         return rs.sel[blockIdx.y];
     }
@@ -723,7 +723,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     dma_waves_from<kQWaves>(s_x, a.xpack, xbytes, 1);
     if (wave != 0) dma_wait();
     FNS_MARK(1, blockIdx.x, 4);
-    route_topk_block<kQThreads>(a.logits, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
+    route_topk_block<kQThreads>((int) threadIdx.x, a.logits, a.NE, K, a.gating, rs.key, rs.sel, rs.pv);
     if (blockIdx.x == 0 && tid < K) publish_route(a, rs, 0, tid);
     if (tid < K) s_w[tid] = route_weight(rs.pv, K, a.norm, tid);
     FNS_MARK(1, blockIdx.x, 1);

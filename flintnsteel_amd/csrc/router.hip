@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route_topk(const float *__res
     __shared__ float s_pv[16];
     PF_MARK(1, 0);
     const int t = blockIdx.x;
-    route_topk_block<kRouteThreads>(logits + (size_t) t * n_expert, n_expert, k, gating, s_key, s_sel, s_pv);
+    route_topk_block<kRouteThreads>((int) threadIdx.x, logits + (size_t) t * n_expert, n_expert, k, gating, s_key, s_sel, s_pv);
     if ((int) threadIdx.x < k) {
         ids[(size_t) t * k + threadIdx.x] = s_sel[threadIdx.x];
         w[(size_t) t * k + threadIdx.x] = route_weight(s_pv, k, norm, threadIdx.x);

@@ -13,12 +13,14 @@ import torch
 from ._lib import call, lib
 
 Q8_0, Q8_1, Q3_K, Q4_K, Q5_K, Q6_K = 8, 9, 11, 12, 13, 14
+IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS = 18, 21, 22, 23
 F32, BF16 = 0, 30
 GATING_SOFTMAX, GATING_SIGMOID = 0, 1
 STATUS_EXCHANGE_TIMEOUT = 1  # FNS_STATUS_EXCHANGE_TIMEOUT
 # bytes per 256 values of a row (a K-quant block; 8 Q8_0 blocks)
-BLOCK_BYTES = {Q8_0: 272, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
-TYPE_NAMES = {Q8_0: "Q8_0", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+BLOCK_BYTES = {Q8_0: 272, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ4_XS: 136}
+TYPE_NAMES = {Q8_0: "Q8_0", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ3_XXS: "IQ3_XXS",
+              IQ3_S: "IQ3_S", IQ2_S: "IQ2_S", IQ4_XS: "IQ4_XS"}
 
 
 def _p(t: torch.Tensor | None):
@@ -438,11 +440,14 @@ def mmq_q8_1_bytes(ncols: int, nrows: int) -> int:
     return int(lib().fns_hip_mmq_q8_1_bytes(ncols, nrows))
 
 
-def mmq(qtype: int, w: torch.Tensor, ncols: int, nrows: int, x: torch.Tensor) -> torch.Tensor:
+def mmq(qtype: int, w: torch.Tensor, ncols: int, nrows: int, x: torch.Tensor, xq: torch.Tensor | None = None,
+        out: torch.Tensor | None = None) -> torch.Tensor:
+    """dst [n_tok][nrows] = W . q8_1(x); xq: scratch of mmq_q8_1_bytes(ncols, n_tok) bytes (allocated if None)."""
     x = x.contiguous()
     n_tok = x.numel() // ncols
-    xq = torch.zeros(mmq_q8_1_bytes(ncols, n_tok), dtype=torch.uint8, device=x.device)
-    dst = _empty_f32(n_tok, nrows, like=x)
+    if xq is None:
+        xq = torch.zeros(mmq_q8_1_bytes(ncols, n_tok), dtype=torch.uint8, device=x.device)
+    dst = _empty_f32(n_tok, nrows, like=x) if out is None else out
     call("fns_hip_mmq", qtype, _p(w), ncols, nrows, _p(x), n_tok, _p(xq), _p(dst), _s())
     return dst
 

@@ -59,6 +59,53 @@ def test_compaction_bit_exact(ops, n_tok, k, n_expert, xr):
     assert np.array_equal(host(dst), rd)
 
 
+def _group_prefix(counts: np.ndarray) -> np.ndarray:
+    """The GEMM's group lists from the per-expert counts: 64-row groups (n_e // 64 full ones and the remainder if
+    it is > 32 rows), then the <= 32-row remainders, each as an exclusive prefix with its total."""
+    r = counts % 64
+    g = counts // 64 + (r > 32)
+    g2 = ((r > 0) & (r <= 32)).astype(np.int64)
+    pre = lambda v: np.concatenate([[0], np.cumsum(v)]).astype(np.int32)  # noqa: E731
+    return np.concatenate([pre(g), pre(g2)])
+
+
+@pytest.mark.parametrize("n_tok,k,n_expert,gating", [(1, 8, 128, 0), (3, 6, 256, 1), (77, 8, 128, 0), (512, 8, 128, 0),
+                                                     (700, 6, 256, 1), (50, 4, 16, 0), (4096, 8, 128, 1),
+                                                     (8192, 8, 128, 0)])
+def test_prefill_routing_and_compaction_sections(ops, n_tok, k, n_expert, gating):
+    """The prefill layer's routing and compaction launches: ids and weights bit-exact against the oracle's routing of
+    the layer's own logits, and the sorted lists, expert bounds and group prefixes against the oracle's compaction
+    (ggml mm_ids_helper order) - with the workspace full of junk before the first call (the GEMM's arrival counters
+    are reset by the compaction launch), then a second call on the same workspace with fewer tokens."""
+    from flintnsteel_amd import synth
+    print(f"prefill routing + compaction n_tok={n_tok} k={k} ne={n_expert}", flush=True)
+    H = 256
+    layer = synth.build_layer(H, 256, n_expert, k, orc.Q4_K, orc.Q4_K, seed=n_tok + k, layer=3, gating=gating,
+                              std=0.3)
+    pre = ops.MoePrefill(layer)
+    ws = pre.workspace(n_tok)
+    ws.fill_(0x4F)
+    for T in (n_tok, max(1, n_tok // 3)):
+        x = synth.activations(T, H, seed=T, layer=5)
+        pre(x, ws=ws)
+        tr = {kk: host(v) for kk, v in pre.trace(ws, T).items()}
+        ids_r, w_r, _, _ = orc.route_topk(tr["logits"], k, gating, True)
+        assert np.array_equal(tr["ids"], ids_r), f"T={T}: ids differ given the same logits"
+        assert np.array_equal(tr["w"].view(np.uint32), w_r.view(np.uint32)), f"T={T}: weights differ"
+        P = T * k
+        rb, rs, rd, _ = orc.compact_ids(tr["ids"], n_expert, 1)
+        off6, _ = pre.section(T, 6)
+        off7, _ = pre.section(T, 7)
+        off8, _ = pre.section(T, 8)
+        src = host(ws[off6: off6 + 4 * P].view(torch.int32))
+        dst = host(ws[off7: off7 + 4 * P].view(torch.int32))
+        sec8 = host(ws[off8: off8 + 4 * 3 * (n_expert + 1)].view(torch.int32))
+        assert np.array_equal(sec8[: n_expert + 1], rb), f"T={T}: bounds"
+        assert np.array_equal(src, rs) and np.array_equal(dst, rd), f"T={T}: sorted lists"
+        counts = np.diff(rb)
+        assert np.array_equal(sec8[n_expert + 1:], _group_prefix(counts)), f"T={T}: group prefixes"
+
+
 @pytest.mark.parametrize("n_tok,ncols", [(77, 2048), (512, 2048), (33, 768), (1, 256)])
 def test_mmq_activation_image_bit_exact(ops, n_tok, ncols):
     """The MMQ activation quantiser (the split image fns_hip_mmq writes into its xq scratch) holds exactly the
