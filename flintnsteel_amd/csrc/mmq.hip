@@ -331,6 +331,7 @@ struct MmqArgs {
     const int32_t *src;        // sorted position -> activation image row (null: identity)
     const int32_t *dst_rows;   // sorted position -> output row (null: identity)
     int n_rows;                // dense: number of activation rows
+    int dense_small;           // dense: 1 = groups of 32 activation rows (one tile), 0 = of 64
     float *dst;                // [out row][nrows] f32 (non-GLU)
     uint8_t *out_pack;         // GLU: act split image rows (by output row)
     int64_t out_img;
@@ -348,6 +349,9 @@ template <> struct WFrag<T_Q4_K> { uint4 h; uint4 q[4]; };
 template <> struct WFrag<T_Q5_K> { uint4 h; uint4 q[4]; uint4 qh; };
 template <> struct WFrag<T_Q6_K> { uint4 ql[4]; uint4 qh[2]; uint4 sc; uint32_t d; };
 template <> struct WFrag<T_Q3_K> { uint4 qs[2]; uint4 hm; uint4 tail; };
+// Q8_0 (8 blocks of 34 bytes per 256 values): the 16 code bytes of column groups 2 h, 2 h + 1 and the f16 d of
+// every block (low 16 bits)
+template <> struct WFrag<T_Q8_0> { uint4 q[8]; uint32_t d[8]; };
 // IQ formats (lane half h, its two column groups of every 32-value sub-block; see decode):
 //   IQ4_XS : header (d, scales_h, scales_l) and qs bytes 8 h .. 8 h + 7 of each sub-block
 //   IQ3_XXS: d, index bytes 4 h .. 4 h + 3 of each sub-block, the sub-block's aux word (signs, scale)
@@ -405,6 +409,12 @@ __device__ __forceinline__ void wfrag_load(Rsrc r, uint32_t vo, uint32_t vc, uin
             f.tail = bload16(r, vo, so + 94);  // scales[12] at +2, d at +14
         }
         f.qs[P] = bload16(r, vc, so + 32 + 32 * P);
+    } else if constexpr (T == T_Q8_0) {  // block s at 34 s: d @0, qs @2 (vc - vo = 16 h selects the lane's 16 bytes)
+#pragma unroll
+        for (int b = 4 * P; b < 4 * P + 4; ++b) {
+            f.q[b] = bload16(r, vc, so + 34 * b + 2);
+            f.d[b] = bload2(r, vo, so + 34 * b);
+        }
     } else if constexpr (T == T_IQ4_XS) {  // d @0, scales_h @2, scales_l @4, qs @8 (16 per sub-block)
         const uint32_t vq = vo + ((vc - vo) >> 1);  // + 8 h
         if constexpr (P == 0) f.h = bload8(r, vo, so);
@@ -444,6 +454,7 @@ template <int T, int P> constexpr int wfrag_loads() {
            : T == T_Q5_K  ? (P ? 2 : 4)
            : T == T_Q6_K  ? (P ? 3 : 5)
            : T == T_Q3_K  ? (P ? 1 : 3)
+           : T == T_Q8_0  ? 8
            : T == T_IQ4_XS ? (P ? 4 : 5)
            : T == T_IQ3_XXS ? (P ? 5 : 6)
            : T == T_IQ3_S ? (P ? 8 : 11)
@@ -482,7 +493,7 @@ __device__ __forceinline__ v8h centred8(uint32_t x, uint32_t y, h2 off, h2 sc) {
 // integer scale as f16 (Q6_K: two operands, scale split as 16 (sc >> 4) + (sc & 15), each product exact). The block's
 // float scale d (and dmin) are applied per superblock. on = (d != 0): a block with d = 0 contributes d * (...) = 0
 // whatever its codes.
-template <int T> constexpr int kNumB = T == T_Q6_K || T == T_IQ4_XS ? 2 : 1;
+template <int T> constexpr int kNumB = T == T_Q6_K || T == T_IQ4_XS || T == T_Q8_0 ? 2 : 1;
 template <int T> struct BOp { v8h b[kNumB<T>]; };
 template <int T>
 __device__ __forceinline__ BOp<T> decode(const WFrag<T> &f, int s, int p, int h, bool on, const uint32_t *grid);
@@ -613,9 +624,32 @@ template <> __device__ __forceinline__ BOp<T_IQ2_S> decode<T_IQ2_S>(const WFrag<
     return r;
 }
 
+// Q8_0: B = code * d split into two f16 operands, hi = f16(code d) and lo = f16(code d - hi) (an fma in f16): code d
+// has at most 19 significant bits and hi + lo holds 22, so the pair is the product exactly when lo is a normal f16
+// (|code d| >= 2^-3); for smaller products lo is rounded to a multiple of 2^-24 (an absolute error of at most 2^-25
+// per weight). The block scale is then inside the operands and the superblock unit is 1. Codes are signed bytes:
+// (1024 + (c ^ 0x80)) - 1152. Weights must stay below the f16 range (|code d| <= 65504), as they do in a Q8_0 block.
+template <> __device__ __forceinline__ BOp<T_Q8_0> decode<T_Q8_0>(const WFrag<T_Q8_0> &f, int s, int p, int, bool, const uint32_t *) {
+    const uint2 q = half8(f.q[s], p);
+    const uint32_t x = q.x ^ 0x80808080u, y = q.y ^ 0x80808080u;
+    const h2 off = splat((_Float16) 1152.0f), d2 = as_h2((f.d[s] & 0xffffu) * 0x10001u);
+    const h2 c[4] = {biased02(x) - off, biased13(x) - off, biased02(y) - off, biased13(y) - off};
+    h2 hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hi[i] = c[i] * d2;
+        lo[i] = fma2(c[i], d2, -hi[i]);
+    }
+    BOp<T_Q8_0> r;
+    r.b[0] = cat4(hi[0], hi[1], hi[2], hi[3]);
+    r.b[1] = cat4(lo[0], lo[1], lo[2], lo[3]);
+    return r;
+}
+
 // Per-superblock float scales of this lane's row: d, and dmin for Q4_K / Q5_K.
 template <int T> __device__ __forceinline__ float blk_d(const WFrag<T> &f) {
     if constexpr (T == T_Q4_K || T == T_Q5_K) return half_to_float(f.h.x & 0xffffu);
+    else if constexpr (T == T_Q8_0) return 1.0f;  // the block scales are inside the B operands
     else if constexpr (T == T_Q6_K) return half_to_float(f.d);
     else if constexpr (T == T_Q3_K) return half_to_float(f.tail.w >> 16);
     else if constexpr (T == T_IQ4_XS) return half_to_float(f.h.x & 0xffffu);
@@ -778,8 +812,8 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
         seg = __builtin_amdgcn_readfirstlane(L.grp[1]);
         cnt = __builtin_amdgcn_readfirstlane(L.grp[2]);
     } else {
-        seg = g * kMmqTok;
-        cnt = min(kMmqTok, a.n_rows - seg);
+        seg = g * ROWS;
+        cnt = min(ROWS, a.n_rows - seg);
     }
     if (cnt <= 0) return;
     MMQ_MARK(0);
@@ -1122,7 +1156,8 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
         return;
     }
     if (j >= a.n_groups) return;
-    mmq_group<T, GLU, 2, false>(a, j, wb, L);
+    if (a.dense_small) mmq_group<T, GLU, 1, false>(a, j, wb, L);
+    else mmq_group<T, GLU, 2, false>(a, j, wb, L);
 }
 
 // Gate/up (with SwiGLU and the Q8_1 of act) and down of the expert path in one launch. The gate/up items come first,
@@ -1205,6 +1240,7 @@ __global__ __launch_bounds__(kMmqThreads) __attribute__((amdgpu_waves_per_eu(2, 
 
 template <bool GLU> const void *mmq_kernel(int type) {
     switch (type) {
+        case T_Q8_0: return (const void *) k_mmq<T_Q8_0, GLU>;
         case T_Q3_K: return (const void *) k_mmq<T_Q3_K, GLU>;
         case T_Q4_K: return (const void *) k_mmq<T_Q4_K, GLU>;
         case T_Q5_K: return (const void *) k_mmq<T_Q5_K, GLU>;
@@ -1227,11 +1263,19 @@ int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st)
     arg.n_main = groups;
     // expert path: n_expert + ceil(pairs / 64) (the 64-row list's bound) bounds both lists together, as expert e
     // has ceil(n_e / 64) groups in all
-    const int total = groups;
+    int total = groups;
     void *args[] = {&arg};
     const int rows = glu ? 128 : 256;  // weight rows per workgroup
-    arg.n_groups = total;
     arg.n_cb = (a.nrows + rows - 1) / rows;
+    // dense: when even twice the workgroups of the 64-row groups fit one per CU, groups of 32 rows (one token tile:
+    // more B decode per MFMA, but twice the workgroups; measured faster for 64 -> 128 workgroups, slower for
+    // 192 -> 384)
+    arg.dense_small = 0;
+    if (!a.bounds && a.n_rows > 32 && (int64_t) 2 * groups * arg.n_cb <= 256) {
+        arg.dense_small = 1;
+        total = (a.n_rows + 31) / 32;
+    }
+    arg.n_groups = total;
     const int64_t items = (int64_t) arg.n_cb * kXcds * ((total + kXcds - 1) / kXcds);
     if (items > INT32_MAX) return host::set_error(host::ERR_SHAPE, "mmq: grid too large");
     const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) items), dim3(kMmqThreads), args, 0, st);
@@ -1275,7 +1319,7 @@ int launch_mmq_moe(int tgu, int tdn, MoeArgs m, hipStream_t st) {
 }
 
 int check_mmq_shape(int type, int64_t ncols, int64_t nrows) {
-    if (!host::is_kquant(type) && !host::is_iq(type))
+    if (!host::is_kquant(type) && !host::is_iq(type) && type != T_Q8_0)
         return host::set_error(host::ERR_TYPE, "mmq: type %d not supported", type);
     if (host::iq_needs_grid(type) && !host::iq_grids_ready())
         return host::set_error(host::ERR_TYPE, "mmq: type %d needs the IQ codebooks (fns_hip_set_iq_grids)", type);
@@ -1381,7 +1425,7 @@ int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t of
 // K-quant and IQ formats, whose sub-block scales fold into exact f16 operands; Q8_0's float block scale does not).
 int mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq, float *dst,
         hipStream_t st) {
-    if (type == T_Q8_0) {
+    if (type == T_Q8_0 && nrows % kMmqRows) {  // the GEMV kernels (any row count), a few token columns per pass
         if (!w || !x || !xq || !dst || n_tok < 0 || ncols <= 0 || ncols % 256 || nrows <= 0)
             return host::set_error(host::ERR_SHAPE, "mmq: bad arguments");
         if (n_tok == 0) return host::OK;
@@ -1406,7 +1450,7 @@ int mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, i
 int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, int64_t n_expert,
                 const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
                 int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, void *xq, float *dst, hipStream_t st) {
-    if (type == T_Q8_0) {  // the GEMV over every (token, slot), as mmq above; the expert sort is still written
+    if (type == T_Q8_0 && nrows % kMmqRows) {  // the GEMV over every (token, slot), as mmq above; the sort is still written
         if (!x || !xq || !table || !ids || !dst || n_used < 1 || n_tok < 0 || ncols <= 0 || ncols % 256 ||
             (x_rows_per_tok != 1 && x_rows_per_tok != n_used))
             return host::set_error(host::ERR_SHAPE, "mmq_experts: bad arguments");

@@ -232,12 +232,14 @@ def test_mmq_experts_group_shapes(ops, qtype):
     assert_close(got.reshape(T * K, nrows), ref, f"mmq_experts group shapes {orc.TYPE_NAMES[qtype]}")
 
 
-def test_mmq_q8_0_dense_and_experts(ops):
+@pytest.mark.parametrize("nrows", [96, 128, 320])
+def test_mmq_q8_0_dense_and_experts(ops, nrows):
     """Q8_0 (the reference's dense and output-head type, src/ggml/ggml_mmq.cu:59) through fns_hip_mmq and
-    fns_hip_mmq_experts (the GEMV kernels over the token columns) against the float64 oracle; gate-like and down-like
-    activation rows."""
-    rng = np.random.default_rng(8)
-    T, ncols, nrows = 37, 512, 96
+    fns_hip_mmq_experts against the float64 oracle - the tiled MFMA GEMM when nrows is a multiple of 64, the GEMV
+    kernels over the token columns otherwise; gate-like and down-like activation rows."""
+    print(f"mmq Q8_0 nrows={nrows}", flush=True)
+    rng = np.random.default_rng(8 + nrows)
+    T, ncols = 37, 512
     w = orc.quantize(orc.Q8_0, rng.normal(0, 0.02, (nrows, ncols)).astype(np.float32))
     x = gaussian(rng, (T, ncols))
     got = host(ops.mmq(orc.Q8_0, dev(w), ncols, nrows, dev(x)))
@@ -254,6 +256,27 @@ def test_mmq_q8_0_dense_and_experts(ops):
         ref = orc.mmvq_experts(orc.Q8_0, list(mats), ncols, nrows, xq, T * xr if xr > 1 else T, 1 if xr > 1 else K,
                                ids.ravel())
         assert_close(got.reshape(T * K, nrows), ref, f"mmq_experts Q8_0 x_rows_per_tok={xr}")
+
+
+def test_mmq_q8_0_dense_ffn_shape(ops):
+    """The tiled Q8_0 GEMM at the reference model's dense FFN shape (2048 -> 6144 and 6144 -> 2048, 512 tokens):
+    a sample of tokens against the float64 oracle, and weight blocks with d = 0, tiny d (the lo operand subnormal)
+    and the largest codes."""
+    print("mmq Q8_0 dense FFN shape", flush=True)
+    rng = np.random.default_rng(81)
+    T = 512
+    toks = [0, 1, 63, 64, 200, 511]
+    for ncols, nrows in ((2048, 6144), (6144, 2048)):
+        wf = rng.normal(0, 0.02, (nrows, ncols)).astype(np.float32)
+        wf[:3, :64] = 0.0                      # d = 0 blocks
+        wf[3, :32] = 1e-4 * rng.standard_normal(32)  # tiny d: products below 2^-3, lo subnormal
+        wf[4, 32:64] = 1.0                      # |code| = 127
+        w = orc.quantize(orc.Q8_0, wf)
+        x = gaussian(rng, (T, ncols))
+        got = host(ops.mmq(orc.Q8_0, dev(w), ncols, nrows, dev(x)))
+        xq = orc.quantize_q8_1(x[toks])
+        ref = orc.mmvq_experts(orc.Q8_0, [w], ncols, nrows, xq, len(toks), 1, np.zeros(len(toks), np.int32))
+        assert_close(got[toks], ref, f"mmq Q8_0 {ncols}->{nrows}")
 
 
 def test_mmq_dense(ops):
