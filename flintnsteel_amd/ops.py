@@ -81,10 +81,12 @@ def mmvq_swiglu(qtype: int, w_gate: torch.Tensor, w_up: torch.Tensor, ncols: int
 
 def mmvq_ids_swiglu_shared(qtype: int, w_gate: torch.Tensor, w_up: torch.Tensor, ncols: int, nrows: int, n_mats: int,
                            xq: torch.Tensor, ids: torch.Tensor, sh_gate: torch.Tensor | None = None,
-                           sh_up: torch.Tensor | None = None):
+                           sh_up: torch.Tensor | None = None, dst: torch.Tensor | None = None,
+                           sh_dst: torch.Tensor | None = None):
     n_ids = ids.numel()
-    dst = _empty_f32(n_ids, nrows, like=xq)
-    sh_dst = _empty_f32(nrows, like=xq) if sh_gate is not None else None
+    dst = _empty_f32(n_ids, nrows, like=xq) if dst is None else dst
+    if sh_gate is not None and sh_dst is None:
+        sh_dst = _empty_f32(nrows, like=xq)
     call("fns_hip_mmvq_ids_swiglu_shared", qtype, _p(w_gate), _p(w_up), ncols, nrows, n_mats, _p(xq), _p(ids), n_ids,
          _p(dst), _p(sh_gate), _p(sh_up), _p(sh_dst), _s())
     return dst, sh_dst

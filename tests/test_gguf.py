@@ -314,3 +314,17 @@ def test_gguf_dense_ffn(tmp_path, shape):
     assert np.array_equal(x.cpu().numpy(), want.cpu().numpy()), "in-place call differs"
     del g
     f.close()
+
+
+@pytest.mark.gpu
+def test_mmvq_bench_tool_on_a_file(tmp_path):
+    """The GEMV timing tool (flintnsteel_amd/mmvq_bench.py, the reference's fns-mmvq-bench) runs on a GGUF file:
+    gate + up, down, the dense GEMV over the shared expert's gate, and the whole layer."""
+    import argparse
+    from flintnsteel_amd import mmvq_bench
+    print("mmvq_bench on a file", flush=True)
+    path = tmp_path / "m.gguf"
+    _moe_file(path)
+    lines = mmvq_bench.run(argparse.Namespace(model=str(path), synthetic=False, layer=1, reps=3, gu=None, down=None))
+    assert len(lines) == 4 and "gate+up Q4_K" in lines[0] and "down    Q6_K" in lines[1], lines
+    assert "ffn_gate_shexp.weight" in lines[2] and "whole MoE layer" in lines[3], lines
