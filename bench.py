@@ -292,6 +292,55 @@ def run_prefill(torch, synth, n_layers: int = 4, T: int = 512, replays: int = 10
             "f16_pipe_util": round(2 * ops_per_layer / (us * 1e-6) / 2.5e15, 4)}
 
 
+def run_dropin(torch, layers, replays: int = 40) -> dict:
+    """The reference's decode MoE sequence (Engine::ffn_block, src/engine.cu:670-694, without RMSNorm and shared
+    expert) as its seven separate calls through the drop-in C ABI - gemv router, route_topk, quantize_q8_1,
+    mmvq_experts_swiglu, amax_guard_q8_1, mmvq_experts, moe_combine - on preallocated buffers (as the engine holds
+    them), over the config-0 layers, replayed from one graph."""
+    import ctypes
+
+    from flintnsteel_amd import ops
+    from flintnsteel_amd._lib import call
+    L = len(layers)
+    P = ctypes.c_void_p
+    st = lambda: P(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    xs = [torch.randn(1, H, device="cuda") for _ in range(L)]
+    outs = [torch.empty(1, H, device="cuda") for _ in range(L)]
+    logits = torch.empty(NE, device="cuda")
+    ids = torch.empty(K_TOP, dtype=torch.int32, device="cuda")
+    w = torch.empty(K_TOP, device="cuda")
+    xq = torch.zeros(K_TOP, ops.q8_1_row_bytes(max(H, F)), dtype=torch.uint8, device="cuda")
+    act = torch.empty(K_TOP, F, device="cuda")
+    esc = torch.empty(K_TOP, device="cuda")
+    dexp = torch.empty(K_TOP, H, device="cuda")
+    p = lambda t: P(t.data_ptr())  # noqa: E731
+
+    def step():
+        for l, layer in enumerate(layers):
+            s = layer.slots
+            call("fns_hip_gemv_router", 0, p(layer.router_w), p(xs[l]), p(logits), H, NE, 1, st())
+            call("fns_hip_route_topk", p(logits), p(ids), p(w), NE, K_TOP, 1, 0, 1, st())
+            call("fns_hip_quantize_q8_1", p(xs[l]), p(xq), H, 1, st())
+            call("fns_hip_mmvq_experts_swiglu", Q4_K, p(s.table), s.gate_off, s.up_off, H, F, p(xq), 1, p(ids), K_TOP,
+                 p(act), st())
+            call("fns_hip_amax_guard_q8_1", p(act), p(esc), p(xq), F, K_TOP, st())
+            call("fns_hip_mmvq_experts", Q4_K, p(s.table), s.down_off, F, H, p(xq), K_TOP, p(ids), K_TOP, p(dexp), st())
+            call("fns_hip_moe_combine", p(dexp), p(esc), p(w), None, p(xs[l]), p(outs[l]), H, K_TOP, 1, st())
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        step()
+    us = time_graph(torch, g, replays, 3) * 1e3 / L
+    del g
+    return {"us_per_layer": round(us, 3), "launches_per_layer": 7}
+
+
 def run_dense_q8_0(torch, n_layers: int = 4, T: int = 512, replays: int = 10) -> dict:
     """The reference model's dense FFN block (src/model.cpp:121-125,163: hidden 2048, FFN 6144, the leading two
     layers) with Q8_0 gate / up / down, prefill of T tokens through fns_hip_dense_ffn_prefill (RMSNorm, mmq of gate
@@ -415,6 +464,8 @@ def main() -> int:
 
     extra = {"config0_layer_hbm_gbs": round(layer_gbs, 1), "config0_stage_us": [round(v, 3) for v in st]}
     if not args.no_extra:
+        extra["config0_dropin_seven_calls"] = run_dropin(torch, layers)
+        log(f"config0 through the seven drop-in calls: {extra['config0_dropin_seven_calls']}")
         for name, gu, dn in (("config1_q3k_q5k", Q3_K, Q5_K),):
             _, ms, _ = run_stack(torch, synth, gu, dn, L, 1, 16, 4, 100)
             us = ms * 1e3 / L

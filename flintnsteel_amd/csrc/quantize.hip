@@ -104,6 +104,33 @@ __global__ __launch_bounds__(256) void k_amax_guard_q8_1(const float *__restrict
     }
 }
 
+// The same for rows of at most 256 C padded columns: each thread's C values are loaded once, all in flight together
+// (clamped, unconditional loads), and quantised from registers; same operations, same bits.
+template <int C>
+__global__ __launch_bounds__(256) void k_amax_guard_q8_1_reg(const float *__restrict__ act, float *__restrict__ escale,
+                                                             uint8_t *__restrict__ xq, int n, int64_t row_bytes) {
+    __shared__ float red[4];
+    const float *r = act + (size_t) blockIdx.x * n;
+    float v[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int i = threadIdx.x + 256 * c;
+        const float x = r[min(i, n - 1)];
+        v[c] = i < n ? x : 0.0f;
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) m = fmaxf(m, fabsf(v[c]));
+    const float e = guard_scale(block_max256(m, red));
+    if (threadIdx.x == 0) escale[blockIdx.x] = e;
+    uint8_t *y = xq + (size_t) blockIdx.x * row_bytes;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int i = threadIdx.x + 256 * c;
+        q8_1_store(i < n ? v[c] / e : 0.0f, y, i / 32, i % 32);
+    }
+}
+
 __global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ act,
                          int64_t total) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -169,8 +196,15 @@ int amax_guard_q8_1(const float *act, float *escale, void *xq, int n, int rows, 
     if (!act || !escale || !xq || n <= 0 || rows < 0)
         return host::set_error(host::ERR_SHAPE, "amax_guard_q8_1: bad arguments");
     if (rows == 0) return host::OK;
-    hipLaunchKernelGGL(k_amax_guard_q8_1, dim3((unsigned) rows), dim3(256), 0, st, act, escale, (uint8_t *) xq, n,
-                       host::q8_1_row_bytes(n));
+    const int64_t npad = host::pad512(n), rb = host::q8_1_row_bytes(n);
+    if (npad <= 512)
+        hipLaunchKernelGGL(k_amax_guard_q8_1_reg<2>, dim3((unsigned) rows), dim3(256), 0, st, act, escale, (uint8_t *) xq, n, rb);
+    else if (npad <= 1024)
+        hipLaunchKernelGGL(k_amax_guard_q8_1_reg<4>, dim3((unsigned) rows), dim3(256), 0, st, act, escale, (uint8_t *) xq, n, rb);
+    else if (npad <= 2048)
+        hipLaunchKernelGGL(k_amax_guard_q8_1_reg<8>, dim3((unsigned) rows), dim3(256), 0, st, act, escale, (uint8_t *) xq, n, rb);
+    else
+        hipLaunchKernelGGL(k_amax_guard_q8_1, dim3((unsigned) rows), dim3(256), 0, st, act, escale, (uint8_t *) xq, n, rb);
     return host::check_launch("amax_guard_q8_1");
 }
 

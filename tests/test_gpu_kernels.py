@@ -256,9 +256,12 @@ def test_moe_combine_bit_exact(ops, k, n):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-def test_amax_guard_q8_1(ops):
-    rng = np.random.default_rng(12)
-    act = gaussian(rng, (4, F), 0.5)
+@pytest.mark.parametrize("n", [96, 512, F, 2048, 2560])
+def test_amax_guard_q8_1(ops, n):
+    """Rows of every width class of the kernel (register-held rows up to 2048 padded columns, the looping form
+    beyond): the guard scales and the Q8_1 bytes bit-exact."""
+    rng = np.random.default_rng(12 + n)
+    act = gaussian(rng, (4, n), 0.5)
     act[1] *= 5000.0  # amax > 1024: e = 2^k
     escale, xq = ops.amax_guard_q8_1(dev(act))
     e = host(escale)
