@@ -9,7 +9,7 @@ renormalisation, SwiGLU experts of width 768, gate/up/down Q4_K (ggml reference 
 router N(0, 0.02), x ~ N(0, 1) fresh per layer and step. A "step" is one token through L resident copies of that
 layer (distinct weights, L * 340 MB > the 256 MB Infinity Cache, so every layer streams its experts from HBM);
 value = step time / L. All inputs are resident in HBM before the timed region; each layer is the library's
-three-kernel fns_hip_moe_layer call, replayed from a HIP graph.
+fns_hip_moe_layer call, replayed from a HIP graph, with the read-ahead hint naming the next layer's router.
 
 The JSON line also carries:
   roofline     - for the dominant kernel (k_layer_fused: routing, gate/up + SwiGLU, Q8_1 of act, down, combine):
@@ -61,7 +61,16 @@ def log(msg: str) -> None:
 
 
 def build_layers(synth, n: int, gu: int, dn: int, seed_base: int):
-    return [synth.build_layer(H, F, NE, K_TOP, gu, dn, SEED, layer=seed_base + l) for l in range(n)]
+    return link_prefetch([synth.build_layer(H, F, NE, K_TOP, gu, dn, SEED, layer=seed_base + l) for l in range(n)])
+
+
+def link_prefetch(layers):
+    """Each layer's read-ahead hint names the next layer's router (FnsMoeLayer.prefetch), as an engine stepping
+    through its layers would pass it; the outputs do not depend on it."""
+    for l, layer in enumerate(layers):
+        nxt = layers[(l + 1) % len(layers)].router_w
+        layer.desc.prefetch, layer.desc.prefetch_bytes = nxt.data_ptr(), nxt.numel() * nxt.element_size()
+    return layers
 
 
 def make_xs(synth, torch, n_tok: int, n_steps: int, n_layers: int, seed_layer0: int):
@@ -105,6 +114,7 @@ def run_flint(torch, synth, n_layers: int = 8, replays: int = 40, gu: int = Q4_K
                   for l in range(n_layers)]
     else:
         layers = [synth.build_flint_layer(H, 512, 256, 6, 1024, gu, dn, SEED, layer=600 + l) for l in range(n_layers)]
+    link_prefetch(layers)
     xs = [synth.activations(1, H, SEED, layer=700 + l) for l in range(n_layers)]
     outs = [torch.empty(1, H, device="cuda") for _ in layers]
     wss = [layer.workspace(1) for layer in layers]

@@ -251,6 +251,7 @@ class MoeLayerDesc(ctypes.Structure):
         ("ffn_norm", ctypes.c_void_p), ("norm_eps", ctypes.c_float), ("shexp_inter", ctypes.c_int),
         ("shexp_gu_type", ctypes.c_int), ("shexp_down_type", ctypes.c_int),
         ("shexp_gate", ctypes.c_void_p), ("shexp_up", ctypes.c_void_p), ("shexp_down", ctypes.c_void_p),
+        ("prefetch", ctypes.c_void_p), ("prefetch_bytes", ctypes.c_size_t),
     ]
 
 

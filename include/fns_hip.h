@@ -141,6 +141,12 @@ typedef struct FnsMoeLayer {
     int shexp_gu_type, shexp_down_type;  /* K-quant types of the shared expert's gate/up and down (0: gu_type / down_type) */
     const void *shexp_gate, *shexp_up;   /* [shexp_inter][hidden] blocks */
     const void *shexp_down;              /* [hidden][shexp_inter] blocks */
+    /* No counterpart in the reference: a read-ahead hint. NULL, or device bytes the next call will read first
+     * (normally the next layer's router_w, prefetch_bytes = its size): the decode router kernel reads them along with
+     * its own work so that they sit in the memory-side cache (MI355X Infinity Cache) when the next layer's router
+     * reads them. Results do not depend on it. */
+    const void *prefetch;
+    size_t prefetch_bytes;
 } FnsMoeLayer;
 
 int fns_hip_moe_workspace_layout(const FnsMoeLayer *layer, int n_tok, size_t *offsets, size_t *total_bytes);

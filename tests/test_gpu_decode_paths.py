@@ -158,3 +158,26 @@ def test_status_word_shared_by_shapes(ops, synth):
         assert small.status(None, 1) == ops.STATUS_EXCHANGE_TIMEOUT and big.status(None, 4) == ops.STATUS_EXCHANGE_TIMEOUT
     assert small.status(None, 1, clear=True) == ops.STATUS_EXCHANGE_TIMEOUT
     assert big.status(None, 1) == 0
+
+
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_prefetch_hint_changes_nothing(ops, synth, n_tok):
+    """The read-ahead hint (FnsMoeLayer.prefetch: the next layer's router) leaves every output and intermediate
+    bit-identical, for sizes below, at and above the router kernel's two loads per thread and not a multiple of 16."""
+    print(f"prefetch hint n_tok={n_tok}", flush=True)
+    a = synth.build_layer(H, F, NE, K, 12, 12, SEED, layer=901)
+    b = synth.build_layer(H, F, NE, K, 12, 12, SEED, layer=902)
+    x = synth.activations(n_tok, H, SEED, layer=903)
+    ws = a.workspace(n_tok)
+    ref = host(a(x, ws=ws))
+    ref_tr = {k: host(v).copy() for k, v in a.trace(ws, n_tok).items()}
+    big = torch.zeros(5 << 20, dtype=torch.uint8, device="cuda")
+    for ptr, nbytes in ((b.router_w.data_ptr(), b.router_w.numel() * 4), (b.router_w.data_ptr(), 1000),
+                        (big.data_ptr(), big.numel() - 7), (b.router_w.data_ptr(), 0)):
+        a.desc.prefetch, a.desc.prefetch_bytes = ptr, nbytes
+        ws.zero_()
+        out = host(a(x, ws=ws))
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), f"prefetch {nbytes} B: output differs"
+        for k, v in a.trace(ws, n_tok).items():
+            assert np.array_equal(host(v), ref_tr[k]), f"prefetch {nbytes} B: {k} differs"
+    a.desc.prefetch, a.desc.prefetch_bytes = None, 0
