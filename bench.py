@@ -407,6 +407,8 @@ def main() -> int:
                     help="profiling mode for rocprofv3: only N back-to-back rounds of the three kernels + a 256 MiB copy")
     ap.add_argument("--profile-prefill", type=int, default=0,
                     help="profiling mode for rocprofv3: only N rounds of config-4 prefill over 2 layers + a 256 MiB copy")
+    ap.add_argument("--profile-dense", type=int, default=0,
+                    help="profiling mode for rocprofv3: only N rounds of the dense Q8_0 FFN prefill and Q8_0 mmq")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the MoE layer would shard "
@@ -421,6 +423,15 @@ def main() -> int:
     torch.cuda.init()
     dev = torch.cuda.get_device_properties(0)
     log(f"device {dev.name} {dev.gcnArchName if hasattr(dev, 'gcnArchName') else ''} CUs {dev.multi_processor_count}")
+
+    if args.profile_dense:
+        r = run_dense_q8_0(torch, n_layers=2, replays=args.profile_dense)
+        a = torch.empty(64 << 20, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)  # 256 MiB read + 256 MiB write: FETCH_SIZE / WRITE_SIZE calibration
+        torch.cuda.synchronize()
+        log(f"profile dense done: {r}")
+        return 0
 
     if args.profile_prefill:
         r = run_prefill(torch, synth, n_layers=2, replays=args.profile_prefill)
