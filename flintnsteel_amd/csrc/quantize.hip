@@ -139,7 +139,12 @@ __global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ 
     act[i] = x / (1.0f + fns_expf(-x)) * u[i];
 }
 
-// out = x + y, four elements per thread (n4 = n / 4 float4s), then the tail
+// out = x + y, one element per thread (any alignment)
+__global__ void k_add1(const float *x, const float *y, float *out, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = x[i] + y[i];
+}
+// out = x + y, four elements per thread (n4 = n / 4 float4s; 16-byte aligned arrays), then the tail
 __global__ void k_add(const float *x, const float *y, float *out, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t n4 = n / 4;
@@ -218,9 +223,11 @@ int swiglu(const float *g, const float *u, float *act, int n, int rows, hipStrea
 
 int add(const float *x, const float *y, float *out, int64_t n, hipStream_t st) {
     if (!x || !y || !out || n < 0) return host::set_error(host::ERR_SHAPE, "add: bad arguments");
-    if (((uintptr_t) x | (uintptr_t) y | (uintptr_t) out) % 16)
-        return host::set_error(host::ERR_SHAPE, "add: arrays must be 16-byte aligned");
     if (n == 0) return host::OK;
+    if (((uintptr_t) x | (uintptr_t) y | (uintptr_t) out) % 16) {
+        hipLaunchKernelGGL(k_add1, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, x, y, out, n);
+        return host::check_launch("add");
+    }
     const int64_t threads = n / 4 + n % 4;
     hipLaunchKernelGGL(k_add, dim3((unsigned) ((threads + 255) / 256)), dim3(256), 0, st, x, y, out, n);
     return host::check_launch("add");

@@ -131,4 +131,3 @@ def test_dense_ffn_host_checks():
     d.down, d.gate_type = ptr, 10  # Q2_K: no GEMV kernel
     assert L.fns_hip_dense_ffn(ctypes.byref(d), ptr, ptr, 1, ctypes.addressof(ws), t1.value, None) == -1
     assert L.fns_hip_dense_ffn(ctypes.byref(d), ptr, ptr, 0, None, 0, None) == 0  # no tokens: no-op
-    assert L.fns_hip_add(ptr, ptr + 4, ptr, 8, None) == -2  # misaligned

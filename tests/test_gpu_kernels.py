@@ -291,3 +291,16 @@ def test_count_routes(ops):
     ops.count_routes(ids, counts)
     c = host(counts.to(torch.int64))
     assert c[3] == 4 and c[5] == 2 and c[127] == 2 and c[0] == 2 and c.sum() == 12
+
+
+@pytest.mark.parametrize("n,off", [(4096, 0), (1027, 0), (1027, 1), (5, 3)])
+def test_add(ops, n, off):
+    """out = x + y (the reference's add_inplace, out-of-place), float4 form and the element form for arrays that
+    are not 16-byte aligned; in place too."""
+    rng = np.random.default_rng(n + off)
+    x, y = gaussian(rng, (n + off,)), gaussian(rng, (n + off,))
+    xd, yd = dev(x), dev(y)
+    got = host(ops.add(xd[off:], yd[off:]))
+    assert np.array_equal(got, (x[off:] + y[off:]).astype(np.float32))
+    ops.add(xd[off:], yd[off:], out=xd[off:])
+    assert np.array_equal(host(xd)[off:], got)

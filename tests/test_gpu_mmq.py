@@ -559,3 +559,26 @@ def test_moe_prefill_fused_wait_timeout_is_reported(ops):
     assert pre.status(ws, T) == 0
     again = host(pre(x, ws=ws))
     assert np.array_equal(again, good) and pre.status(ws, T) == 0
+
+
+def test_moe_prefill_fused_launch_with_shared_expert_in_place(ops):
+    """The fused gate/up + down launch with everything the layer adds around it: the shared expert, RMSNorm,
+    sigmoid gating over 256 experts, and the residual in place (out = x_resid) - bit for bit against the same layer
+    with the F16 guard on (two GEMM launches; no row scaled)."""
+    from flintnsteel_amd import synth
+    H, F, NE, K, FS, T = 2048, 512, 256, 6, 1024, 200
+    print("fused launch with shared expert, in place", flush=True)
+    lay = synth.build_flint_layer(H, F, NE, K, FS, orc.Q4_K, orc.Q4_K, 20261022, layer=55, guard=False)
+    twin = ops.MoeLayer(lay.router_w, lay.slots, orc.Q4_K, orc.Q4_K, H, F, K, gating=ops.GATING_SIGMOID, guard=True,
+                        ffn_norm=lay.ffn_norm, norm_eps=1e-6, shexp=lay.shexp)
+    fused, two = ops.MoePrefill(lay), ops.MoePrefill(twin)
+    x = synth.activations(T, H, seed=20261022, layer=56)
+    r1, r2 = synth.activations(T, H, seed=20261022, layer=57), synth.activations(T, H, seed=20261022, layer=57)
+    ws_f, ws_t = fused.workspace(T), two.workspace(T)
+    fused(x, out=r1, ws=ws_f, x_resid=r1)
+    two(x, out=r2, ws=ws_t, x_resid=r2)
+    a, b = host(r1), host(r2)
+    assert (host(two.trace(ws_t, T)["escale"]) == 1.0).all()
+    assert fused.status(ws_f, T) == 0
+    rows = np.flatnonzero((a != b).any(axis=1))
+    assert np.isfinite(a).all() and rows.size == 0, f"rows {rows[:16].tolist()} of {rows.size} differ"
