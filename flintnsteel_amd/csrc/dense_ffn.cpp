@@ -7,6 +7,8 @@
 //     rms_norm_mul), mmq of gate and of up, swiglu, mmq of down, out = x + ffn.
 // The GEMMs are the dense forms of the MoE path's kernels (mmvq.hip, mmq.hip); the layer adds no kernel of its own
 // beyond the residual add.
+#include <cstdint>
+
 #include "fns_host.hpp"
 #include "fns_internal.hpp"
 
@@ -80,6 +82,8 @@ int dense_ffn(const FnsDenseFfn *D, const float *x, float *out, int64_t n_tok, v
         FNS_TRY(swiglu(w.gate, w.act, w.act, F, n, st));
         FNS_TRY(mmq(D->down_type, D->down, F, H, w.act, n_tok, w.xq, w.ffn, st));
     } else {
+        if ((int64_t) n * F > INT32_MAX)
+            return host::set_error(host::ERR_SHAPE, "dense_ffn: decode form limited to n_tok * inter < 2^31 values");
         if (!host::is_supported(D->gate_type) || !host::is_supported(D->up_type) || !host::is_supported(D->down_type))
             return host::set_error(host::ERR_TYPE, "dense_ffn: a matrix type the GEMV kernels do not support");
         if (D->ffn_norm) FNS_TRY(rms_norm_q8_1(x, D->ffn_norm, w.h, w.xq, H, D->norm_eps, n, st));
