@@ -202,9 +202,11 @@ def test_mmvq_vs_exact_input(ops, gate_up_mats):
 
 @pytest.mark.parametrize("n_expert,k,gating", [(128, 8, 0), (256, 6, 1), (100, 8, 0), (256, 8, 0), (64, 1, 1),
                                                (128, 16, 0)])
-def test_route_topk_bit_exact(ops, n_expert, k, gating):
-    rng = np.random.default_rng(n_expert * 31 + k)
-    logits = gaussian(rng, (5, n_expert), 2.0)
+@pytest.mark.parametrize("n_tok", [5, 70])
+def test_route_topk_bit_exact(ops, n_expert, k, gating, n_tok):
+    """Both launch forms (1024 threads per token up to 64 tokens, 256 beyond) against the oracle, with ties."""
+    rng = np.random.default_rng(n_expert * 31 + k + n_tok)
+    logits = gaussian(rng, (n_tok, n_expert), 2.0)
     logits[1, 10:20] = 1.5        # exact ties: the lower index wins
     logits[2] = 0.0               # all equal
     ids, w = ops.route_topk(dev(logits), k, gating)
