@@ -4,7 +4,9 @@
 //     mmvq_swiglu of gate and up at one token (two mmvq and glu_mmvq at more, or when gate and up differ in type:
 //     the same bits), quantize_q8_1 of act, mmvq of down, out = x + ffn;
 //   prefill (reference src/engine.cu:331-337): rms_norm (the f32 output of rms_norm_q8_1, the reference's
-//     rms_norm_mul), mmq of gate and of up, swiglu, mmq of down, out = x + ffn.
+//     rms_norm_mul), mmq of gate and of up, swiglu, mmq of down, out = x + ffn. When gate and up share a type the
+//     tiled GEMM takes, gate and up run as one GLU launch (SwiGLU and act's Q8_1 in the epilogue, as the MoE
+//     path's shared expert) and down with its K range split in up to 4 parts summed with the residual add.
 // The GEMMs are the dense forms of the MoE path's kernels (mmvq.hip, mmq.hip); the layer adds no kernel of its own
 // beyond the residual add.
 #include <cstdint>
@@ -16,8 +18,10 @@ namespace fns::impl {
 
 namespace {
 
+constexpr int kMaxParts = 4;  // K-split parts of the prefill form's down GEMM
+
 struct DenseWs {
-    float *h, *gate, *act, *ffn;
+    float *h, *gate, *act, *ffn, *parts;
     void *xq;
     size_t total;
 };
@@ -38,6 +42,7 @@ DenseWs dense_layout(const FnsDenseFfn *D, int64_t n, uint8_t *base) {
     w.act = (float *) (base + off), off += sf;
     w.ffn = (float *) (base + off), off += sh;
     w.xq = base + off, off += align256(sq);
+    w.parts = (float *) (base + off), off += (size_t) kMaxParts * sh;
     w.total = off;
     return w;
 }
@@ -72,6 +77,23 @@ int dense_ffn(const FnsDenseFfn *D, const float *x, float *out, int64_t n_tok, v
         return host::set_error(host::ERR_SHAPE, "dense_ffn: workspace of %zu bytes, %zu needed", ws_bytes, w.total);
     const int H = D->hidden, F = D->inter, n = (int) n_tok;
     const float *h = x;
+    if (prefill && D->gate_type == D->up_type && mmq_tiled(D->gate_type, H, F) && mmq_tiled(D->down_type, F, H)) {
+        // the tiled GEMMs on images built once: x image, gate + up in one launch (SwiGLU and the Q8_1 of act in its
+        // epilogue, the act images land in the gate/act region), down with its K range split so that the launch
+        // fills the GPU, then out = x + (sum of the parts)
+        if (D->ffn_norm) {
+            FNS_TRY(rms_norm_q8_1(x, D->ffn_norm, w.h, w.xq, H, D->norm_eps, n, st));
+            h = w.h;
+        }
+        FNS_TRY(mmq_quant_image(h, H, n_tok, w.xq, st));
+        void *act_img = w.gate;  // n x F image bytes (4.125 per value) fit the gate and act regions together
+        FNS_TRY(mmq_dense_glu(D->gate_type, D->gate, D->up, H, F, w.xq, n_tok, act_img, st));
+        const int64_t items = (n_tok + 63) / 64 * ((H + 255) / 256);
+        int parts = 1;
+        while (parts < kMaxParts && items * parts * 2 <= 512 && F / 256 >= parts * 2) parts *= 2;
+        FNS_TRY(mmq_dense_parts(D->down_type, D->down, F, H, act_img, n_tok, w.parts, parts, st));
+        return add_parts(x, w.parts, parts, out, (int64_t) n * H, st);
+    }
     if (prefill) {
         if (D->ffn_norm) {
             FNS_TRY(rms_norm_q8_1(x, D->ffn_norm, w.h, w.xq, H, D->norm_eps, n, st));

@@ -75,6 +75,12 @@ int mmq_gemm_experts(int type, const char *const *table, size_t off_a, size_t of
                      float *act_out, hipStream_t st);
 int mmq(int type, const void *w, int64_t ncols, int64_t nrows, const float *x, int64_t n_tok, void *xq, float *dst,
         hipStream_t st);
+int mmq_dense_glu(int type, const void *gate, const void *up, int64_t ncols, int64_t nrows, const void *ximg,
+                  int64_t n_tok, void *act_img, hipStream_t st);
+int mmq_dense_parts(int type, const void *w, int64_t ncols, int64_t nrows, const void *ximg, int64_t n_tok, float *dst,
+                    int ksplit, hipStream_t st);
+bool mmq_tiled(int type, int64_t ncols, int64_t nrows);  // the tiled GEMM takes this type and shape
+int add_parts(const float *x, const float *parts, int n_parts, float *out, int64_t n, hipStream_t st);
 int mmq_experts(int type, const char *const *table, size_t off, int64_t ncols, int64_t nrows, int64_t n_expert,
                 const float *x, int64_t x_rows_per_tok, int64_t n_tok, const int32_t *ids, int64_t n_used,
                 int32_t *ids_src1, int32_t *ids_dst, int32_t *bounds, void *xq, float *dst, hipStream_t st);

@@ -332,6 +332,8 @@ struct MmqArgs {
     const int32_t *dst_rows;   // sorted position -> output row (null: identity)
     int n_rows;                // dense: number of activation rows
     int dense_small;           // dense: 1 = groups of 32 activation rows (one tile), 0 = of 64
+    int ksplit;                // dense, non-GLU: > 1 = the K range split into ksplit parts (blockIdx.y), part p's
+    int64_t part_stride;       //   partial sums written at dst + p * part_stride floats
     float *dst;                // [out row][nrows] f32 (non-GLU)
     uint8_t *out_pack;         // GLU: act split image rows (by output row)
     int64_t out_img;
@@ -865,6 +867,15 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
         if constexpr (MIN) dma16<CPOL>(rx, sh_s + srow * kRowS, so, (uint32_t) (kb * kSbMin));
     };
 
+    // the superblocks [kb0, kb_end) of this item: all of them, or part blockIdx.y of a split K range
+    int kb0 = 0, kb_end = nb, part = 0;
+    if constexpr (!GLU && !DEV) {
+        if (a.ksplit > 1) {
+            part = (int) blockIdx.y;
+            kb0 = part * nb / a.ksplit;
+            kb_end = (part + 1) * nb / a.ksplit;
+        }
+    }
     WFrag<T> f0, f1, n0, n1;
     bool failed = false;
     if constexpr (DEV && !GLU) {  // the first weights in flight, then the wait for the group's act rows
@@ -874,10 +885,10 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
         dma_chunk(sh_a0, 0, 0);
         dma_sums(0);
     } else {
-        dma_chunk(sh_a0, 0, 0);
-        dma_sums(0);
-        wfrag_load<T, 0>(r0, v0, c0, 0, f0);
-        wfrag_load<T, 0>(r1, v1, c1, 0, f1);
+        dma_chunk(sh_a0, kb0, 0);
+        dma_sums(kb0);
+        wfrag_load<T, 0>(r0, v0, c0, (uint32_t) (kb0 * BB), f0);
+        wfrag_load<T, 0>(r1, v1, c1, (uint32_t) (kb0 * BB), f1);
     }
     dma_wait();
     lds_barrier();
@@ -983,7 +994,7 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
     // one superblock with fragments f0, f1 (current; their first part loaded) and n0, n1 (next, first part loaded here)
     auto superblock = [&](int kb, WFrag<T> &f0, WFrag<T> &f1, WFrag<T> &n0, WFrag<T> &n1)
                           __attribute__((always_inline)) {
-        const bool more = kb + 1 < nb;
+        const bool more = kb + 1 < kb_end;
         const int kn = more ? kb + 1 : kb;  // the last superblock reloads itself: same load count every iteration
         dma_chunk(sh_a1, kb, 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -1061,9 +1072,9 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
         MMQ_MARK(2 + kb);
     };
     // the fragment sets swap roles every superblock
-    for (int kb = 0; kb < nb; kb += 2) {
+    for (int kb = kb0; kb < kb_end; kb += 2) {
         superblock(kb, f0, f1, n0, n1);
-        if (kb + 1 < nb) superblock(kb + 1, n0, n1, f0, f1);
+        if (kb + 1 < kb_end) superblock(kb + 1, n0, n1, f0, f1);
     }
 
     dma_wait();  // the last (unused) sums load
@@ -1075,7 +1086,7 @@ __device__ __forceinline__ void mmq_group(const MmqArgs &a, int g, int wb, const
             for (int r = 0; r < 16; ++r) {
                 const int i = t * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
                 if (i < cnt) {
-                    float *o = a.dst + (size_t) sh_dst[i] * a.nrows;
+                    float *o = a.dst + (size_t) part * a.part_stride + (size_t) sh_dst[i] * a.nrows;
                     if (row0 < a.nrows) o[row0] = failed ? __builtin_nanf("") : acc[t][0][r];
                     if (row0 + 128 < a.nrows) o[row0 + 128] = failed ? __builtin_nanf("") : acc[t][1][r];
                 }
@@ -1271,14 +1282,17 @@ int launch_mmq(int type, bool glu, const MmqArgs &a, int groups, hipStream_t st)
     // more B decode per MFMA, but twice the workgroups; measured faster for 64 -> 128 workgroups, slower for
     // 192 -> 384)
     arg.dense_small = 0;
-    if (!a.bounds && a.n_rows > 32 && (int64_t) 2 * groups * arg.n_cb <= 256) {
+    const int ks = !glu && !a.bounds && a.ksplit > 1 ? a.ksplit : 1;
+    if (ks > 1 && (a.ncols / 256 < ks || ks > 8)) return host::set_error(host::ERR_SHAPE, "mmq: bad K split");
+    arg.ksplit = ks;
+    if (!a.bounds && a.n_rows > 32 && (int64_t) 2 * groups * arg.n_cb * ks <= 256) {
         arg.dense_small = 1;
         total = (a.n_rows + 31) / 32;
     }
     arg.n_groups = total;
     const int64_t items = (int64_t) arg.n_cb * kXcds * ((total + kXcds - 1) / kXcds);
     if (items > INT32_MAX) return host::set_error(host::ERR_SHAPE, "mmq: grid too large");
-    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) items), dim3(kMmqThreads), args, 0, st);
+    const hipError_t e = hipLaunchKernel(fn, dim3((unsigned) items, (unsigned) ks), dim3(kMmqThreads), args, 0, st);
     if (e != hipSuccess) return host::set_error(host::ERR_LAUNCH, "mmq: %s", hipGetErrorString(e));
     return host::check_launch("mmq");
 }
@@ -1557,6 +1571,48 @@ int mmq_dense_shared(const FnsMoeLayer *L, const void *ximg, int64_t n_tok, void
     d.n_rows = (int) n_tok;
     d.dst = sh;
     return launch_mmq(dt, false, d, groups, st);
+}
+
+// Dense GEMMs on activation images already built (the dense FFN block): gate/up in one GLU launch (SwiGLU and the
+// Q8_1 of act in the epilogue, act images out), and a plain launch whose K range may be split into ksplit parts
+// (dst then holds ksplit partial sums, part_stride floats apart).
+bool mmq_tiled(int type, int64_t ncols, int64_t nrows) {
+    const bool t = host::is_kquant(type) || type == T_Q8_0 || (host::is_iq(type) && (!host::iq_needs_grid(type) ||
+                                                                                      host::iq_grids_ready()));
+    return t && ncols > 0 && ncols % 256 == 0 && ncols <= 65536 && nrows > 0 && nrows % kMmqRows == 0;
+}
+
+int mmq_dense_glu(int type, const void *gate, const void *up, int64_t ncols, int64_t nrows, const void *ximg,
+                  int64_t n_tok, void *act_img, hipStream_t st) {
+    FNS_TRY(check_mmq_shape(type, ncols, nrows));
+    MmqArgs g{};
+    g.w_dense = (const uint8_t *) gate;
+    g.off_a = 0;
+    g.off_b = (const uint8_t *) up - (const uint8_t *) gate;
+    g.ncols = (int) ncols;
+    g.nrows = (int) nrows;
+    g.xpack = (const uint8_t *) ximg;
+    g.x_img = (int64_t) mmq_image_bytes(ncols);
+    g.n_rows = (int) n_tok;
+    g.out_pack = (uint8_t *) act_img;
+    g.out_img = (int64_t) mmq_image_bytes(nrows);
+    return launch_mmq(type, true, g, (int) ((n_tok + kMmqTok - 1) / kMmqTok), st);
+}
+
+int mmq_dense_parts(int type, const void *w, int64_t ncols, int64_t nrows, const void *ximg, int64_t n_tok, float *dst,
+                    int ksplit, hipStream_t st) {
+    FNS_TRY(check_mmq_shape(type, ncols, nrows));
+    MmqArgs d{};
+    d.w_dense = (const uint8_t *) w;
+    d.ncols = (int) ncols;
+    d.nrows = (int) nrows;
+    d.xpack = (const uint8_t *) ximg;
+    d.x_img = (int64_t) mmq_image_bytes(ncols);
+    d.n_rows = (int) n_tok;
+    d.dst = dst;
+    d.ksplit = ksplit;
+    d.part_stride = n_tok * nrows;
+    return launch_mmq(type, false, d, (int) ((n_tok + kMmqTok - 1) / kMmqTok), st);
 }
 
 namespace {

@@ -139,6 +139,15 @@ __global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ 
     act[i] = x / (1.0f + fns_expf(-x)) * u[i];
 }
 
+// out = x + ((p_0 + p_1) + ...) over n_parts partial sums of n values each (in part order), one element per thread
+__global__ void k_add_parts(const float *x, const float *parts, int n_parts, float *out, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float s = parts[i];
+    for (int p = 1; p < n_parts; ++p) s = s + parts[(size_t) p * n + i];
+    out[i] = x[i] + s;
+}
+
 // out = x + y, one element per thread (any alignment)
 __global__ void k_add1(const float *x, const float *y, float *out, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -219,6 +228,13 @@ int swiglu(const float *g, const float *u, float *act, int n, int rows, hipStrea
     if (total == 0) return host::OK;
     hipLaunchKernelGGL(k_swiglu, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, st, g, u, act, total);
     return host::check_launch("swiglu");
+}
+
+int add_parts(const float *x, const float *parts, int n_parts, float *out, int64_t n, hipStream_t st) {
+    if (!x || !parts || !out || n < 0 || n_parts < 1) return host::set_error(host::ERR_SHAPE, "add_parts: bad arguments");
+    if (n == 0) return host::OK;
+    hipLaunchKernelGGL(k_add_parts, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, x, parts, n_parts, out, n);
+    return host::check_launch("add_parts");
 }
 
 int add(const float *x, const float *y, float *out, int64_t n, hipStream_t st) {
