@@ -286,6 +286,19 @@ struct IqGrids {
     uint64_t iq2s[1024];
 };
 static __device__ IqGrids g_iq_grids;
+// LDS copies of the two small codebooks (1 and 2 KiB) for the GEMV kernels: an LDS read per lookup instead of a
+// gathered global load. Every kernel that decodes IQ3_XXS or IQ3_S blocks fills them first (iq_grids_to_lds) and
+// reaches a workgroup barrier before its first lookup. (The 8 KiB IQ2_S codebook stays in global memory.)
+static __shared__ uint32_t s_iq3xxs_grid[256];
+static __shared__ uint32_t s_iq3s_grid[512];
+template <int T> __device__ __forceinline__ void iq_grids_to_lds(int tid, int nthreads) {
+    if constexpr (T == T_IQ3_XXS) {
+        for (int i = tid; i < 256; i += nthreads) s_iq3xxs_grid[i] = g_iq_grids.iq3xxs[i];
+    } else if constexpr (T == T_IQ3_S) {
+        for (int i = tid; i < 512; i += nthreads) s_iq3s_grid[i] = g_iq_grids.iq3s[i];
+    }
+}
+template <int T> constexpr bool kIqLdsGrid = T == T_IQ3_XXS || T == T_IQ3_S;
 
 // The IQ4_NL values {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113} as four byte tables.
 constexpr uint32_t kIq4T0 = 0xBFAD9881u, kIq4T1 = 0xF6EADDCFu, kIq4T2 = 0x26190D01u, kIq4T3 = 0x71594535u;
@@ -342,7 +355,7 @@ __device__ __forceinline__ float iq3xxs_quarter(const uint8_t *blk, const ActQ &
         for (int l = 0; l < 4; ++l) {
             const uint32_t idx = l < 2 ? i0 : i1, sh = 16 * (l & 1);
             const uint32_t sg = ksigns((aux >> (7 * l)) & 127u);
-            const uint32_t g0 = g_iq_grids.iq3xxs[(idx >> sh) & 0xffu], g1 = g_iq_grids.iq3xxs[(idx >> (sh + 8)) & 0xffu];
+            const uint32_t g0 = s_iq3xxs_grid[(idx >> sh) & 0xffu], g1 = s_iq3xxs_grid[(idx >> (sh + 8)) & 0xffu];
             s = dot4(signed_grid(g0, spread4(sg & 0xfu)), x.a[8 * h + 2 * l], s);
             s = dot4(signed_grid(g1, spread4(sg >> 4)), x.a[8 * h + 2 * l + 1], s);
         }
@@ -367,7 +380,7 @@ __device__ __forceinline__ float iq3s_quarter(const uint8_t *blk, const ActQ &x,
         for (int l = 0; l < 8; ++l) {
             const uint32_t gi = (((l < 4 ? i0 : i1) >> (8 * (l & 3))) & 0xffu) | (((qh >> l) & 1u) << 8);
             const uint32_t sb = (sg >> (4 * l)) & 0xfu;  // byte l/2, nibble l%2
-            s = dot4(signed_grid(g_iq_grids.iq3s[gi], spread4(sb)), x.a[8 * h + l], s);
+            s = dot4(signed_grid(s_iq3s_grid[gi], spread4(sb)), x.a[8 * h + l], s);
         }
         s *= 1 + 2 * (int) ((scw >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xfu);
         acc += (d * x.d[h]) * (float) s;

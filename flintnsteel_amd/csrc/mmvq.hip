@@ -258,6 +258,7 @@ __global__ __launch_bounds__(256) void k_mmvq_q(const MmvqParams p) {
         img[j] = act_img(smem + j * ib, npad);
         if (j < ncol) stage_q8_1_img(p.xq + (int64_t) xrow[j] * p.xq_row_bytes, npad, smem + j * ib, tid, 256);
     }
+    iq_grids_to_lds<T>(tid, 256);  // (visible after the barrier)
     __syncthreads();
     const int nblk = p.ncols / 256, lane = tid % LPR;
     const int row = blockIdx.x * (256 / LPR) + tid / LPR;

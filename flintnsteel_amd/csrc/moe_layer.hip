@@ -467,6 +467,7 @@ __global__ __launch_bounds__(NTH) void k_gate_up_q(const LayerArgs a) {
     const int xbytes = img_bytes(npad);
     const int wgid = blockIdx.y * gridDim.x + blockIdx.x;
     FNS_MARK(1, wgid, 0);
+    iq_grids_to_lds<TQ>(tid, NTH);  // the codebook (IQ3_XXS / IQ3_S), visible after the barriers before the dots
 
     __shared__ const uint8_t *s_tab[256];
     // waves 1..NW-1: the x images and the expert table (so the slot address is an LDS read once routing is done)
@@ -572,6 +573,7 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
     const int nblk = F / 256;
     const int row_bytes = nblk * BB;
     FNS_MARK(2, blockIdx.x, 0);
+    iq_grids_to_lds<TQ>(tid, kQThreads);  // the codebook (IQ3_XXS / IQ3_S), visible after the barriers below
 
     dma_waves_from<kQWaves>(smem, a.apack, CH * fbytes, 0);
     if (tid < CH) {
@@ -729,6 +731,9 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     uint8_t *s_gu = s_a + K * fbytes + fsbytes;  // [32 up rows | 32 gate rows]
     uint8_t *s_dn = s_gu + 2 * gu_region;  // [K][8 down rows], then the shared expert's 8 rows
     FNS_MARK(1, blockIdx.x, 0);
+    // the codebooks (IQ3_XXS / IQ3_S) into LDS, visible after the routing's barriers
+    iq_grids_to_lds<TGU>(tid, kQThreads);
+    if constexpr (TDN != TGU) iq_grids_to_lds<TDN>(tid, kQThreads);
 
     // 1. waves 1-15: x image and expert table; wave 0: logits. Routing (all selected slots are needed here).
     if (wave != 0 && tid - kWave < a.NE)
