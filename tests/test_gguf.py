@@ -270,7 +270,7 @@ def _dense_ref(arrays, gt, ut, dt, h_dim, f_dim, x: np.ndarray, eps: float) -> n
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", ["small", "flint"])
+@pytest.mark.parametrize("shape", ["small", "small_same", "flint", "flint_k"])
 def test_gguf_dense_ffn(tmp_path, shape):
     """A dense FFN block loaded from GGUF (fns_hip_dense_ffn_from_gguf) equals the same block built from the arrays,
     bit for bit, in the decode (1 and 4 tokens) and prefill forms, and both forms match the float64 chain. "flint" is
@@ -278,8 +278,11 @@ def test_gguf_dense_ffn(tmp_path, shape):
     import torch
     from flintnsteel_amd import ops, synth
     from tests.helpers import assert_close_chain
-    h_dim, f_dim = (H, DF) if shape == "small" else (2048, 6144)
-    gt, ut, dt = (orc.Q4_K, orc.Q5_K, orc.Q6_K) if shape == "small" else (orc.Q8_0, orc.Q8_0, orc.Q6_K)
+    # small: gate / up of different types (three mmq calls); small_same, flint, flint_k: one GLU launch for gate and
+    # up and the down GEMM with its K range split (K-quant min terms in flint_k)
+    h_dim, f_dim = (H, DF) if shape.startswith("small") else (2048, 6144)
+    gt, ut, dt = {"small": (orc.Q4_K, orc.Q5_K, orc.Q6_K), "small_same": (orc.Q4_K, orc.Q4_K, orc.Q6_K),
+                  "flint": (orc.Q8_0, orc.Q8_0, orc.Q6_K), "flint_k": (orc.Q5_K, orc.Q5_K, orc.Q4_K)}[shape]
     print(f"dense ffn {shape} {h_dim}x{f_dim}", flush=True)
     path = tmp_path / "d.gguf"
     arrays = _dense_file(path, gt, ut, dt, layer=1, h=h_dim, f=f_dim)
