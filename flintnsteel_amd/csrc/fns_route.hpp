@@ -275,13 +275,99 @@ __device__ __forceinline__ void route_topk_pairs(int gtid, const float *__restri
     __syncthreads();
 }
 
+// Group form (n_expert <= 256, k <= 8, NT >= 256): gating and keys as route_topk_filter (wave 0, the same bits);
+// then each expert's rank among the 16 experts of its group (16 consecutive experts), the group's top k stored as
+// candidates (16 k of them, at group * k + rank), and the candidates ranked among themselves (eight threads per
+// candidate). The overall top k are among the groups' top k, so the selection is route_topk_filter's (the same as
+// k rounds of argmax with ties to the lower index), with three barriers and no single-wave phase after the keys.
+// Candidate slots a group does not fill (fewer than k live experts in it) hold key 0 and rank below every live key.
+// Scratch: keys [0, 256), candidates [256, 256 + 16 k).
+template <int NT>
+__device__ __forceinline__ void route_topk_groups(int gtid, const float *__restrict__ lg, int n_expert, int k,
+                                                  int gating, uint64_t *scratch, int *sel, float *pv) {
+    static_assert(NT >= 256 && NT % 64 == 0 && NT <= 1024, "one thread per expert");
+    constexpr int P = 8, CPP = NT / P;
+    uint64_t *s_key = scratch, *s_cand = scratch + 256;
+    const int tid = gtid, lane = tid % kWave, nc = 16 * k;
+    if (tid < kWave) {
+        float p[4];
+        if (gating == 0) {
+            float v[4], m = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = lane + 64 * j;
+                v[j] = e < n_expert ? lg[e] : -__builtin_inff();
+                m = fmaxf(m, v[j]);
+            }
+            m = lanes_max<64>(m);
+            float ev[4], s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ev[j] = lane + 64 * j < n_expert ? fns_expf(v[j] - m) : 0.0f;
+                s = s + ev[j];
+            }
+            s = lanes_sum<64>(s);
+            const float inv = 1.0f / s;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = ev[j] * inv;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = lane + 64 * j;
+                p[j] = e < n_expert ? 1.0f / (1.0f + fns_expf(-lg[e])) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            s_key[e] = e < n_expert ? ((uint64_t) __builtin_bit_cast(uint32_t, p[j]) << 32) | (uint32_t) ~e : 0ull;
+        }
+    } else {
+        for (int i = tid - kWave; i < nc; i += NT - kWave) s_cand[i] = 0ull;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        const int g = tid >> 4;
+        const uint64_t ke = s_key[tid];
+        int r = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            const ulonglong2 kk = *(const ulonglong2 *) (s_key + 16 * g + i);
+            r += kk.x > ke ? 1 : 0;
+            r += kk.y > ke ? 1 : 0;
+        }
+        if (r < k && ke != 0ull) s_cand[g * k + r] = ke;
+    }
+    __syncthreads();
+    const int part = tid % P;
+    for (int c0 = 0; c0 < nc; c0 += CPP) {
+        const int c = c0 + tid / P;
+        const uint64_t kc = c < nc ? s_cand[c] : 0ull;
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < 128 / P; ++j) {  // nc <= 128: every read issued before the compares
+            const int i = part + P * j;
+            rank += i < nc && s_cand[i < nc ? i : 0] > kc ? 1 : 0;
+        }
+        rank = lanes_sum_i<P>(rank);
+        if (c < nc && part == 0 && rank < k && kc != 0ull) {
+            sel[rank] = (int) ~(uint32_t) kc;
+            pv[rank] = __builtin_bit_cast(float, (uint32_t) (kc >> 32));
+        }
+    }
+    __syncthreads();
+}
+
 // Gating + top-k + renormalisation for one token by a whole workgroup (n_expert <= 256): the all-pairs rank up to
-// 128 experts, the group-maximum filter beyond (4x the pairs at 256 experts); both give the same selection.
+// 128 experts; beyond, the group form (k <= 8, workgroups of 256 threads or more) or the group-maximum filter (4x the
+// pairs at 256 experts). All give the same selection.
 // gtid: the thread's index in its group of NT (the workgroup, or one of its equal groups, each ranking its own token).
 template <int NT>
 __device__ __forceinline__ void route_topk_block(int gtid, const float *__restrict__ lg, int n_expert, int k,
                                                  int gating, uint64_t *scratch, int *sel, float *pv) {
     if (n_expert <= 128) route_topk_pairs<NT>(gtid, lg, n_expert, k, gating, scratch, sel, pv);
+    else if (NT >= 256 && k <= 8)
+        route_topk_groups<(NT >= 256 ? NT : 256)>(gtid, lg, n_expert, k, gating, scratch, sel, pv);
     else route_topk_filter<NT>(gtid, lg, n_expert, k, gating, scratch, sel, pv);
 }
 

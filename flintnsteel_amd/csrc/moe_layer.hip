@@ -365,7 +365,7 @@ __device__ void route_all(const LayerArgs &a) {
         s_lg[grp][gt] = __hip_atomic_load(a.logits + (size_t) grp * NE + gt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid < NE) s_tabp[tid] = gload<const uint8_t *>((const uint8_t *) (a.table + tid));
     __syncthreads();
-    route_topk_filter<256>(gt, s_lg[grp < T ? grp : T - 1], NE, K, a.gating, s_tk[grp], s_sel[grp], s_pv[grp]);
+    route_topk_block<256>(gt, s_lg[grp < T ? grp : T - 1], NE, K, a.gating, s_tk[grp], s_sel[grp], s_pv[grp]);
     __syncthreads();
     FNS_MARK(0, blockIdx.x, 6);
     if (tid < T * K) {  // (token, slot): ids, weights, down pointers

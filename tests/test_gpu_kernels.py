@@ -201,7 +201,7 @@ def test_mmvq_vs_exact_input(ops, gate_up_mats):
 # ---- routing, combine, guard -------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("n_expert,k,gating", [(128, 8, 0), (256, 6, 1), (100, 8, 0), (256, 8, 0), (64, 1, 1),
-                                               (128, 16, 0)])
+                                               (128, 16, 0), (200, 8, 1), (256, 1, 0), (256, 12, 1), (129, 6, 0)])
 @pytest.mark.parametrize("n_tok", [5, 70])
 def test_route_topk_bit_exact(ops, n_expert, k, gating, n_tok):
     """Both launch forms (1024 threads per token up to 64 tokens, 256 beyond) against the oracle, with ties."""
