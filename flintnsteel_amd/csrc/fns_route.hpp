@@ -103,6 +103,16 @@ constexpr int kTopkScratch = 432;
 // to the whole workgroup on return.
 // gtid: the thread's index in its group of NT (NT = the workgroup, or one of its equal groups each ranking its own
 // token: the barriers are the workgroup's, reached by every group in step).
+// Sigmoid keys with one expert per thread (workgroups of 256 threads or more): elementwise, so the same operations
+// and bits as the wave-0 loop of the forms below.
+__device__ __forceinline__ void sigmoid_keys(int tid, const float *__restrict__ lg, int n_expert, uint64_t *s_key) {
+    if (tid < 256) {
+        const int e = tid;
+        const float p = e < n_expert ? 1.0f / (1.0f + fns_expf(-lg[e])) : 0.0f;
+        s_key[e] = e < n_expert ? ((uint64_t) __builtin_bit_cast(uint32_t, p) << 32) | (uint32_t) ~e : 0ull;
+    }
+}
+
 template <int NT>
 __device__ __forceinline__ void route_topk_filter(int gtid, const float *__restrict__ lg, int n_expert, int k,
                                                   int gating, uint64_t *scratch, int *sel, float *pv) {
@@ -112,7 +122,11 @@ __device__ __forceinline__ void route_topk_filter(int gtid, const float *__restr
     uint64_t *s_key = scratch, *s_cand = scratch + 256, *s_gm = scratch + 384, *s_t0 = scratch + 416;
     int *s_cnt = (int *) (scratch + 417);  // candidates per wave (16 at most)
     const int tid = gtid, lane = tid % kWave, wave = tid / kWave;
-    if (tid < kWave) {
+    const bool par_sig = NT >= 256 && gating != 0;
+    if (par_sig) {
+        sigmoid_keys(tid, lg, n_expert, s_key);
+        if (tid == 0) *s_t0 = 0ull;
+    } else if (tid < kWave) {
         float p[4];
         if (gating == 0) {
             float v[4], m = -__builtin_inff();
@@ -217,7 +231,9 @@ __device__ __forceinline__ void route_topk_pairs(int gtid, const float *__restri
     constexpr int P = 8;         // threads per expert
     constexpr int EPP = NT / P;  // experts per pass
     const int tid = gtid, lane = tid % kWave;
-    if (tid < kWave) {
+    if (NT >= 256 && gating != 0) {
+        sigmoid_keys(tid, lg, n_expert, s_key);
+    } else if (tid < kWave) {
         float p[4];
         if (gating == 0) {
             float v[4], m = -__builtin_inff();
@@ -289,7 +305,10 @@ __device__ __forceinline__ void route_topk_groups(int gtid, const float *__restr
     constexpr int P = 8, CPP = NT / P;
     uint64_t *s_key = scratch, *s_cand = scratch + 256;
     const int tid = gtid, lane = tid % kWave, nc = 16 * k;
-    if (tid < kWave) {
+    if (gating != 0) {
+        sigmoid_keys(tid, lg, n_expert, s_key);
+        for (int i = tid; i < nc; i += NT) s_cand[i] = 0ull;
+    } else if (tid < kWave) {  // softmax: wave 0, the fixed reduction order
         float p[4];
         if (gating == 0) {
             float v[4], m = -__builtin_inff();
