@@ -543,6 +543,8 @@ __global__ __launch_bounds__(NTH) void k_gate_up_q(const LayerArgs a) {
 
 // ---- K3: (guard) + down GEMV + combine -------------------------------------------------------------------------------
 __device__ __forceinline__ float guard_scale(float amax) {
+    // amax <= 1024 (the common case): the sequence below gives exactly 1 (log <= 0, ceil <= 0, clamped to 0, exp(0))
+    if (amax <= 1024.0f) return 1.0f;
     float e = amax * (1.0f / 1024.0f);
     e = logf(e);
     e = e * 1.4426950408889634f;

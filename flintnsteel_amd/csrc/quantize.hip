@@ -61,6 +61,8 @@ __global__ __launch_bounds__(256) void k_rms_norm_q8_1(const float *__restrict__
 
 // F16 guard scale of a row with the fp32 sequence of the reference (src/kernels.cu:544-551).
 __device__ __forceinline__ float guard_scale(float amax) {
+    // amax <= 1024 (the common case): the sequence below gives exactly 1 (log <= 0, ceil <= 0, clamped to 0, exp(0))
+    if (amax <= 1024.0f) return 1.0f;
     float e = amax * (1.0f / 1024.0f);
     e = logf(e);
     e = e * 1.4426950408889634f;
