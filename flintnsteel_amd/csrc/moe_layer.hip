@@ -155,7 +155,15 @@ __global__ __launch_bounds__(NT) void k_route_quant(const LayerArgs a) {
             if (threadIdx.x < 256) {
                 const float *xr = a.x + (size_t) t * H;
                 float s = 0.0f;
-                for (int i = threadIdx.x; i < H; i += 256) s += xr[i] * xr[i];
+                // eight values per lane per pass, every load issued first (clamped), summed in the same order
+                for (int i0 = threadIdx.x; i0 < H; i0 += 8 * 256) {
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = xr[min(i0 + 256 * u, H - 1)];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (i0 + 256 * u < H) s += v[u] * v[u];
+                }
                 s = lanes_sum<64>(s);
                 if (threadIdx.x % 64 == 0) s_nred[threadIdx.x / 64] = s;
             }
