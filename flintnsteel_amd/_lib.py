@@ -53,6 +53,7 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_moe_layer_noalloc": [_P, _P, _P, _P, _I, _P],
     "fns_hip_moe_noalloc_max_bytes": [],
     "fns_hip_moe_layer_status": [_P, _I, _P, _I, _P, _P],
+    "fns_hip_moe_layer_status_collect": [_P, _I, _P, _P, _P],
     "fns_hip_moe_set_test_hooks": [_I, _I],
     "fns_hip_moe_set_path": [_I],
     "fns_hip_moe_layer_kernels": [_P, _I, _P],
@@ -65,6 +66,7 @@ SIGNATURES: dict[str, list] = {
     "fns_hip_moe_prefill_section": [_P, _I64, _I, _P, _P],
     "fns_hip_moe_prefill": [_P, _P, _P, _P, _I64, _P, _SZ, _P],
     "fns_hip_moe_prefill_status": [_P, _I64, _P, _I, _P, _P],
+    "fns_hip_moe_prefill_status_collect": [_P, _I64, _P, _P, _P],
     "fns_hip_fill_normal": [_P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F, _F, _P],
     "fns_hip_quantize_weights": [_I, _P, _P, _I64, _I64, _P],
     "fns_hip_selftest_lanes": [_P, _P],

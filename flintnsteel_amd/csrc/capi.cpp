@@ -154,6 +154,10 @@ int fns_hip_moe_layer_status(const FnsMoeLayer *layer, int n_tok, void *workspac
     return impl::moe_layer_status(layer, n_tok, workspace, clear, status, S(stream));
 }
 
+int fns_hip_moe_layer_status_collect(const FnsMoeLayer *layer, int n_tok, void *workspace, uint32_t *dst, void *stream) {
+    return impl::moe_layer_status_collect(layer, n_tok, workspace, dst, S(stream));
+}
+
 int fns_hip_moe_set_path(int path) { return impl::moe_set_path(path); }
 
 int fns_hip_moe_layer_kernels(const FnsMoeLayer *layer, int n_tok, int *kernels) {
@@ -230,6 +234,11 @@ int fns_hip_dense_ffn_prefill(const FnsDenseFfn *ffn, const float *x, float *out
 int fns_hip_moe_prefill_status(const FnsMoeLayer *layer, int64_t n_tok, void *workspace, int clear, uint32_t *status,
                                void *stream) {
     return impl::moe_prefill_status(layer, n_tok, workspace, clear, status, S(stream));
+}
+
+int fns_hip_moe_prefill_status_collect(const FnsMoeLayer *layer, int64_t n_tok, void *workspace, uint32_t *dst,
+                                       void *stream) {
+    return impl::moe_prefill_status_collect(layer, n_tok, workspace, dst, S(stream));
 }
 
 int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x_resid, float *out, int64_t n_tok,

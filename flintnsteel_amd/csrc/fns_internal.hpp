@@ -89,9 +89,12 @@ void moe_test_hooks(int *spin_limit, int *withhold);  // the values set by moe_s
 int moe_set_path(int path);
 int moe_layer_kernels(const FnsMoeLayer *L, int n_tok, int *kernels);
 int moe_layer_status(const FnsMoeLayer *L, int n_tok, void *ws, int clear, uint32_t *status, hipStream_t st);
+int moe_layer_status_collect(const FnsMoeLayer *L, int n_tok, void *ws, uint32_t *dst, hipStream_t st);
+int status_collect(uint32_t *word, uint32_t *dst, hipStream_t st);
 int moe_prefill_workspace(const FnsMoeLayer *L, int64_t n_tok, size_t *offsets, size_t *total);
 int moe_prefill_section(const FnsMoeLayer *L, int64_t n_tok, int section, size_t *offset, size_t *bytes);
 int moe_prefill_status(const FnsMoeLayer *L, int64_t n_tok, void *ws, int clear, uint32_t *status, hipStream_t st);
+int moe_prefill_status_collect(const FnsMoeLayer *L, int64_t n_tok, void *ws, uint32_t *dst, hipStream_t st);
 int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int64_t n_tok, void *ws,
                 size_t ws_bytes, hipStream_t st);
 

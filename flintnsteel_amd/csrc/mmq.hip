@@ -1636,6 +1636,14 @@ int moe_prefill_status(const FnsMoeLayer *L, int64_t n_tok, void *ws, int clear,
     return host::OK;
 }
 
+int moe_prefill_status_collect(const FnsMoeLayer *L, int64_t n_tok, void *ws, uint32_t *dst, hipStream_t st) {
+    if (!ws || !dst) return host::set_error(host::ERR_SHAPE, "moe_prefill_status_collect: null argument");
+    size_t off;
+    FNS_TRY(moe_prefill_section(L, n_tok, 8, &off, nullptr));
+    const int64_t words = 3 * (L->n_expert + 1) + main_groups(L->n_expert, n_tok * L->k) + L->n_expert;
+    return status_collect((uint32_t *) ((uint8_t *) ws + off) + words, dst, st);
+}
+
 int moe_prefill(const FnsMoeLayer *L, const float *x, const float *x_resid, float *out, int64_t n_tok, void *ws,
                 size_t ws_bytes, hipStream_t st) {
     if (!L || !x || !out || !ws || !L->router_w || !L->table) return host::set_error(host::ERR_SHAPE, "moe_prefill: null argument");

@@ -1459,6 +1459,30 @@ int moe_layer_status(const FnsMoeLayer *L, int n_tok, void *ws, int clear, uint3
     return host::OK;
 }
 
+// One thread: ORs the status word into *dst when it is non-zero (dst untouched otherwise, so host-pinned memory is read
+// and written only after a failure) and clears the word. A kernel rather than copies and a memset, so that a HIP graph
+// can hold it.
+__global__ void k_status_collect(uint32_t *word, uint32_t *dst) {
+    const uint32_t v = *word;
+    if (v != 0) {
+        *dst = *dst | v;
+        *word = 0;
+    }
+}
+
+int status_collect(uint32_t *word, uint32_t *dst, hipStream_t st) {
+    hipLaunchKernelGGL(k_status_collect, dim3(1), dim3(1), 0, st, word, dst);
+    return host::check_launch("status collect");
+}
+
+int moe_layer_status_collect(const FnsMoeLayer *L, int n_tok, void *ws, uint32_t *dst, hipStream_t st) {
+    if (!dst) return host::set_error(host::ERR_SHAPE, "moe_layer_status_collect: null destination");
+    FNS_TRY(moe_workspace_layout(L, n_tok, nullptr, nullptr));
+    uint8_t *base = (uint8_t *) ws;
+    if (!base) FNS_TRY(scratch_of_device(st, &base));
+    return status_collect((uint32_t *) (base + kHdrStatusOff), dst, st);
+}
+
 int moe_set_path(int path) {
     if (path < 0 || path > 1) return host::set_error(host::ERR_SHAPE, "moe_set_path: path must be 0 or 1");
     g_path_override = path;

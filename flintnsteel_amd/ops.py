@@ -23,6 +23,13 @@ TYPE_NAMES = {Q8_0: "Q8_0", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_
               IQ3_S: "IQ3_S", IQ2_S: "IQ2_S", IQ4_XS: "IQ4_XS"}
 
 
+def _status_dst(t: torch.Tensor):
+    """Pointer of a status collect's destination: a device tensor or pinned host memory of at least 4 bytes."""
+    if t.numel() * t.element_size() < 4 or not (t.is_cuda or t.is_pinned()):
+        raise ValueError("status destination: a device or pinned host tensor of at least 4 bytes")
+    return ctypes.c_void_p(t.data_ptr())
+
+
 def _p(t: torch.Tensor | None):
     if t is None:
         return None
@@ -340,6 +347,11 @@ class MoeLayer:
         call("fns_hip_moe_layer_status", ctypes.byref(self.desc), n_tok, _p(ws), int(clear), ctypes.byref(st), _s())
         return st.value
 
+    def status_collect(self, ws: torch.Tensor | None, dst: torch.Tensor, n_tok: int = 1) -> None:
+        """Enqueues the graph-capturable collect (fns_hip_moe_layer_status_collect): a non-zero status word is ORed
+        into dst[0] (a uint32-sized tensor, device or pinned host) and cleared."""
+        call("fns_hip_moe_layer_status_collect", ctypes.byref(self.desc), n_tok, _p(ws), _status_dst(dst), _s())
+
     def kernels(self, n_tok: int = 1) -> int:
         """Kernels one call at n_tok tokens launches on the current device: 2 (router + fused layer) or 3 (router,
         gate/up, down)."""
@@ -410,6 +422,11 @@ class MoePrefill:
         call("fns_hip_moe_prefill_status", ctypes.byref(self.layer.desc), n_tok, _p(ws), int(clear), ctypes.byref(st),
              _s())
         return st.value
+
+    def status_collect(self, ws: torch.Tensor, dst: torch.Tensor, n_tok: int) -> None:
+        """Enqueues the graph-capturable collect (fns_hip_moe_prefill_status_collect) into dst[0]."""
+        call("fns_hip_moe_prefill_status_collect", ctypes.byref(self.layer.desc), n_tok, _p(ws), _status_dst(dst),
+             _s())
 
     def section(self, n_tok: int, index: int) -> tuple[int, int]:
         """(byte offset, bytes) of workspace section `index` (fns_hip_moe_prefill_section)."""

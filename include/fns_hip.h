@@ -176,6 +176,13 @@ size_t fns_hip_moe_noalloc_max_bytes(void);
 #define FNS_STATUS_EXCHANGE_TIMEOUT 1u
 int fns_hip_moe_layer_status(const FnsMoeLayer *layer, int n_tok, void *workspace, int clear, uint32_t *status,
                              void *stream);
+/* No counterpart in the reference: the graph-capturable form of fns_hip_moe_layer_status for engines that replay a
+ * graph per token. Enqueues one single-thread kernel on `stream` that, when the workspace's status word is non-zero,
+ * ORs it into *dst (device memory or host memory from hipHostMalloc; the caller zeroes it) and clears the word; a
+ * zero word leaves *dst untouched. Layers that share one workspace share its word, so one collect per token covers
+ * them. workspace NULL: the no-allocation array of the current device. */
+int fns_hip_moe_layer_status_collect(const FnsMoeLayer *layer, int n_tok, void *workspace, uint32_t *dst,
+                                     void *stream);
 /* Test hook, no counterpart in the reference: the decode kernel's poll limit (0: the default, 65536 polls) and a
  * number of producer arrivals to withhold (> 0: the exchange never completes, every workgroup gives up after
  * spin_limit polls) for the calls that follow; the failure path is then exercised with every kernel exiting normally.
@@ -246,6 +253,10 @@ int fns_hip_moe_prefill(const FnsMoeLayer *layer, const float *x, const float *x
  * withheld arrivals of fns_hip_moe_set_test_hooks apply to this wait too. Not graph-capturable (it synchronises). */
 int fns_hip_moe_prefill_status(const FnsMoeLayer *layer, int64_t n_tok, void *workspace, int clear, uint32_t *status,
                                void *stream);
+/* No counterpart in the reference: the graph-capturable form of fns_hip_moe_prefill_status, with the behaviour of
+ * fns_hip_moe_layer_status_collect. */
+int fns_hip_moe_prefill_status_collect(const FnsMoeLayer *layer, int64_t n_tok, void *workspace, uint32_t *dst,
+                                       void *stream);
 
 /* --- dense FFN layer (the reference model's leading dense blocks) ---
  * The dense branch of the reference's Engine::ffn_block (src/engine.cu:655-667: rms_norm_q8_1, dense_glu

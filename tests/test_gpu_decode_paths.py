@@ -160,6 +160,51 @@ def test_status_word_shared_by_shapes(ops, synth):
     assert big.status(None, 1) == 0
 
 
+def test_status_collect_in_graph(ops, synth):
+    """fns_hip_moe_layer_status_collect captured in a HIP graph after the layer, into pinned host memory: clean
+    replays leave it 0; after an eager call that times out (test hooks), a replay of a graph holding only the collect
+    ORs the bit in and clears the word, and the next replays stay clean and equal the first."""
+    from flintnsteel_amd._lib import call
+    layer = synth.build_layer(H, F, NE, K, 12, 12, SEED, layer=950)
+    x = synth.activations(1, H, SEED, layer=951)
+    ws = layer.workspace(1)
+    out = torch.empty(1, H, device="cuda")
+    dst = torch.zeros(1, dtype=torch.int32).pin_memory()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        layer(x, out=out, ws=ws)
+        layer.status_collect(ws, dst)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    ref = host(out)
+    g, gc = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer(x, out=out, ws=ws)
+        layer.status_collect(ws, dst)
+    with torch.cuda.graph(gc):
+        layer.status_collect(ws, dst)
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(dst[0]) == 0 and same_bits(host(out), ref), f"clean replay {rep}"
+    print("forced exchange timeout (withheld arrivals, poll limit 64)", flush=True)
+    call("fns_hip_moe_set_test_hooks", 64, 1)
+    try:
+        bad = host(layer(x, ws=ws))
+    finally:
+        call("fns_hip_moe_set_test_hooks", 0, 0)
+    assert np.isnan(bad).all()
+    gc.replay()
+    torch.cuda.synchronize()
+    assert int(dst[0]) == ops.STATUS_EXCHANGE_TIMEOUT and layer.status(ws, 1) == 0
+    dst.zero_()
+    for rep in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(dst[0]) == 0 and same_bits(host(out), ref), f"replay {rep} after the timeout"
+
+
 @pytest.mark.parametrize("n_tok", [1, 4])
 def test_prefetch_hint_changes_nothing(ops, synth, n_tok):
     """The read-ahead hint (FnsMoeLayer.prefetch: the next layer's router) leaves every output and intermediate

@@ -559,6 +559,18 @@ def test_moe_prefill_fused_wait_timeout_is_reported(ops):
     assert pre.status(ws, T) == 0
     again = host(pre(x, ws=ws))
     assert np.array_equal(again, good) and pre.status(ws, T) == 0
+    # the graph-capturable collect: nothing to report leaves the destination alone; after a forced timeout it ORs the
+    # bit into the destination and clears the word
+    dst = torch.full((1,), 4, dtype=torch.int32, device="cuda")
+    pre.status_collect(ws, dst, T)
+    assert int(host(dst)[0]) == 4
+    call("fns_hip_moe_set_test_hooks", 200, 1)
+    try:
+        pre(x, ws=ws)
+    finally:
+        call("fns_hip_moe_set_test_hooks", 0, 0)
+    pre.status_collect(ws, dst, T)
+    assert int(host(dst)[0]) == 4 | ops.STATUS_EXCHANGE_TIMEOUT and pre.status(ws, T) == 0
 
 
 def test_moe_prefill_fused_launch_with_shared_expert_in_place(ops):
