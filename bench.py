@@ -151,6 +151,20 @@ def time_graph(torch, g, replays: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / replays
 
 
+def replay_spread(torch, g, n: int, layers_per_replay: int) -> dict:
+    """After the timed region: n replays of the same graph, each between its own pair of HIP events, as µs per
+    layer (median, 10th and 90th percentile), so that the value's mean over a few replays can be read against the
+    distribution."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e0, e1 in evs:
+        e0.record()
+        g.replay()
+        e1.record()
+    torch.cuda.synchronize()
+    v = sorted(e0.elapsed_time(e1) * 1e3 / layers_per_replay for e0, e1 in evs)
+    return {"median": round(v[n // 2], 3), "p10": round(v[n // 10], 3), "p90": round(v[(9 * n) // 10], 3), "n": n}
+
+
 def stage_times(torch, layers, xs, outs, wss, reps: int) -> list[float]:
     """Average duration (us) of each of the three kernels, timed with HIP events on the launch stream around graph
     replays of back-to-back launches of that kernel over the L rotating layers (each reads what the previous stage
@@ -470,6 +484,9 @@ def main() -> int:
     ms_per_step = ms_replay / steps_per_graph
     us_layer = ms_per_step * 1e3 / L
     log(f"config 0: {us_layer:.2f} us/layer ({ms_per_step:.3f} ms per step of {L} layers)")
+    spread = replay_spread(torch, g, 64, steps_per_graph * L)
+    log(f"config 0, 64 replays timed one by one (us/layer): median {spread['median']} p10 {spread['p10']} "
+        f"p90 {spread['p90']}")
     st = stage_times(torch, layers, xs, outs, wss, reps=16)
     log(f"per-kernel (us): router {st[0]:.2f}  gate/up {st[1]:.2f}  down+combine {st[2]:.2f}")
     ex_bytes = K_TOP * expert_bytes(Q4_K, Q4_K)
@@ -483,7 +500,8 @@ def main() -> int:
     layer_gbs = layer_bytes(Q4_K, Q4_K) / (us_layer * 1e-6) / 1e9
     del g
 
-    extra = {"config0_layer_hbm_gbs": round(layer_gbs, 1), "config0_stage_us": [round(v, 3) for v in st]}
+    extra = {"config0_layer_hbm_gbs": round(layer_gbs, 1), "config0_stage_us": [round(v, 3) for v in st],
+             "config0_replays_us_per_layer": spread}
     if not args.no_extra:
         extra["config0_dropin_seven_calls"] = run_dropin(torch, layers)
         log(f"config0 through the seven drop-in calls: {extra['config0_dropin_seven_calls']}")
