@@ -713,7 +713,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     __shared__ const uint8_t *s_tab[256];
     __shared__ float s_dexp[16][kFusedRows];
     __shared__ float s_e[16], s_w[16], s_act[kGuRows], s_res[kFusedRows], s_sh[kFusedRows];
-    __shared__ int s_fail;
+    __shared__ int s_fail, s_big;
     constexpr int BG = Traits<TGU>::bytes, BD = Traits<TDN>::bytes;
     const int tid = threadIdx.x, wave = tid / kWave, lane64 = tid % kWave;
     const int H = a.H, F = a.F, K = a.K;
@@ -754,7 +754,7 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
         s_res[lane64] = a.x_resid ? a.x_resid[r0 + lane64] : 0.0f;
         s_sh[lane64] = a.sh ? a.sh[r0 + lane64] : 0.0f;  // the shared expert's output (an earlier kernel's)
     }
-    if (tid == 0) s_fail = 0;
+    if (tid == 0) s_fail = s_big = 0;
     dma_waves_from<kQWaves>(s_x, a.xpack, xbytes, 1);
     if (wave != 0) dma_wait();
     FNS_MARK(1, blockIdx.x, 4);
@@ -912,6 +912,14 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
     __syncthreads();
     FNS_MARK(1, blockIdx.x, 9);
     if (a.guard) {
+        // every block maximum <= 1024 (the common case): every slot's scale is exactly 1 (guard_scale), found with
+        // one compare per value and one barrier instead of a cross-lane maximum per slot; otherwise (or NaN) the
+        // per-slot maxima below
+        for (int i = tid; i < K * (F / 32); i += kQThreads)
+            if (!(s_bamax[(i / (F / 32)) * (fpad / 32) + i % (F / 32)] <= 1024.0f)) s_big = 1;
+        __syncthreads();
+    }
+    if (a.guard && s_big) {
         for (int ch = wave; ch < K; ch += kQWaves) {
             float m = 0.0f;
             // (the F / 32 blocks the producers wrote: the padding blocks of act are zeros and never stored here)
