@@ -80,6 +80,7 @@ struct LayerArgs {
     int *chan;            // n_tok > 1: [kMaxCh][kChanInts] channel table, then n_distinct, then the router arrival count
     int64_t xq_row_bytes;
     int fused;            // the shape fits the fused kernel (n_tok = 1)
+    int dn_defer;         // fused kernel: 10-ns ticks a workgroup without gate/up rows defers its down-row fetch
     int spin_limit;       // fused kernel: polls of the release flag before a workgroup gives up
     int withhold;         // test hook: arrivals each producer group withholds (> 0: the release never comes)
     const float *sh;      // [T][H] shared-expert output added in the combine, or null
@@ -672,6 +673,10 @@ __global__ __launch_bounds__(kQThreads) void k_down_q(const LayerArgs a) {
 // zeroes the counters; a kernel boundary orders that before this kernel. Per-(row, slot) arithmetic is that of the
 // two-kernel path, so results are the same bit for bit.
 constexpr int kFusedRows = 8;
+#ifndef FNS_DEFER_BYTES_PER_TICK
+#define FNS_DEFER_BYTES_PER_TICK 50000
+#endif
+constexpr int64_t kDeferBytesPerTick = FNS_DEFER_BYTES_PER_TICK;  // 5 TB/s in bytes per 10-ns tick of s_memrealtime
 constexpr int kSpinLimit = 1 << 16;
 constexpr uint32_t kStatusTimeout = 1u;  // FNS_STATUS_EXCHANGE_TIMEOUT
 constexpr int kCpolDevice = 16;  // cache-policy bits of a device-scope (sc1) load: not served from a stale L2 line
@@ -796,6 +801,11 @@ __global__ __launch_bounds__(kQThreads) void k_layer_fused(const LayerArgs a) {
             dma_blocks<TGU>(s_gu, wa, 2 * wave * nbg, (2 * wave + 2) * nbg);
             dma_blocks<TGU>(s_gu + gu_region, wb, 2 * wave * nbg, (2 * wave + 2) * nbg);
         } else {
+            // Defer the down rows by about the time the layer's gate/up bytes take at 5 TB/s: those bytes are on
+            // the critical path (the exchange waits for them) and otherwise share the HBM with these from the start.
+            // Timing only; the down rows land long before the exchange releases.
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            while (__builtin_amdgcn_s_memrealtime() - t0 < (uint64_t) a.dn_defer) __builtin_amdgcn_s_sleep(8);
             dma_down();
         }
     }
@@ -1104,6 +1114,9 @@ bool use_fused(const FnsMoeLayer *L, const LayerArgs &a) {
 int launch_fused(const FnsMoeLayer *L, const LayerArgs &a, hipStream_t st) {
     const size_t lds = fused_lds(a.H, a.F, a.K, stage_bytes_of(L->gu_type), stage_bytes_of(L->down_type), a.shd ? a.Fs : 0);
     LayerArgs arg = a;
+    // non-producer workgroups defer their down rows by the gate/up bytes' time at 5 TB/s (50,000 bytes per 10 ns)
+    const int64_t gu_bytes = ((int64_t) a.K * a.F + (a.shd ? a.Fs : 0)) * 2 * (a.H / 256) * block_bytes(L->gu_type);
+    arg.dn_defer = (int) std::min<int64_t>(gu_bytes / kDeferBytesPerTick, 2000);
     void *args[] = {&arg};
     const hipError_t e = hipLaunchKernel(fused_kernel(L->gu_type, L->down_type, a.shd != nullptr),
                                          dim3((unsigned) (a.H / kFusedRows)),
